@@ -1,0 +1,331 @@
+"""Python host interface of libcdna4_attn.so, the MI355X (gfx950) attention hot path.
+
+Mirrors the reference's host API for the path (cdna3-prims/include/cdna3/attention.hpp,
+cdna3-prims/include/cdna3/runtime/forward.hpp) over the library's C ABI (include/cdna4_attn.h):
+
+    prefill(Q, K, V, O, PrefillCfg(...))          cdna3::attn::prefill   (attention.hpp:86)
+    decode(q, K, V, o, DecodeCfg(...))            cdna3::attn::decode    (attention.hpp:117)
+    decode_dme(q, K, V, o, DecodeDmeCfg(...))     cdna3::attn::decode_dme (attention.hpp:152)
+    rmsnorm_f32, layernorm_f32, rope_f16, rope_table_f32    runtime entry points
+    reduce, scan_inclusive                        device-wide wave::dpp reductions / scans
+    flash_attn(q, k, v), flash_attn_decode(q, k_cache, v_cache)
+                                                  the reference's torch ops (fa_torch_op.hip:36,
+                                                  fa_decode_op.hip:26), as plain functions
+
+Tensors are torch tensors on the current HIP device; PyTorch only provides device memory and
+the stream. Every call enqueues on torch's current stream (or the `stream` argument) and does
+not synchronise. A non-zero library return code raises RuntimeError, as the reference's
+launchers return hipErrorInvalidValue and its torch ops raise through TORCH_CHECK. There is no
+fallback: if the library is missing, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from typing import Optional
+
+import torch
+
+__all__ = [
+    "F32", "F16", "BF16", "F64", "I32", "I64", "SUM", "MAX", "MIN",
+    "PrefillCfg", "DecodeCfg", "DecodeDmeCfg", "library_path", "lib", "abi_version", "error_string",
+    "prefill", "decode", "decode_dme", "decode_workspace_size", "reduce", "reduce_workspace_size",
+    "scan_inclusive", "scan_workspace_size", "rmsnorm_f32", "layernorm_f32", "rope_f16",
+    "rope_table_f32", "flash_attn", "flash_attn_decode", "CDNA4Error",
+]
+
+# Element types and operators (include/cdna4_attn.h).
+F32, F16, BF16, F64, I32, I64 = 0, 1, 2, 3, 4, 5
+SUM, MAX, MIN = 0, 1, 2
+_OPS = {"sum": SUM, "max": MAX, "min": MIN, SUM: SUM, MAX: MAX, MIN: MIN}
+_TORCH_DTYPES = {
+    torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16,
+    torch.float64: F64, torch.int32: I32, torch.int64: I64,
+}
+
+
+class CDNA4Error(RuntimeError):
+    """A non-zero return code of libcdna4_attn.so; `.code` is the hipError_t value."""
+
+    def __init__(self, what: str, code: int):
+        super().__init__(f"{what}: {error_string(code)} (code {code})")
+        self.code = code
+
+
+class PrefillCfg(ctypes.Structure):
+    """cdna3_prefill_cfg: field for field the reference's PrefillCfg (attention.hpp:63-71)."""
+    _fields_ = [("D", ctypes.c_int), ("seqQ", ctypes.c_int), ("seqK", ctypes.c_int),
+                ("nQHeads", ctypes.c_int), ("nKVHeads", ctypes.c_int), ("batch", ctypes.c_int),
+                ("causal", ctypes.c_int)]
+
+
+class DecodeCfg(ctypes.Structure):
+    """cdna3_decode_cfg: the reference's DecodeCfg {D, N, nQHeads, nKVHeads} (attention.hpp:73-78)
+    plus batch (default 1) and stride_kv (0 = packed)."""
+    _fields_ = [("D", ctypes.c_int), ("N", ctypes.c_int), ("nQHeads", ctypes.c_int),
+                ("nKVHeads", ctypes.c_int), ("batch", ctypes.c_int), ("stride_kv", ctypes.c_int)]
+
+    def __init__(self, D=0, N=0, nQHeads=0, nKVHeads=0, batch=1, stride_kv=0):
+        super().__init__(D, N, nQHeads, nKVHeads, batch, stride_kv)
+
+
+def DecodeDmeCfg(D: int, N: int, nQHeads: int, nKVHeads: int, stride_kv: int, batch: int = 1) -> DecodeCfg:
+    """The reference's DecodeDmeCfg {D, N, nQHeads, nKVHeads, stride_kv}
+    (detail/fa_decode_dme_kernel.hpp:45-48) as a DecodeCfg."""
+    return DecodeCfg(D, N, nQHeads, nKVHeads, batch, stride_kv)
+
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def library_path() -> str:
+    return os.path.join(_HERE, "libcdna4_attn.so")
+
+
+def _declare(l: ctypes.CDLL) -> None:
+    c_int, c_size, vp, c_float = ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_float
+    sig = {
+        "cdna3_abi_version": (c_int, []),
+        "cdna3_error_string": (ctypes.c_char_p, [c_int]),
+        "cdna3_attn_prefill": (c_int, [vp, vp, vp, vp, ctypes.POINTER(PrefillCfg), c_int, vp]),
+        "cdna3_attn_decode_workspace_size": (c_size, [ctypes.POINTER(DecodeCfg)]),
+        "cdna3_attn_decode": (c_int, [vp, vp, vp, vp, ctypes.POINTER(DecodeCfg), c_int, vp, c_size, vp]),
+        "cdna3_reduce_workspace_size": (c_size, [c_size, c_int]),
+        "cdna3_reduce": (c_int, [c_int, c_int, vp, c_size, vp, vp, c_size, vp]),
+        "cdna3_scan_workspace_size": (c_size, [c_size, c_int]),
+        "cdna3_scan_inclusive": (c_int, [c_int, c_int, vp, c_size, vp, vp, c_size, vp]),
+        "cdna3_rmsnorm_f32": (c_int, [vp, vp, vp, c_int, c_int, c_float, vp]),
+        "cdna3_layernorm_f32": (c_int, [vp, vp, vp, vp, c_int, c_int, c_float, vp]),
+        "cdna3_rope_f16": (c_int, [vp, vp, vp, c_int, c_int, c_int, vp]),
+        "cdna3_rope_table_f32": (c_int, [vp, vp, c_int, c_int, c_int, c_float, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(l, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library. Raises if it has not been built (no fallback path exists)."""
+    global _LIB
+    if _LIB is None:
+        path = library_path()
+        if not os.path.exists(path):
+            raise RuntimeError(f"libcdna4_attn.so not built ({path}); run __graft_entry__.build()")
+        l = ctypes.CDLL(path)
+        _declare(l)
+        _LIB = l
+    return _LIB
+
+
+def header_symbols() -> list:
+    """Every function name declared in include/cdna4_attn.h."""
+    hdr = os.path.join(_HERE, "..", "..", "include", "cdna4_attn.h")
+    text = open(hdr).read()
+    return sorted(set(re.findall(r"\b(cdna3_[a-z0-9_]+)\s*\(", text)))
+
+
+def abi_version() -> int:
+    return lib().cdna3_abi_version()
+
+
+def error_string(code: int) -> str:
+    return lib().cdna3_error_string(code).decode()
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise CDNA4Error(what, rc)
+
+
+def _stream(stream) -> ctypes.c_void_p:
+    if stream is None:
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, torch.cuda.Stream):
+        return ctypes.c_void_p(stream.cuda_stream)
+    return ctypes.c_void_p(int(stream))
+
+
+def _ptr(t: Optional[torch.Tensor]) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _dev(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not t.is_cuda:
+            raise ValueError("tensors must be on the GPU")
+        if not t.is_contiguous():
+            raise ValueError("tensors must be contiguous")
+
+
+def _dtype(t: torch.Tensor) -> int:
+    try:
+        return _TORCH_DTYPES[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}") from None
+
+
+# ---- attention ----------------------------------------------------------------------------
+
+def prefill(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, O: torch.Tensor, cfg: PrefillCfg,
+            stream=None) -> None:
+    """cdna3::attn::prefill: Q, O [batch][nQH][seqQ][D]; K, V [batch][nKVH][seqK][D];
+    fp16, bf16 or fp32 (all four alike)."""
+    _dev(Q, K, V, O)
+    dt = _dtype(Q)
+    if not (K.dtype == V.dtype == O.dtype == Q.dtype):
+        raise ValueError("Q, K, V, O must share one dtype")
+    nq = cfg.batch * cfg.nQHeads * cfg.seqQ * cfg.D
+    nk = cfg.batch * cfg.nKVHeads * cfg.seqK * cfg.D
+    if Q.numel() < nq or O.numel() < nq or K.numel() < nk or V.numel() < nk:
+        raise ValueError("tensor smaller than the configuration")
+    _check(lib().cdna3_attn_prefill(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), ctypes.byref(cfg), dt,
+                                    _stream(stream)), "cdna3_attn_prefill")
+
+
+def decode_workspace_size(cfg: DecodeCfg) -> int:
+    return int(lib().cdna3_attn_decode_workspace_size(ctypes.byref(cfg)))
+
+
+def decode(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, o: torch.Tensor, cfg: DecodeCfg,
+           workspace: Optional[torch.Tensor] = None, stream=None) -> None:
+    """cdna3::attn::decode with batch: q, o [batch][nQH][D]; K, V [batch][nKVH][stride][D];
+    fp16 or bf16. `workspace` (uint8, >= decode_workspace_size(cfg) bytes) holds split-K
+    partials; without one the library uses its own per-device buffer."""
+    _dev(q, K, V, o)
+    dt = _dtype(q)
+    if not (K.dtype == V.dtype == o.dtype == q.dtype):
+        raise ValueError("q, K, V, o must share one dtype")
+    stride = cfg.stride_kv or cfg.N
+    if q.numel() < cfg.batch * cfg.nQHeads * cfg.D or o.numel() < cfg.batch * cfg.nQHeads * cfg.D:
+        raise ValueError("q/o smaller than the configuration")
+    if min(K.numel(), V.numel()) < cfg.batch * cfg.nKVHeads * stride * cfg.D:
+        raise ValueError("K/V smaller than the configuration")
+    ws_bytes = 0
+    if workspace is not None:
+        _dev(workspace)
+        ws_bytes = workspace.numel() * workspace.element_size()
+    _check(lib().cdna3_attn_decode(_ptr(q), _ptr(K), _ptr(V), _ptr(o), ctypes.byref(cfg), dt, _ptr(workspace),
+                                   ws_bytes, _stream(stream)), "cdna3_attn_decode")
+
+
+def decode_dme(q, K, V, o, cfg: DecodeCfg, workspace=None, stream=None) -> None:
+    """cdna3::attn::decode_dme: decode reading a strided [nKVH][stride_kv][D] cache in place."""
+    decode(q, K, V, o, cfg, workspace, stream)
+
+
+# ---- device-wide reduce / scan ----------------------------------------------------------
+
+def reduce_workspace_size(n: int, dtype: int) -> int:
+    return int(lib().cdna3_reduce_workspace_size(n, dtype))
+
+
+def scan_workspace_size(n: int, dtype: int) -> int:
+    return int(lib().cdna3_scan_workspace_size(n, dtype))
+
+
+def _acc_dtype(t: torch.Tensor) -> torch.dtype:
+    return torch.float32 if t.dtype in (torch.float16, torch.bfloat16) else t.dtype
+
+
+def reduce(x: torch.Tensor, op="sum", out: Optional[torch.Tensor] = None,
+           workspace: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Reduce a whole contiguous array with wave::dpp semantics; fp16/bf16 accumulate in fp32."""
+    _dev(x)
+    dt, o = _dtype(x), _OPS[op]
+    n = x.numel()
+    if out is None:
+        out = torch.empty(1, dtype=_acc_dtype(x), device=x.device)
+    if workspace is None:
+        workspace = torch.empty(reduce_workspace_size(n, dt), dtype=torch.uint8, device=x.device)
+    _check(lib().cdna3_reduce(o, dt, _ptr(x), n, _ptr(out), _ptr(workspace), workspace.numel(), _stream(stream)),
+           "cdna3_reduce")
+    return out
+
+
+def scan_inclusive(x: torch.Tensor, op="sum", out: Optional[torch.Tensor] = None,
+                   workspace: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Inclusive scan of a whole contiguous array; fp16/bf16 accumulate (and return) fp32."""
+    _dev(x)
+    dt, o = _dtype(x), _OPS[op]
+    n = x.numel()
+    if out is None:
+        out = torch.empty(n, dtype=_acc_dtype(x), device=x.device)
+    if workspace is None:
+        workspace = torch.empty(max(1, scan_workspace_size(n, dt)), dtype=torch.uint8, device=x.device)
+    _check(lib().cdna3_scan_inclusive(o, dt, _ptr(x), n, _ptr(out), _ptr(workspace), workspace.numel(),
+                                      _stream(stream)), "cdna3_scan_inclusive")
+    return out
+
+
+# ---- runtime norms and RoPE --------------------------------------------------------------
+
+def rmsnorm_f32(X: torch.Tensor, W: torch.Tensor, eps: float = 1e-6, out: Optional[torch.Tensor] = None,
+                stream=None) -> torch.Tensor:
+    """rmsnorm_f32_kernel: X fp32 [M][H], W fp16 [H] -> Y fp32 [M][H]."""
+    _dev(X, W)
+    if X.dtype != torch.float32 or W.dtype != torch.float16:
+        raise ValueError("X must be fp32 and W fp16")
+    M, H = X.shape
+    out = torch.empty_like(X) if out is None else out
+    _check(lib().cdna3_rmsnorm_f32(_ptr(X), _ptr(W), _ptr(out), M, H, eps, _stream(stream)), "cdna3_rmsnorm_f32")
+    return out
+
+
+def layernorm_f32(X: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float = 1e-5,
+                  out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Two-pass layernorm: X, Y fp32 [M][H]; gamma, beta fp32 [H]."""
+    _dev(X, gamma, beta)
+    M, H = X.shape
+    out = torch.empty_like(X) if out is None else out
+    _check(lib().cdna3_layernorm_f32(_ptr(X), _ptr(gamma), _ptr(beta), _ptr(out), M, H, eps, _stream(stream)),
+           "cdna3_layernorm_f32")
+    return out
+
+
+def rope_f16(T: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, seq: int, heads: int, D: int,
+             stream=None) -> None:
+    """rope_kernel, in place on T fp16 [seq][heads*D] with cos/sin fp32 [seq][D]."""
+    _dev(T, cos, sin)
+    _check(lib().cdna3_rope_f16(_ptr(T), _ptr(cos), _ptr(sin), seq, heads, D, _stream(stream)), "cdna3_rope_f16")
+
+
+def rope_table_f32(pos0: int, T: int, D: int, theta: float = 10000.0, device=None, stream=None):
+    """Session::fill_rope on the device: cos, sin fp32 [T][D] for positions pos0 .. pos0+T-1."""
+    device = device or torch.device("cuda", torch.cuda.current_device())
+    cos = torch.empty((T, D), dtype=torch.float32, device=device)
+    sin = torch.empty((T, D), dtype=torch.float32, device=device)
+    _check(lib().cdna3_rope_table_f32(_ptr(cos), _ptr(sin), pos0, T, D, theta, _stream(stream)),
+           "cdna3_rope_table_f32")
+    return cos, sin
+
+
+# ---- the reference's torch-op contracts, as plain functions ------------------------------
+
+def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """amdinstinct.flash_attn (fa_torch_op.hip:36-59): causal GQA prefill on head-major
+    q [nQH][seq][D], k, v [nKVH][seq][D] (fp16; bf16 also accepted) -> o [nQH][seq][D]."""
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("q, k, v must be [heads, seq, D]")
+    nqh, seq, D = q.shape
+    nkvh = k.shape[0]
+    if k.shape[1] != seq or v.shape[1] != seq or k.shape[2] != D or v.shape[2] != D:
+        raise ValueError("k/v shape must match q")
+    o = torch.empty_like(q)
+    prefill(q, k, v, o, PrefillCfg(D, seq, seq, nqh, nkvh, 1, 1))
+    return o
+
+
+def flash_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor) -> torch.Tensor:
+    """amdinstinct.flash_attn_decode (fa_decode_op.hip:26-50): q [nQH][D], caches [nKVH][N][D]."""
+    if q.dim() != 2 or k_cache.dim() != 3 or v_cache.dim() != 3:
+        raise ValueError("q must be [nQH, D] and caches [nKVH, N, D]")
+    nqh, D = q.shape
+    nkvh, N, _ = k_cache.shape
+    if k_cache.shape[2] != D or tuple(v_cache.shape) != tuple(k_cache.shape):
+        raise ValueError("cache shape mismatch")
+    o = torch.empty((nqh, D), dtype=q.dtype, device=q.device)
+    decode(q, k_cache, v_cache, o, DecodeCfg(D, N, nqh, nkvh, 1, 0))
+    return o

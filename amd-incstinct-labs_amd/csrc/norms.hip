@@ -1,0 +1,244 @@
+// Runtime norm and RoPE entry points for gfx950: RMSNorm and two-pass LayerNorm with one
+// wave per row (DPP/permlane butterfly reductions, zero LDS), rotate-half RoPE with one
+// thread per (d, d + D/2) pair, and the RoPE cos/sin table built on the device.
+//
+// Reference behaviour restated:
+//   rmsnorm_f32_kernel  cdna3-prims/include/cdna3/runtime/forward.hpp:34-56
+//   layernorm_kernel    research/wave-primitives/benchmarks/bench_layernorm.hip:51-114
+//   rope_kernel         cdna3-prims/include/cdna3/runtime/forward.hpp:135-148
+//   Session::fill_rope  cdna3-prims/include/cdna3/runtime/session.hpp:120-135
+#include "common.hpp"
+#include "wave_primitives/detail/xlane.hpp"
+
+namespace cdna4 {
+namespace {
+
+using wave::xlane::allreduce;
+using wave::xlane::Sum;
+
+constexpr int kNormWaves = 4;   // rows per 256-thread block, one wave per row
+
+// Row cached in registers: NV float4 per lane covers H <= 256 * NV (H % 4 == 0).
+template <int NV>
+__device__ __forceinline__ void load_row(const float* __restrict__ x, int H, unsigned lane, float4 (&v)[NV]) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int c = (k * 64 + (int)lane) * 4;
+        v[k] = (c < H) ? *(const float4*)(x + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_vec(const float* __restrict__ X, const uint16_t* __restrict__ W,
+                                                   float* __restrict__ Y, int M, int H, float eps) {
+    const unsigned lane = threadIdx.x & 63u;
+    const int row = blockIdx.x * kNormWaves + (int)(threadIdx.x >> 6);
+    if (row >= M) return;
+    const float* x = X + (size_t)row * H;
+    float* y = Y + (size_t)row * H;
+    float4 v[NV];
+    load_row<NV>(x, H, lane, v);
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) ss += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
+    ss = allreduce(ss, Sum{});
+    const float inv = rsqrtf(ss / (float)H + eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int c = (k * 64 + (int)lane) * 4;
+        if (c < H) {
+            const uint2 wb = *(const uint2*)(W + c);
+            float4 o;
+            o.x = v[k].x * inv * f16_bits_to_f32(wb.x & 0xffffu);
+            o.y = v[k].y * inv * f16_bits_to_f32(wb.x >> 16);
+            o.z = v[k].z * inv * f16_bits_to_f32(wb.y & 0xffffu);
+            o.w = v[k].w * inv * f16_bits_to_f32(wb.y >> 16);
+            *(float4*)(y + c) = o;
+        }
+    }
+}
+
+// Any H and alignment: two passes over the row (the second pass hits the cache).
+__global__ __launch_bounds__(256) void rmsnorm_any(const float* __restrict__ X, const uint16_t* __restrict__ W,
+                                                   float* __restrict__ Y, int M, int H, float eps) {
+    const unsigned lane = threadIdx.x & 63u;
+    const int row = blockIdx.x * kNormWaves + (int)(threadIdx.x >> 6);
+    if (row >= M) return;
+    const float* x = X + (size_t)row * H;
+    float* y = Y + (size_t)row * H;
+    float ss = 0.f;
+    for (int c = lane; c < H; c += 64) ss += x[c] * x[c];
+    ss = allreduce(ss, Sum{});
+    const float inv = rsqrtf(ss / (float)H + eps);
+    for (int c = lane; c < H; c += 64) y[c] = x[c] * inv * f16_bits_to_f32(W[c]);
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void layernorm_vec(const float* __restrict__ X, const float* __restrict__ G,
+                                                     const float* __restrict__ B, float* __restrict__ Y, int M,
+                                                     int H, float eps) {
+    const unsigned lane = threadIdx.x & 63u;
+    const int row = blockIdx.x * kNormWaves + (int)(threadIdx.x >> 6);
+    if (row >= M) return;
+    const float* x = X + (size_t)row * H;
+    float* y = Y + (size_t)row * H;
+    float4 v[NV];
+    load_row<NV>(x, H, lane, v);
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+    const float mean = allreduce(s, Sum{}) / (float)H;
+    // Second pass over the register-cached deviations (padding lanes contribute 0).
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int c = (k * 64 + (int)lane) * 4;
+        if (c < H) {
+            const float a = v[k].x - mean, b = v[k].y - mean, d = v[k].z - mean, e = v[k].w - mean;
+            q += (a * a + b * b) + (d * d + e * e);
+        }
+    }
+    const float inv = rsqrtf(allreduce(q, Sum{}) / (float)H + eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int c = (k * 64 + (int)lane) * 4;
+        if (c < H) {
+            const float4 g = *(const float4*)(G + c), bb = *(const float4*)(B + c);
+            float4 o;
+            o.x = (v[k].x - mean) * inv * g.x + bb.x;
+            o.y = (v[k].y - mean) * inv * g.y + bb.y;
+            o.z = (v[k].z - mean) * inv * g.z + bb.z;
+            o.w = (v[k].w - mean) * inv * g.w + bb.w;
+            *(float4*)(y + c) = o;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void layernorm_any(const float* __restrict__ X, const float* __restrict__ G,
+                                                     const float* __restrict__ B, float* __restrict__ Y, int M,
+                                                     int H, float eps) {
+    const unsigned lane = threadIdx.x & 63u;
+    const int row = blockIdx.x * kNormWaves + (int)(threadIdx.x >> 6);
+    if (row >= M) return;
+    const float* x = X + (size_t)row * H;
+    float* y = Y + (size_t)row * H;
+    float s = 0.f;
+    for (int c = lane; c < H; c += 64) s += x[c];
+    const float mean = allreduce(s, Sum{}) / (float)H;
+    float q = 0.f;
+    for (int c = lane; c < H; c += 64) { const float d = x[c] - mean; q += d * d; }
+    const float inv = rsqrtf(allreduce(q, Sum{}) / (float)H + eps);
+    for (int c = lane; c < H; c += 64) y[c] = (x[c] - mean) * inv * G[c] + B[c];
+}
+
+// One thread per (row, head, d) with d < D/2: reads t[d] and t[d + D/2] once, writes both.
+__global__ __launch_bounds__(256) void rope_pairs(uint16_t* __restrict__ T, const float* __restrict__ cosv,
+                                                  const float* __restrict__ sinv, int seq, int heads, int D) {
+    const int half = D >> 1;
+    const size_t total = (size_t)seq * heads * half;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    const int d = (int)(idx % half);
+    const size_t sh = idx / half;               // s * heads + h
+    const int s = (int)(sh / heads);
+    uint16_t* t = T + sh * D;
+    const float* c = cosv + (size_t)s * D;
+    const float* sn = sinv + (size_t)s * D;
+    const float a = f16_bits_to_f32(t[d]);
+    const float b = f16_bits_to_f32(t[d + half]);
+    const float lo = a * c[d] + (-b) * sn[d];
+    const float hi = b * c[d + half] + a * sn[d + half];
+    t[d] = (uint16_t)f32_to_f16_bits(lo);
+    t[d + half] = (uint16_t)f32_to_f16_bits(hi);
+}
+
+__global__ __launch_bounds__(256) void rope_table(float* __restrict__ cosv, float* __restrict__ sinv, int pos0,
+                                                  int T, int D, float theta) {
+    const int half = D >> 1;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)T * half) return;
+    const int d = (int)(idx % half);
+    const int s = (int)(idx / half);
+    const float freq = 1.f / powf(theta, (2.f * (float)d) / (float)D);
+    const float ang = (float)(pos0 + s) * freq;
+    const float cv = cosf(ang), sv = sinf(ang);
+    cosv[(size_t)s * D + d] = cv;
+    cosv[(size_t)s * D + d + half] = cv;
+    sinv[(size_t)s * D + d] = sv;
+    sinv[(size_t)s * D + d + half] = sv;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <class Launch>
+int dispatch_nv(int H, Launch&& launch) {
+    if (H <= 256) return launch(std::integral_constant<int, 1>{});
+    if (H <= 512) return launch(std::integral_constant<int, 2>{});
+    if (H <= 1024) return launch(std::integral_constant<int, 4>{});
+    if (H <= 2048) return launch(std::integral_constant<int, 8>{});
+    return launch(std::integral_constant<int, 16>{});
+}
+
+}  // namespace
+}  // namespace cdna4
+
+using namespace cdna4;
+
+extern "C" int cdna3_rmsnorm_f32(const float* X, const void* W, float* Y, int M, int H, float eps,
+                                 cdna4_stream_t stream) {
+    if (M < 0 || H <= 0 || (M > 0 && (!X || !W || !Y))) return CDNA4_ERR_INVALID_VALUE;
+    if (M == 0) return 0;
+    if (int e = check_device()) return e;
+    hipStream_t s = (hipStream_t)stream;
+    const unsigned grid = ceil_div((size_t)M, kNormWaves);
+    const uint16_t* w = (const uint16_t*)W;
+    const bool vec = (H % 4 == 0) && H <= 4096 && aligned16(X) && aligned16(Y) && (((uintptr_t)W & 7u) == 0);
+    if (!vec) {
+        rmsnorm_any<<<grid, 256, 0, s>>>(X, w, Y, M, H, eps);
+        return launch_status();
+    }
+    return dispatch_nv(H, [&](auto nv) {
+        rmsnorm_vec<decltype(nv)::value><<<grid, 256, 0, s>>>(X, w, Y, M, H, eps);
+        return launch_status();
+    });
+}
+
+extern "C" int cdna3_layernorm_f32(const float* X, const float* gamma, const float* beta, float* Y, int M, int H,
+                                   float eps, cdna4_stream_t stream) {
+    if (M < 0 || H <= 0 || (M > 0 && (!X || !gamma || !beta || !Y))) return CDNA4_ERR_INVALID_VALUE;
+    if (M == 0) return 0;
+    if (int e = check_device()) return e;
+    hipStream_t s = (hipStream_t)stream;
+    const unsigned grid = ceil_div((size_t)M, kNormWaves);
+    const bool vec = (H % 4 == 0) && H <= 4096 && aligned16(X) && aligned16(Y) && aligned16(gamma) && aligned16(beta);
+    if (!vec) {
+        layernorm_any<<<grid, 256, 0, s>>>(X, gamma, beta, Y, M, H, eps);
+        return launch_status();
+    }
+    return dispatch_nv(H, [&](auto nv) {
+        layernorm_vec<decltype(nv)::value><<<grid, 256, 0, s>>>(X, gamma, beta, Y, M, H, eps);
+        return launch_status();
+    });
+}
+
+extern "C" int cdna3_rope_f16(void* T, const float* cos_tab, const float* sin_tab, int seq, int heads, int D,
+                              cdna4_stream_t stream) {
+    if (seq < 0 || heads <= 0 || D <= 0 || (D & 1)) return CDNA4_ERR_INVALID_VALUE;
+    if (seq == 0) return 0;
+    if (!T || !cos_tab || !sin_tab) return CDNA4_ERR_INVALID_VALUE;
+    if (int e = check_device()) return e;
+    const size_t total = (size_t)seq * heads * (D / 2);
+    rope_pairs<<<ceil_div(total, 256), 256, 0, (hipStream_t)stream>>>((uint16_t*)T, cos_tab, sin_tab, seq, heads, D);
+    return launch_status();
+}
+
+extern "C" int cdna3_rope_table_f32(float* cos_tab, float* sin_tab, int pos0, int T, int D, float theta,
+                                    cdna4_stream_t stream) {
+    if (T < 0 || D <= 0 || (D & 1) || pos0 < 0 || !(theta > 0.f)) return CDNA4_ERR_INVALID_VALUE;
+    if (T == 0) return 0;
+    if (!cos_tab || !sin_tab) return CDNA4_ERR_INVALID_VALUE;
+    if (int e = check_device()) return e;
+    const size_t total = (size_t)T * (D / 2);
+    rope_table<<<ceil_div(total, 256), 256, 0, (hipStream_t)stream>>>(cos_tab, sin_tab, pos0, T, D, theta);
+    return launch_status();
+}

@@ -1,0 +1,422 @@
+// FlashAttention-2 prefill for gfx950 (MI355X).
+//
+// Reference behaviour restated (cdna3-prims/include/cdna3/detail/fa_prefill_kernel.hpp:
+// 43-177, launched by cdna3-prims/include/cdna3/attention.hpp:86-109): O = softmax(Q K^T /
+// sqrt(D)) V per (batch, query head), query head h reads kv head h / (nQH / nKVH), causal
+// mask "key > query -> excluded", fp32 softmax and accumulation, O / l with an l > 0 guard.
+//
+// MI355X design of the f16 / bf16 kernel (fa_mfma):
+//   * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_{f16,bf16}. In that orientation
+//     the S^T accumulator of a lane holds one query column (q = lane % 16) and 4 keys, so
+//     the softmax state (m, l) and the O^T accumulator of a query live in the same lanes:
+//     the running rescale is a per-lane multiply, and P goes from the S^T accumulator
+//     straight into the B operand of the P.V MFMA without any data movement, because the
+//     rows of each K operand tile are permuted (key = 8*(m/4) + 4*t + m%4 for A-row m of
+//     sub-tile t) so that the 8 keys a lane holds are the 8 consecutive keys its B operand
+//     needs.
+//   * The row max over a query's 64 keys spans the lane's own registers and the three
+//     other lanes that hold the same query (lanes q, q+16, q+32, q+48): two permlane swaps.
+//   * K and V tiles go HBM -> LDS with global_load_lds_dwordx4 (asynchronous, no VGPRs),
+//     double-buffered so tile i+1 streams in while tile i is on the matrix cores. The
+//     16-byte chunks of a key row are XOR-swizzled so the K operand reads (ds_read_b128,
+//     16 rows per lane group) and the V^T operand reads (ds_read_b64_tr_b16, 4 rows x 32
+//     bytes per lane group) are both free of bank conflicts.
+//   * Q stays in VGPRs as B operands for the whole kernel; softmax is base-2 with a
+//     log2(e)-prescaled scale; causal blocks are issued heaviest first, with all q blocks
+//     of a (batch, head) on the same XCD so its K/V stay in that XCD's L2.
+// The fp32 kernel (fa_f32) is a plain VALU kernel for the fp32 arm of the reference
+// configuration (fp32 in and out, accuracy 1e-4).
+#include "common.hpp"
+#include "wave_primitives/detail/xlane.hpp"
+#include <math.h>
+
+namespace cdna4 {
+namespace {
+
+using wave::xlane::allreduce;
+using wave::xlane::cross_row_allreduce;
+using wave::xlane::Max;
+using wave::xlane::Sum;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+#define LDS_AS __attribute__((address_space(3)))
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kBc = 64;       // keys per K/V tile
+constexpr int kWaves = 4;     // waves per workgroup
+
+template <bool kBf16>
+__device__ __forceinline__ f32x4 mfma(const u32x4& a, const u32x4& b, const f32x4& c) {
+    if constexpr (kBf16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+template <bool kBf16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (kBf16) return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+    else return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+}
+
+// XOR swizzle of the 16-byte chunks of key row r inside a K/V tile (see file comment).
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+    if constexpr (D == 128)
+        return ((r >> 3) & 1) | ((r & 1) << 1) | (((r >> 1) & 1) << 2) | (((r >> 4) & 1) << 3);
+    else
+        return ((r >> 3) & 1) | (((r >> 1) & 1) << 1) | (((r >> 4) & 1) << 2);
+}
+
+struct PrefillArgs {
+    const uint16_t* Q; const uint16_t* K; const uint16_t* V; uint16_t* O;
+    int seqQ, seqK, nQH, nKVH, batch, causal;
+    int nqb;          // q blocks per (batch, head)
+    int xcd_map;      // 1: (batch, head) -> XCD-aware block order
+    float sc;         // log2(e) / sqrt(D)
+};
+
+// Issue the asynchronous copy of keys [k0, k0 + kBc) of one head into an LDS tile.
+template <int D>
+__device__ __forceinline__ void load_tile(const uint16_t* __restrict__ head, int k0, int seqK,
+                                          uint16_t* tile, int wave, int lane) {
+    constexpr int CPR = D / 8;                       // 16-byte chunks per key row
+    constexpr int NI = kBc * CPR / (64 * kWaves);    // wave instructions per tile
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        const int p0 = (j * kWaves + wave) * 64;
+        const int p = p0 + lane;
+        const int r = p / CPR;
+        const int lc = (p % CPR) ^ swz<D>(r);
+        const int key = min(k0 + r, seqK - 1);
+        __builtin_amdgcn_global_load_lds((const void*)(head + (size_t)key * D + lc * 8),
+                                         (LDS_AS void*)(tile + p0 * 8), 16, 0, 0);
+    }
+}
+
+template <int D, int QT, bool kBf16>
+__global__ __launch_bounds__(256) void fa_mfma(PrefillArgs a) {
+    constexpr int ND = D / 32;    // 32-wide d chunks (K dimension of S^T)
+    constexpr int NDT = D / 16;   // 16-wide d tiles (M dimension of O^T)
+    constexpr int BM = kWaves * QT * 16;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBc * D];   // [buffer][K|V]
+
+    const int lane = (int)(threadIdx.x & 63u);
+    const int wave = (int)(threadIdx.x >> 6);
+    const int li = lane & 15, g = lane >> 4;
+
+    // Block -> (batch, head, q block).
+    const int nbh = a.batch * a.nQH;
+    int bh, qrev;
+    if (a.xcd_map) {
+        const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = nbh >> 3;
+        bh = (slot % per) * 8 + xcd;
+        qrev = slot / per;
+    } else {
+        bh = blockIdx.x % nbh;
+        qrev = blockIdx.x / nbh;
+    }
+    const int qblk = a.causal ? (a.nqb - 1 - qrev) : qrev;
+    const int b = bh / a.nQH, h = bh % a.nQH;
+    const int kvh = h / (a.nQH / a.nKVH);
+    const int q0 = qblk * BM;
+    const int qw0 = q0 + wave * QT * 16;   // first query row of this wave
+
+    const uint16_t* Kh = a.K + ((size_t)b * a.nKVH + kvh) * (size_t)a.seqK * D;
+    const uint16_t* Vh = a.V + ((size_t)b * a.nKVH + kvh) * (size_t)a.seqK * D;
+    const uint16_t* Qh = a.Q + ((size_t)b * a.nQH + h) * (size_t)a.seqQ * D;
+
+    // Q as B operands: lane holds Q[q = qw0 + t*16 + li][32*c + 8*g .. +8].
+    u32x4 qb[QT][ND];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+        const int q = min(qw0 + t * 16 + li, a.seqQ - 1);
+#pragma unroll
+        for (int c = 0; c < ND; ++c) qb[t][c] = *(const u32x4*)(Qh + (size_t)q * D + c * 32 + g * 8);
+    }
+
+    f32x4 o[QT][NDT];
+    float m[QT], l[QT];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+        m[t] = -INFINITY; l[t] = 0.f;
+#pragma unroll
+        for (int d = 0; d < NDT; ++d) o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    int ntiles = (a.seqK + kBc - 1) / kBc;
+    if (a.causal) ntiles = min(ntiles, (min(q0 + BM, a.seqQ) - 1) / kBc + 1);
+    const int wave_qmax = min(qw0 + QT * 16, a.seqQ) - 1;   // last real query of this wave
+
+    load_tile<D>(Kh, 0, a.seqK, lds[0][0], wave, lane);
+    load_tile<D>(Vh, 0, a.seqK, lds[0][1], wave, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    for (int it = 0; it < ntiles; ++it) {
+        const int buf = it & 1;
+        if (it + 1 < ntiles) {
+            load_tile<D>(Kh, (it + 1) * kBc, a.seqK, lds[buf ^ 1][0], wave, lane);
+            load_tile<D>(Vh, (it + 1) * kBc, a.seqK, lds[buf ^ 1][1], wave, lane);
+        }
+        const int k0 = it * kBc;
+        if (!(a.causal && k0 > wave_qmax)) {
+            const uint16_t* Kt = lds[buf][0];
+            const uint16_t* Vt = lds[buf][1];
+            // ---- S^T = K Q^T: s[t][kc][u] holds keys k0 + 32kc + 8g + 4u + e for query li.
+            f32x4 s[QT][2][2];
+#pragma unroll
+            for (int t = 0; t < QT; ++t)
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) s[t][kc][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int r = kc * 32 + (li >> 2) * 8 + u * 4 + (li & 3);
+#pragma unroll
+                    for (int c = 0; c < ND; ++c) {
+                        const int lc = c * 4 + g;
+                        const u32x4 ka = *(const u32x4*)(Kt + r * D + ((lc ^ swz<D>(r)) * 8));
+#pragma unroll
+                        for (int t = 0; t < QT; ++t) s[t][kc][u] = mfma<kBf16>(ka, qb[t][c], s[t][kc][u]);
+                    }
+                }
+            }
+            // ---- online softmax (base 2) for each query tile.
+            const bool need_mask = (a.causal && k0 + kBc - 1 > qw0) || (k0 + kBc > a.seqK);
+            u32x4 pb[QT][2];
+#pragma unroll
+            for (int t = 0; t < QT; ++t) {
+                const int q = qw0 + t * 16 + li;
+                float mx = -INFINITY;
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            float v = s[t][kc][u][e] * a.sc;
+                            if (need_mask) {
+                                const int key = k0 + kc * 32 + g * 8 + u * 4 + e;
+                                if (key >= a.seqK || (a.causal && key > q)) v = -INFINITY;
+                            }
+                            s[t][kc][u][e] = v;
+                            mx = fmaxf(mx, v);
+                        }
+                mx = cross_row_allreduce(mx, Max{});
+                const float mnew = fmaxf(m[t], mx);
+                const float mref = (mnew == -INFINITY) ? 0.f : mnew;
+                const float alpha = exp2f(m[t] - mref);
+                m[t] = mnew;
+                float ps = 0.f;
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) {
+                    float p[8];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            p[u * 4 + e] = exp2f(s[t][kc][u][e] - mref);
+                            ps += p[u * 4 + e];
+                        }
+                    pb[t][kc] = u32x4{pack2<kBf16>(p[0], p[1]), pack2<kBf16>(p[2], p[3]),
+                                      pack2<kBf16>(p[4], p[5]), pack2<kBf16>(p[6], p[7])};
+                }
+                l[t] = l[t] * alpha + ps;
+#pragma unroll
+                for (int d = 0; d < NDT; ++d) o[t][d] *= alpha;
+            }
+            // ---- O^T += V^T P^T: A = V^T rows d, 8 consecutive keys per lane via transpose reads.
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc) {
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const int lc = dt * 2 + ((li & 3) >> 1);
+                    const int r0 = kc * 32 + g * 8 + (li >> 2);
+                    const int r1 = r0 + 4;
+                    const int off = (li & 1) * 4;
+                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (LDS_AS s16x4*)(Vt + r0 * D + ((lc ^ swz<D>(r0)) * 8) + off));
+                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (LDS_AS s16x4*)(Vt + r1 * D + ((lc ^ swz<D>(r1)) * 8) + off));
+                    const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+                    const u32x4 va = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
+#pragma unroll
+                    for (int t = 0; t < QT; ++t) o[t][dt] = mfma<kBf16>(va, pb[t][kc], o[t][dt]);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+
+    // ---- O = O^T / l: lane holds d = 16dt + 4g + e of query li.
+    uint16_t* Oh = a.O + ((size_t)b * a.nQH + h) * (size_t)a.seqQ * D;
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+        const float lt = cross_row_allreduce(l[t], Sum{});
+        const float inv = (lt > 0.f) ? 1.f / lt : 1.f;
+        const int q = qw0 + t * 16 + li;
+        if (q < a.seqQ) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const u32x2 w = u32x2{pack2<kBf16>(o[t][dt][0] * inv, o[t][dt][1] * inv),
+                                      pack2<kBf16>(o[t][dt][2] * inv, o[t][dt][3] * inv)};
+                *(u32x2*)(Oh + (size_t)q * D + dt * 16 + g * 4) = w;
+            }
+        }
+    }
+}
+
+// ---- fp32 kernel: one wave per 16 query rows, one key per lane ------------------------
+constexpr int kF32Br = 16;
+
+template <int D>
+__global__ __launch_bounds__(64) void fa_f32(const float* __restrict__ Q, const float* __restrict__ K,
+                                              const float* __restrict__ V, float* __restrict__ O, int seqQ,
+                                              int seqK, int nQH, int nKVH, int causal, int nqb) {
+    __shared__ float q_s[kF32Br][D];
+    __shared__ float v_s[64][D + 1];
+    __shared__ float p_s[kF32Br][64];
+    const int lane = threadIdx.x;
+    const int qb = blockIdx.x % nqb;
+    const int bh = blockIdx.x / nqb;
+    const int b = bh / nQH, h = bh % nQH;
+    const int kvh = h / (nQH / nKVH);
+    const int q0 = qb * kF32Br;
+    const float* Qh = Q + ((size_t)b * nQH + h) * (size_t)seqQ * D;
+    const float* Kh = K + ((size_t)b * nKVH + kvh) * (size_t)seqK * D;
+    const float* Vh = V + ((size_t)b * nKVH + kvh) * (size_t)seqK * D;
+    for (int i = lane; i < kF32Br * D; i += 64) {
+        const int r = i / D, c = i % D;
+        q_s[r][c] = (q0 + r < seqQ) ? Qh[(size_t)(q0 + r) * D + c] : 0.f;
+    }
+    constexpr int EPL = D / 64;   // output columns per lane
+    float m[kF32Br], l[kF32Br], acc[kF32Br][EPL];
+#pragma unroll
+    for (int r = 0; r < kF32Br; ++r) {
+        m[r] = -INFINITY; l[r] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[r][e] = 0.f;
+    }
+    const float scale = 1.f / sqrtf((float)D);
+    int kend = seqK;
+    if (causal) kend = min(seqK, min(q0 + kF32Br, seqQ));
+    __syncthreads();
+    for (int k0 = 0; k0 < kend; k0 += 64) {
+        const int key = k0 + lane;
+        const bool valid = key < kend;
+        for (int i = lane; i < 64 * D; i += 64) {
+            const int r = i / D, c = i % D;
+            v_s[r][c] = (k0 + r < seqK) ? Vh[(size_t)(k0 + r) * D + c] : 0.f;
+        }
+        float kr[D];
+#pragma unroll
+        for (int c = 0; c < D; ++c) kr[c] = valid ? Kh[(size_t)key * D + c] : 0.f;
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < kF32Br; ++r) {
+            float dot = 0.f;
+#pragma unroll
+            for (int c = 0; c < D; ++c) dot += q_s[r][c] * kr[c];
+            float s = dot * scale;
+            if (!valid || (causal && key > q0 + r)) s = -INFINITY;
+            const float mx = allreduce(s, Max{});
+            const float mnew = fmaxf(m[r], mx);
+            const float mref = (mnew == -INFINITY) ? 0.f : mnew;
+            const float p = expf(s - mref);
+            const float alpha = expf(m[r] - mref);
+            l[r] = l[r] * alpha + allreduce(p, Sum{});
+            m[r] = mnew;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[r][e] *= alpha;
+            p_s[r][lane] = p;
+        }
+        __syncthreads();
+        const int nk = min(64, kend - k0);
+        for (int k = 0; k < nk; ++k) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const float v = v_s[k][lane + 64 * e];
+#pragma unroll
+                for (int r = 0; r < kF32Br; ++r) acc[r][e] += p_s[r][k] * v;
+            }
+        }
+        __syncthreads();
+    }
+    float* Oh = O + ((size_t)b * nQH + h) * (size_t)seqQ * D;
+#pragma unroll
+    for (int r = 0; r < kF32Br; ++r) {
+        if (q0 + r >= seqQ) break;
+        const float inv = (l[r] > 0.f) ? 1.f / l[r] : 1.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) Oh[(size_t)(q0 + r) * D + lane + 64 * e] = acc[r][e] * inv;
+    }
+}
+
+template <int D, int QT, bool kBf16>
+int launch_mfma(const cdna3_prefill_cfg& c, const void* Q, const void* K, const void* V, void* O, hipStream_t s) {
+    constexpr int BM = kWaves * QT * 16;
+    PrefillArgs a;
+    a.Q = (const uint16_t*)Q; a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.O = (uint16_t*)O;
+    a.seqQ = c.seqQ; a.seqK = c.seqK; a.nQH = c.nQHeads; a.nKVH = c.nKVHeads; a.batch = c.batch;
+    a.causal = c.causal ? 1 : 0;
+    a.nqb = (c.seqQ + BM - 1) / BM;
+    const long long nbh = (long long)c.batch * c.nQHeads;
+    a.xcd_map = (nbh % 8 == 0) ? 1 : 0;
+    a.sc = kLog2e / sqrtf((float)D);
+    const long long blocks = nbh * a.nqb;
+    if (blocks > 0x7fffffffLL) return CDNA4_ERR_INVALID_VALUE;
+    fa_mfma<D, QT, kBf16><<<(unsigned)blocks, 256, 0, s>>>(a);
+    return launch_status();
+}
+
+template <int D, bool kBf16>
+int dispatch_mfma(const cdna3_prefill_cfg& c, const void* Q, const void* K, const void* V, void* O, hipStream_t s) {
+    // Two q tiles per wave when that still gives >= 2 workgroups per CU, else one.
+    const long long big_blocks = (long long)c.batch * c.nQHeads * ((c.seqQ + 127) / 128);
+    if (big_blocks >= 512) return launch_mfma<D, 2, kBf16>(c, Q, K, V, O, s);
+    return launch_mfma<D, 1, kBf16>(c, Q, K, V, O, s);
+}
+
+}  // namespace
+}  // namespace cdna4
+
+using namespace cdna4;
+
+extern "C" int cdna3_attn_prefill(const void* Q, const void* K, const void* V, void* O, const cdna3_prefill_cfg* cfg,
+                                  int dtype, cdna4_stream_t stream) {
+    if (!cfg) return CDNA4_ERR_INVALID_VALUE;
+    const cdna3_prefill_cfg& c = *cfg;
+    if (c.D != 64 && c.D != 128) return CDNA4_ERR_INVALID_VALUE;
+    if (c.seqQ < 1 || c.seqK < 1 || c.nQHeads < 1 || c.nKVHeads < 1 || c.batch < 1) return CDNA4_ERR_INVALID_VALUE;
+    if (c.nQHeads % c.nKVHeads) return CDNA4_ERR_INVALID_VALUE;
+    if (c.causal && c.seqQ != c.seqK) return CDNA4_ERR_INVALID_VALUE;
+    if (!Q || !K || !V || !O) return CDNA4_ERR_INVALID_VALUE;
+    if (dtype != CDNA4_F16 && dtype != CDNA4_BF16 && dtype != CDNA4_F32) return CDNA4_ERR_INVALID_VALUE;
+    if (dtype != CDNA4_F32 && ((((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V) & 15u) || ((uintptr_t)O & 7u)))
+        return CDNA4_ERR_INVALID_VALUE;
+    if (int e = check_device()) return e;
+    hipStream_t s = (hipStream_t)stream;
+    if (dtype == CDNA4_F32) {
+        const int nqb = (c.seqQ + kF32Br - 1) / kF32Br;
+        const long long blocks = (long long)c.batch * c.nQHeads * nqb;
+        if (blocks > 0x7fffffffLL) return CDNA4_ERR_INVALID_VALUE;
+        if (c.D == 128)
+            fa_f32<128><<<(unsigned)blocks, 64, 0, s>>>((const float*)Q, (const float*)K, (const float*)V, (float*)O,
+                                                       c.seqQ, c.seqK, c.nQHeads, c.nKVHeads, c.causal ? 1 : 0, nqb);
+        else
+            fa_f32<64><<<(unsigned)blocks, 64, 0, s>>>((const float*)Q, (const float*)K, (const float*)V, (float*)O,
+                                                      c.seqQ, c.seqK, c.nQHeads, c.nKVHeads, c.causal ? 1 : 0, nqb);
+        return launch_status();
+    }
+    const bool bf = dtype == CDNA4_BF16;
+    if (c.D == 128) return bf ? dispatch_mfma<128, true>(c, Q, K, V, O, s) : dispatch_mfma<128, false>(c, Q, K, V, O, s);
+    return bf ? dispatch_mfma<64, true>(c, Q, K, V, O, s) : dispatch_mfma<64, false>(c, Q, K, V, O, s);
+}

@@ -1,0 +1,412 @@
+// Device-wide reduce and inclusive scan built on the wave64 DPP primitives (gfx950).
+//
+// The reference has these operations only at wave level (research/wave-primitives/
+// include/wave_primitives/wave_reduce_dpp.hpp:106-113, wave_scan_dpp.hpp:70-87). Here
+// they run over whole HBM arrays without a single LDS instruction:
+//   reduce: stage 1 streams the input with 16-byte loads, each wave folds its share in
+//           registers and combines its 64 lanes with the DPP/permlane butterfly, then
+//           writes one partial; stage 2 (one wave) folds the partials.
+//   scan:   one pass with decoupled look-back. Each single-wave workgroup scans a tile
+//           held in registers (per-lane serial + wave scan per 64x16-byte chunk),
+//           publishes its aggregate, reads its predecessors' aggregates / prefixes 64 at
+//           a time (one per lane) and writes the output. A small fill kernel clears the
+//           tile flags first.
+#include "common.hpp"
+#include "wave_primitives/detail/xlane.hpp"
+
+namespace cdna4 {
+namespace {
+
+using wave::xlane::allreduce;
+using wave::xlane::scan_with_carry;
+using wave::xlane::dpp;
+using wave::xlane::kRowShr1;
+
+// ---- element traits: 16-byte vector <-> accumulator values ------------------------
+template <int DT> struct Elem;
+template <> struct Elem<CDNA4_F32> {
+    using In = float; using Acc = float; using Out = float; static constexpr int VEC = 4;
+    __device__ static Acc load1(const In* p) { return *p; }
+    __device__ static void unpack(const u32x4& v, Acc (&o)[VEC]) {
+        // Element by value: clang folds __builtin_bit_cast of an ext-vector element lvalue
+        // to element 0 (observed with ROCm 7.2 clang), so the element is copied first.
+        o[0] = f32_from_bits(v[0]); o[1] = f32_from_bits(v[1]);
+        o[2] = f32_from_bits(v[2]); o[3] = f32_from_bits(v[3]);
+    }
+};
+template <> struct Elem<CDNA4_I32> {
+    using In = int32_t; using Acc = int32_t; using Out = int32_t; static constexpr int VEC = 4;
+    __device__ static Acc load1(const In* p) { return *p; }
+    __device__ static void unpack(const u32x4& v, Acc (&o)[VEC]) {
+        o[0] = (int32_t)v[0]; o[1] = (int32_t)v[1]; o[2] = (int32_t)v[2]; o[3] = (int32_t)v[3];
+    }
+};
+template <> struct Elem<CDNA4_F64> {
+    using In = double; using Acc = double; using Out = double; static constexpr int VEC = 2;
+    __device__ static Acc load1(const In* p) { return *p; }
+    __device__ static void unpack(const u32x4& v, Acc (&o)[VEC]) {
+        o[0] = __builtin_bit_cast(double, ((uint64_t)v[1] << 32) | v[0]);
+        o[1] = __builtin_bit_cast(double, ((uint64_t)v[3] << 32) | v[2]);
+    }
+};
+template <> struct Elem<CDNA4_I64> {
+    using In = int64_t; using Acc = int64_t; using Out = int64_t; static constexpr int VEC = 2;
+    __device__ static Acc load1(const In* p) { return *p; }
+    __device__ static void unpack(const u32x4& v, Acc (&o)[VEC]) {
+        o[0] = (int64_t)(((uint64_t)v[1] << 32) | v[0]);
+        o[1] = (int64_t)(((uint64_t)v[3] << 32) | v[2]);
+    }
+};
+template <> struct Elem<CDNA4_F16> {
+    using In = uint16_t; using Acc = float; using Out = float; static constexpr int VEC = 8;
+    __device__ static Acc load1(const In* p) { return f16_bits_to_f32(*p); }
+    __device__ static void unpack(const u32x4& v, Acc (&o)[VEC]) {
+        const uint32_t w[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { o[2 * i] = f16_bits_to_f32(w[i] & 0xffffu); o[2 * i + 1] = f16_bits_to_f32(w[i] >> 16); }
+    }
+};
+template <> struct Elem<CDNA4_BF16> {
+    using In = uint16_t; using Acc = float; using Out = float; static constexpr int VEC = 8;
+    __device__ static Acc load1(const In* p) { return bf16_bits_to_f32(*p); }
+    __device__ static void unpack(const u32x4& v, Acc (&o)[VEC]) {
+        const uint32_t w[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { o[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu); o[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16); }
+    }
+};
+
+using OpSum = wave::xlane::Sum;
+using OpMax = wave::xlane::Max;
+using OpMin = wave::xlane::Min;
+
+// ---- reduce -------------------------------------------------------------------------
+constexpr int kReduceThreads = 256;          // 4 waves, no LDS: each wave writes a partial
+constexpr int kReduceMaxBlocks = 2048;       // 8192 partials at most
+constexpr int kReduceUnroll = 4;             // 16-byte loads in flight per lane
+
+template <int DT, class Op, bool kVec>
+__global__ __launch_bounds__(kReduceThreads) void reduce_stage1(const void* __restrict__ in_, size_t n,
+                                                                 void* __restrict__ part_) {
+    using E = Elem<DT>;
+    using Acc = typename E::Acc;
+    const typename E::In* in = (const typename E::In*)in_;
+    Op op;
+    const Acc id = Op::template identity<Acc>();
+    Acc acc[kReduceUnroll];
+#pragma unroll
+    for (int u = 0; u < kReduceUnroll; ++u) acc[u] = id;
+    const size_t nthr = (size_t)gridDim.x * kReduceThreads;
+    const size_t tid = (size_t)blockIdx.x * kReduceThreads + threadIdx.x;
+    size_t scalar_from = 0;
+    if constexpr (kVec) {
+        const u32x4* vin = (const u32x4*)in;
+        const size_t nvec = n / E::VEC;
+        size_t i = tid;
+        for (; i + (kReduceUnroll - 1) * nthr < nvec; i += kReduceUnroll * nthr) {
+            u32x4 v[kReduceUnroll];
+#pragma unroll
+            for (int u = 0; u < kReduceUnroll; ++u) v[u] = __builtin_nontemporal_load(vin + i + u * nthr);
+#pragma unroll
+            for (int u = 0; u < kReduceUnroll; ++u) {
+                Acc x[E::VEC];
+                E::unpack(v[u], x);
+#pragma unroll
+                for (int e = 0; e < E::VEC; ++e) acc[u] = op(acc[u], x[e]);
+            }
+        }
+        for (; i < nvec; i += nthr) {
+            Acc x[E::VEC];
+            E::unpack(vin[i], x);
+#pragma unroll
+            for (int e = 0; e < E::VEC; ++e) acc[0] = op(acc[0], x[e]);
+        }
+        scalar_from = nvec * E::VEC;
+    }
+    for (size_t i = scalar_from + tid; i < n; i += nthr) acc[1] = op(acc[1], E::load1(in + i));
+    static_assert(kReduceUnroll == 4, "combine below assumes four accumulators");
+    Acc a = op(op(acc[0], acc[1]), op(acc[2], acc[3]));
+    a = allreduce(a, op);
+    if ((threadIdx.x & 63u) == 0) ((Acc*)part_)[blockIdx.x * (kReduceThreads / 64) + threadIdx.x / 64] = a;
+}
+
+template <int DT, class Op>
+__global__ __launch_bounds__(64) void reduce_stage2(const void* __restrict__ part_, int count,
+                                                     void* __restrict__ out_) {
+    using Acc = typename Elem<DT>::Acc;
+    const Acc* part = (const Acc*)part_;
+    Op op;
+    Acc a = Op::template identity<Acc>();
+    for (int i = threadIdx.x; i < count; i += 64) a = op(a, part[i]);
+    a = allreduce(a, op);
+    if (threadIdx.x == 0) *(Acc*)out_ = a;
+}
+
+unsigned reduce_blocks(size_t n, int vec) {
+    const size_t per_block = (size_t)kReduceThreads * vec * kReduceUnroll;
+    size_t b = (n + per_block - 1) / per_block;
+    if (b < 1) b = 1;
+    if (b > kReduceMaxBlocks) b = kReduceMaxBlocks;
+    return (unsigned)b;
+}
+
+template <int DT, class Op>
+int reduce_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
+    using E = Elem<DT>;
+    const unsigned blocks = reduce_blocks(n, E::VEC);
+    const bool vec = ((uintptr_t)in % 16) == 0;
+    if (vec)
+        reduce_stage1<DT, Op, true><<<blocks, kReduceThreads, 0, s>>>(in, n, ws);
+    else
+        reduce_stage1<DT, Op, false><<<blocks, kReduceThreads, 0, s>>>(in, n, ws);
+    reduce_stage2<DT, Op><<<1, 64, 0, s>>>(ws, (int)(blocks * (kReduceThreads / 64)), out);
+    return launch_status();
+}
+
+// ---- scan (decoupled look-back, single-wave workgroups) ------------------------------
+template <int DT> struct ScanTile { static constexpr int U = (Elem<DT>::VEC == 8) ? 8 : 16; };
+
+struct ScanState {
+    uint32_t* flag;   // per tile: 0 = nothing, 1 = aggregate published, 2 = prefix published
+    uint64_t* agg;    // per tile: aggregate bits
+    uint64_t* pre;    // per tile: inclusive prefix bits
+    uint32_t* error;  // set when a look-back wait exceeds its bound
+};
+
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+template <typename Acc> __device__ __forceinline__ uint64_t to_bits(Acc v) {
+    if constexpr (sizeof(Acc) == 4) return (uint64_t)__builtin_bit_cast(uint32_t, v);
+    else return __builtin_bit_cast(uint64_t, v);
+}
+template <typename Acc> __device__ __forceinline__ Acc from_bits(uint64_t b) {
+    if constexpr (sizeof(Acc) == 4) return __builtin_bit_cast(Acc, (uint32_t)b);
+    else return __builtin_bit_cast(Acc, b);
+}
+
+__global__ __launch_bounds__(256) void scan_clear_flags(uint32_t* flag, size_t ntiles, uint32_t* error) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < ntiles) flag[i] = 0u;
+    if (i == 0) *error = 0u;
+}
+
+template <typename Acc>
+__device__ __forceinline__ void publish(const ScanState& st, size_t t, Acc v, uint32_t status) {
+    if (threadIdx.x == 0) {
+        uint64_t* slot = (status == 1u) ? st.agg + t : st.pre + t;
+        __hip_atomic_store(slot, to_bits(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(st.flag + t, status, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Combined value of all tiles before `tile`, on every lane.
+template <typename Acc, class Op>
+__device__ Acc look_back(const ScanState& st, size_t tile, Op op) {
+    const unsigned lane = threadIdx.x;
+    const Acc id = Op::template identity<Acc>();
+    Acc acc = id;
+    long long pos = (long long)tile - 1;
+    while (true) {
+        const long long t = pos - (long long)lane;
+        uint32_t s = 2u;
+        uint64_t mzero = 0, mpre = 0;
+        for (uint32_t spin = 0;; ++spin) {
+            s = (t >= 0) ? __hip_atomic_load(st.flag + t, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) : 2u;
+            mpre = __ballot(s == 2u);
+            mzero = __ballot(s == 0u);
+            const uint64_t below = mpre ? ((mpre & (~mpre + 1ull)) - 1ull) : ~0ull;  // lanes before first prefix
+            if ((mzero & below) == 0ull) break;
+            if (spin >= kSpinLimit) {
+                if (lane == 0) __hip_atomic_store(st.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        const int first_pre = mpre ? __builtin_ctzll(mpre) : 64;
+        Acc v = id;
+        if ((int)lane < first_pre && s == 1u) {
+            v = from_bits<Acc>(__hip_atomic_load(st.agg + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        } else if ((int)lane == first_pre && t >= 0) {
+            v = from_bits<Acc>(__hip_atomic_load(st.pre + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        }
+        acc = op(allreduce(v, op), acc);
+        if (first_pre < 64) break;
+        pos -= 64;
+    }
+    return acc;
+}
+
+template <int DT, class Op, bool kVec>
+__global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, size_t n,
+                                                  void* __restrict__ out_, ScanState st) {
+    using E = Elem<DT>;
+    using Acc = typename E::Acc;
+    using Out = typename E::Out;
+    constexpr int VEC = E::VEC;
+    constexpr int U = ScanTile<DT>::U;
+    constexpr size_t TILE = (size_t)64 * VEC * U;
+    const typename E::In* in = (const typename E::In*)in_;
+    Out* out = (Out*)out_;
+    Op op;
+    const Acc id = Op::template identity<Acc>();
+    const unsigned lane = threadIdx.x;
+    const size_t tile = blockIdx.x;
+    const size_t base = tile * TILE;
+
+    Acc v[U][VEC];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const size_t e0 = base + ((size_t)j * 64 + lane) * VEC;
+        if (kVec && e0 + VEC <= n) {
+            E::unpack(__builtin_nontemporal_load((const u32x4*)(in + e0)), v[j]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) v[j][e] = (e0 + e < n) ? E::load1(in + e0 + e) : id;
+        }
+    }
+    // Tile-local inclusive scan in registers.
+    Acc run = id;
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+#pragma unroll
+        for (int e = 1; e < VEC; ++e) v[j][e] = op(v[j][e - 1], v[j][e]);
+        Acc carry;
+        const Acc inc = scan_with_carry(v[j][VEC - 1], op, carry);
+        const Acc exc = dpp<kRowShr1>(carry, inc);          // lane's exclusive within chunk
+        const Acc pre = op(run, exc);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[j][e] = op(pre, v[j][e]);
+        run = op(run, wave::xlane::lane63(inc));             // chunk total, on every lane
+    }
+    const Acc tile_total = run;
+    Acc excl = id;
+    if (tile == 0) {
+        publish(st, tile, tile_total, 2u);
+    } else {
+        publish(st, tile, tile_total, 1u);
+        excl = look_back<Acc>(st, tile, op);
+        publish(st, tile, op(excl, tile_total), 2u);
+    }
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const size_t e0 = base + ((size_t)j * 64 + lane) * VEC;
+        Out o[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = (Out)op(excl, v[j][e]);
+        if (kVec && e0 + VEC <= n) {
+            constexpr int kWords = (int)(sizeof(Out) * VEC / 16);
+#pragma unroll
+            for (int w = 0; w < kWords; ++w) {
+                u32x4 q;
+                __builtin_memcpy(&q, (const char*)o + 16 * w, 16);
+                __builtin_nontemporal_store(q, (u32x4*)(out + e0) + w);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e)
+                if (e0 + e < n) out[e0 + e] = o[e];
+        }
+    }
+}
+
+template <int DT>
+size_t scan_tiles_for(size_t n) {
+    const size_t tile = (size_t)64 * Elem<DT>::VEC * ScanTile<DT>::U;
+    return (n + tile - 1) / tile;
+}
+
+size_t scan_ntiles(size_t n, int dtype) {
+    switch (dtype) {
+        case CDNA4_F32: return scan_tiles_for<CDNA4_F32>(n);
+        case CDNA4_I32: return scan_tiles_for<CDNA4_I32>(n);
+        case CDNA4_F64: return scan_tiles_for<CDNA4_F64>(n);
+        case CDNA4_I64: return scan_tiles_for<CDNA4_I64>(n);
+        case CDNA4_F16: return scan_tiles_for<CDNA4_F16>(n);
+        case CDNA4_BF16: return scan_tiles_for<CDNA4_BF16>(n);
+        default: return 0;
+    }
+}
+
+// Workspace layout: [error:u32 pad to 256][flag: ntiles u32, pad 256][agg: ntiles u64][pre: ntiles u64]
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+size_t scan_ws_bytes(size_t ntiles) {
+    return 256 + align256(ntiles * 4) + align256(ntiles * 8) * 2;
+}
+
+template <int DT, class Op>
+int scan_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
+    const size_t ntiles = scan_tiles_for<DT>(n);
+    if (ntiles == 0) return 0;
+    if (ntiles > 0x7fffffffull) return CDNA4_ERR_INVALID_VALUE;
+    char* w = (char*)ws;
+    ScanState st;
+    st.error = (uint32_t*)w;
+    st.flag = (uint32_t*)(w + 256);
+    st.agg = (uint64_t*)(w + 256 + align256(ntiles * 4));
+    st.pre = (uint64_t*)(w + 256 + align256(ntiles * 4) + align256(ntiles * 8));
+    scan_clear_flags<<<ceil_div(ntiles, 256), 256, 0, s>>>(st.flag, ntiles, st.error);
+    const bool vec = ((uintptr_t)in % 16) == 0 && ((uintptr_t)out % 16) == 0;
+    if (vec)
+        scan_tiles<DT, Op, true><<<(unsigned)ntiles, 64, 0, s>>>(in, n, out, st);
+    else
+        scan_tiles<DT, Op, false><<<(unsigned)ntiles, 64, 0, s>>>(in, n, out, st);
+    return launch_status();
+}
+
+template <template <int, class> class F, int DT>
+int by_op(int op, const void* in, size_t n, void* out, void* ws, hipStream_t s) {
+    switch (op) {
+        case CDNA4_OP_SUM: return F<DT, OpSum>::run(in, n, out, ws, s);
+        case CDNA4_OP_MAX: return F<DT, OpMax>::run(in, n, out, ws, s);
+        case CDNA4_OP_MIN: return F<DT, OpMin>::run(in, n, out, ws, s);
+        default: return CDNA4_ERR_INVALID_VALUE;
+    }
+}
+template <template <int, class> class F>
+int by_dtype(int op, int dtype, const void* in, size_t n, void* out, void* ws, hipStream_t s) {
+    switch (dtype) {
+        case CDNA4_F32: return by_op<F, CDNA4_F32>(op, in, n, out, ws, s);
+        case CDNA4_I32: return by_op<F, CDNA4_I32>(op, in, n, out, ws, s);
+        case CDNA4_F64: return by_op<F, CDNA4_F64>(op, in, n, out, ws, s);
+        case CDNA4_I64: return by_op<F, CDNA4_I64>(op, in, n, out, ws, s);
+        case CDNA4_F16: return by_op<F, CDNA4_F16>(op, in, n, out, ws, s);
+        case CDNA4_BF16: return by_op<F, CDNA4_BF16>(op, in, n, out, ws, s);
+        default: return CDNA4_ERR_INVALID_VALUE;
+    }
+}
+template <int DT, class Op> struct ReduceF { static int run(const void* i, size_t n, void* o, void* w, hipStream_t s) { return reduce_launch<DT, Op>(i, n, o, w, s); } };
+template <int DT, class Op> struct ScanF { static int run(const void* i, size_t n, void* o, void* w, hipStream_t s) { return scan_launch<DT, Op>(i, n, o, w, s); } };
+
+bool valid_dtype(int dtype) { return dtype >= CDNA4_F32 && dtype <= CDNA4_I64; }
+bool valid_op(int op) { return op >= CDNA4_OP_SUM && op <= CDNA4_OP_MIN; }
+
+}  // namespace
+}  // namespace cdna4
+
+using namespace cdna4;
+
+extern "C" size_t cdna3_reduce_workspace_size(size_t /*n*/, int /*dtype*/) {
+    return (size_t)kReduceMaxBlocks * (kReduceThreads / 64) * 8;
+}
+
+extern "C" int cdna3_reduce(int op, int dtype, const void* in, size_t n, void* out, void* workspace,
+                            size_t ws_bytes, cdna4_stream_t stream) {
+    if (!valid_op(op) || !valid_dtype(dtype) || out == nullptr || (n > 0 && in == nullptr)) return CDNA4_ERR_INVALID_VALUE;
+    if (workspace == nullptr || ws_bytes < cdna3_reduce_workspace_size(n, dtype)) return CDNA4_ERR_INVALID_VALUE;
+    if (int e = check_device()) return e;
+    return by_dtype<ReduceF>(op, dtype, in, n, out, workspace, (hipStream_t)stream);
+}
+
+extern "C" size_t cdna3_scan_workspace_size(size_t n, int dtype) {
+    return scan_ws_bytes(scan_ntiles(n, dtype));
+}
+
+extern "C" int cdna3_scan_inclusive(int op, int dtype, const void* in, size_t n, void* out, void* workspace,
+                                    size_t ws_bytes, cdna4_stream_t stream) {
+    if (!valid_op(op) || !valid_dtype(dtype)) return CDNA4_ERR_INVALID_VALUE;
+    if (n == 0) return 0;
+    if (in == nullptr || out == nullptr || workspace == nullptr || ws_bytes < cdna3_scan_workspace_size(n, dtype))
+        return CDNA4_ERR_INVALID_VALUE;
+    if (int e = check_device()) return e;
+    return by_dtype<ScanF>(op, dtype, in, n, out, workspace, (hipStream_t)stream);
+}

@@ -1,0 +1,38 @@
+#pragma once
+// cdna3/runtime/forward.hpp — the runtime's norm and RoPE entry points (gfx950), host side.
+//
+// The reference launched __global__ kernels directly (cdna3-prims/include/cdna3/runtime/
+// forward.hpp:34-56 rmsnorm_f32_kernel, :135-148 rope_kernel; the two-pass DPP layernorm of
+// research/wave-primitives/benchmarks/bench_layernorm.hip:51-114; host table fill_rope in
+// session.hpp:120-135). Here they are host functions over libcdna4_attn.so:
+//   hipLaunchKernelGGL(rmsnorm_f32_kernel, dim3(M), dim3(256), 0, s, X, W, Y, M, H, eps)
+//     -> cdna3::runtime::rmsnorm_f32(X, W, Y, M, H, eps, s)
+//   hipLaunchKernelGGL(rope_kernel, grid, 256, 0, s, T, cos, sin, seq, heads, D)
+//     -> cdna3::runtime::rope_f16(T, cos, sin, seq, heads, D, s)
+#include <hip/hip_runtime_api.h>
+#include <hip/hip_fp16.h>
+#include "../../cdna4_attn.h"
+
+namespace cdna3 {
+namespace runtime {
+
+inline hipError_t rmsnorm_f32(const float* X, const __half* W, float* Y, int M, int H, float eps,
+                              hipStream_t stream = nullptr) {
+    return (hipError_t)cdna3_rmsnorm_f32(X, W, Y, M, H, eps, (cdna4_stream_t)stream);
+}
+inline hipError_t layernorm_f32(const float* X, const float* gamma, const float* beta, float* Y, int M, int H,
+                                float eps = 1e-5f, hipStream_t stream = nullptr) {
+    return (hipError_t)cdna3_layernorm_f32(X, gamma, beta, Y, M, H, eps, (cdna4_stream_t)stream);
+}
+inline hipError_t rope_f16(__half* T, const float* cos, const float* sin, int seq, int heads, int D,
+                           hipStream_t stream = nullptr) {
+    return (hipError_t)cdna3_rope_f16(T, cos, sin, seq, heads, D, (cdna4_stream_t)stream);
+}
+// Device-side fill_rope: cos/sin [T][D] for absolute positions pos0 .. pos0 + T - 1.
+inline hipError_t rope_table_f32(float* cos, float* sin, int pos0, int T, int D, float theta,
+                                 hipStream_t stream = nullptr) {
+    return (hipError_t)cdna3_rope_table_f32(cos, sin, pos0, T, D, theta, (cdna4_stream_t)stream);
+}
+
+}  // namespace runtime
+}  // namespace cdna3

@@ -1,0 +1,157 @@
+/*
+ * cdna4_attn.h — C ABI of libcdna4_attn.so, the MI355X (gfx950) attention hot path.
+ *
+ * Plain C: device pointers, sizes, plain structs and a stream handle. No C++ or torch
+ * types cross this boundary. Every entry point:
+ *   - enqueues its kernels on `stream` (NULL = the default stream) and returns without
+ *     synchronising;
+ *   - returns 0 (hipSuccess) or a hipError_t value: CDNA4_ERR_INVALID_VALUE (1) for a
+ *     shape, dtype or op it does not support, CDNA4_ERR_INVALID_DEVICE_FUNCTION (98)
+ *     when the current device is not gfx950, otherwise the launch error;
+ *   - never allocates, except cdna3_attn_decode with workspace == NULL (see there).
+ * All entry points are re-entrant from any host thread; ordering comes from the stream.
+ *
+ * Tensor layouts are row-major and contiguous unless a stride is given.
+ */
+#ifndef CDNA4_ATTN_H
+#define CDNA4_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t is `struct ihipStream_t*`; this typedef is layout-identical. */
+typedef struct ihipStream_t* cdna4_stream_t;
+
+#define CDNA4_ABI_VERSION 1
+
+enum {
+    CDNA4_OK = 0,
+    CDNA4_ERR_INVALID_VALUE = 1,
+    CDNA4_ERR_INVALID_DEVICE_FUNCTION = 98
+};
+
+/* Element types. */
+enum {
+    CDNA4_F32 = 0,
+    CDNA4_F16 = 1,
+    CDNA4_BF16 = 2,
+    CDNA4_F64 = 3,
+    CDNA4_I32 = 4,
+    CDNA4_I64 = 5
+};
+
+/* Reduction / scan operators. */
+enum {
+    CDNA4_OP_SUM = 0,
+    CDNA4_OP_MAX = 1,
+    CDNA4_OP_MIN = 2
+};
+
+/* Field for field the reference's cdna3::attn::PrefillCfg
+ * (cdna3-prims/include/cdna3/attention.hpp:63-71). */
+typedef struct {
+    int D;         /* head dimension: 64 or 128 */
+    int seqQ;      /* query rows per (batch, head) */
+    int seqK;      /* key/value rows per (batch, kv head) */
+    int nQHeads;
+    int nKVHeads;  /* nQHeads % nKVHeads == 0 (GQA) */
+    int batch;
+    int causal;    /* 1: key k visible to query q iff k <= q (requires seqQ == seqK) */
+} cdna3_prefill_cfg;
+
+/* The reference's DecodeCfg {D, N, nQHeads, nKVHeads} (attention.hpp:73-78) and
+ * DecodeDmeCfg {.., stride_kv} (detail/fa_decode_dme_kernel.hpp:45-48), plus batch. */
+typedef struct {
+    int D;          /* 64 or 128 */
+    int N;          /* cached keys per sequence */
+    int nQHeads;
+    int nKVHeads;
+    int batch;      /* >= 1 */
+    int stride_kv;  /* rows between kv heads in K/V; 0 or N = packed; >= N otherwise */
+} cdna3_decode_cfg;
+
+/* ---- library ---------------------------------------------------------------- */
+
+/* ABI version of the loaded library (CDNA4_ABI_VERSION it was built with). */
+int cdna3_abi_version(void);
+
+/* Static text for a return code of this library. */
+const char* cdna3_error_string(int code);
+
+/* ---- attention: prefill ------------------------------------------------------
+ * Replaces cdna3::attn::prefill (cdna3-prims/include/cdna3/attention.hpp:86-109).
+ * Q, O: [batch][nQHeads][seqQ][D]; K, V: [batch][nKVHeads][seqK][D]; dtype is
+ * CDNA4_F16, CDNA4_BF16 or CDNA4_F32 for all four. Scale 1/sqrt(D), softmax and
+ * accumulation in fp32. Query head h reads kv head h / (nQHeads / nKVHeads).
+ * Unlike the reference, any seqQ, seqK >= 1 is accepted (ragged tails are masked);
+ * shapes the reference would silently truncate therefore compute the full result.
+ * Invalid: D not in {64,128}, non-positive sizes, nQHeads % nKVHeads != 0,
+ * causal with seqQ != seqK, an unknown dtype.
+ */
+int cdna3_attn_prefill(const void* Q, const void* K, const void* V, void* O,
+                       const cdna3_prefill_cfg* cfg, int dtype, cdna4_stream_t stream);
+
+/* ---- attention: decode (one query per sequence, split-K) --------------------
+ * Replaces cdna3::attn::decode (attention.hpp:117-137) and cdna3::attn::decode_dme
+ * (attention.hpp:152-173); the reference has no batch dimension (batch == 1 here).
+ * q, o: [batch][nQHeads][D]; K, V: [batch][nKVHeads][stride_kv][D] (first N rows of
+ * each head are read). dtype CDNA4_F16 or CDNA4_BF16 (q, K, V, o alike).
+ * Split-K partial results go to `workspace` (ws_bytes >= the size returned by
+ * cdna3_attn_decode_workspace_size; the contents need no initialisation). With
+ * workspace == NULL the library uses a per-device buffer it allocates on first use
+ * and keeps until process exit; that form is not safe under stream capture.
+ */
+size_t cdna3_attn_decode_workspace_size(const cdna3_decode_cfg* cfg);
+int cdna3_attn_decode(const void* q, const void* K, const void* V, void* o,
+                      const cdna3_decode_cfg* cfg, int dtype,
+                      void* workspace, size_t ws_bytes, cdna4_stream_t stream);
+
+/* ---- device-wide reduce / scan on the wave64 DPP primitives ------------------
+ * Device-wide counterparts of wave::dpp::reduce_* / scan_inclusive_* (research/
+ * wave-primitives/include/wave_primitives/wave_reduce_dpp.hpp:106-113,
+ * wave_scan_dpp.hpp:70-87), which exist only at wave level in the reference.
+ * dtype: CDNA4_F32, F64, I32, I64 (result type = input type) or CDNA4_F16 / BF16
+ * (fp32 accumulation, fp32 result). Integer sums wrap in two's complement.
+ * reduce: `out` receives one element. scan: `out` receives n elements.
+ * n == 0: reduce writes the operator's identity; scan writes nothing.
+ * Workspace: >= the returned size, no initialisation needed.
+ */
+size_t cdna3_reduce_workspace_size(size_t n, int dtype);
+int cdna3_reduce(int op, int dtype, const void* in, size_t n, void* out,
+                 void* workspace, size_t ws_bytes, cdna4_stream_t stream);
+size_t cdna3_scan_workspace_size(size_t n, int dtype);
+int cdna3_scan_inclusive(int op, int dtype, const void* in, size_t n, void* out,
+                         void* workspace, size_t ws_bytes, cdna4_stream_t stream);
+
+/* ---- runtime norms and RoPE ---------------------------------------------------
+ * cdna3_rmsnorm_f32 replaces rmsnorm_f32_kernel (cdna3-prims/include/cdna3/runtime/
+ * forward.hpp:34-56): Y[m][i] = X[m][i] * rsqrt(mean_i(X[m][:]^2) + eps) * W[i],
+ * X, Y fp32 [M][H], W fp16 [H]. Any H >= 1.
+ * cdna3_layernorm_f32 replaces the two-pass DPP layernorm_kernel (research/
+ * wave-primitives/benchmarks/bench_layernorm.hip:51-114) with runtime H:
+ * Y = (X - mean) * rsqrt(var + eps) * gamma + beta, var = mean((X - mean)^2).
+ * cdna3_rope_f16 replaces rope_kernel (forward.hpp:135-148): rotate-half RoPE in place
+ * on T fp16 [seq][heads][D] with cos/sin fp32 [seq][D]; each (d, d+D/2) pair is read
+ * and written by one thread (the reference updates the pair from two threads).
+ * cdna3_rope_table_f32 fills cos/sin [T][D] for positions pos0.. on the device, as the
+ * host loop Session::fill_rope does (cdna3-prims/include/cdna3/runtime/session.hpp:
+ * 120-135): freq_d = theta^(-2d/D), entries d and d + D/2 share angle pos * freq_d.
+ */
+int cdna3_rmsnorm_f32(const float* X, const void* W_f16, float* Y, int M, int H,
+                      float eps, cdna4_stream_t stream);
+int cdna3_layernorm_f32(const float* X, const float* gamma, const float* beta, float* Y,
+                        int M, int H, float eps, cdna4_stream_t stream);
+int cdna3_rope_f16(void* T, const float* cos_tab, const float* sin_tab, int seq,
+                   int heads, int D, cdna4_stream_t stream);
+int cdna3_rope_table_f32(float* cos_tab, float* sin_tab, int pos0, int T, int D,
+                         float theta, cdna4_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CDNA4_ATTN_H */

@@ -1,0 +1,205 @@
+"""Prefill and decode on gfx950 against the CPU oracle (the restated fp32 references of
+cdna3-prims/tests/validate_attention_api.hip:27-72), on the rounded inputs the GPU sees.
+Bound per output dtype: gpu_util.tolerance (fp32 1e-4, fp16 2e-3, bf16 2e-3 + 2^-9, all in
+units of max(1, |ref|))."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+import cdna4
+import oracle
+from gpu_util import DEV, ROOT, host, max_rel_err, rounded, tolerance
+
+pytestmark = pytest.mark.gpu
+
+
+def prefill_case(D, SQ, SK, HQ, HK, B, causal, dtype, seed=42, dist="normal", std=0.5):
+    gen = (lambda s, n: oracle.normal(s, n, 0.0, std)) if dist == "normal" else (lambda s, n: oracle.uniform(s, n))
+    q, Q = rounded(gen(seed, B * HQ * SQ * D), dtype)
+    k, K = rounded(gen(seed + 1, B * HK * SK * D), dtype)
+    v, V = rounded(gen(seed + 2, B * HK * SK * D), dtype)
+    O = torch.empty_like(Q)
+    cdna4.prefill(Q, K, V, O, cdna4.PrefillCfg(D, SQ, SK, HQ, HK, B, causal))
+    ref = oracle.prefill(q, k, v, D, SQ, SK, HQ, HK, B, causal)
+    return host(O).reshape(ref.shape), ref, (q, k, v)
+
+
+# The reference's prefill validation set (validate_attention_api.hip:154-161).
+REF_PREFILL = [(128, 256, 256, 2, 2, 1, 0), (128, 256, 256, 4, 2, 1, 0), (128, 256, 256, 2, 2, 1, 1),
+               (128, 256, 256, 4, 2, 1, 1), (64, 256, 256, 2, 2, 1, 0), (128, 1024, 1024, 8, 8, 1, 0),
+               (128, 512, 512, 32, 8, 1, 1)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("cfg", REF_PREFILL)
+def test_prefill_reference_validation_set(cfg, dtype):
+    got, ref, _ = prefill_case(*cfg, dtype)
+    err = max_rel_err(got, ref)
+    print(f"prefill {cfg} {dtype}: err {err:.2e}")
+    assert err <= tolerance(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_prefill_fa2_reference_config(dtype):
+    # B1 H8 S512 D64, non-causal, U(-1,1) fp32 from seed 42; fp16-rounded arm.
+    got, ref, _ = prefill_case(64, 512, 512, 8, 8, 1, 0, dtype, seed=42, dist="uniform")
+    err = float(np.max(np.abs(got - ref))) if dtype == torch.float32 else max_rel_err(got, ref)
+    print(f"fa2 reference config {dtype}: err {err:.2e}")
+    assert err <= tolerance(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("cfg", [(64, 100, 200, 4, 2, 2, 0), (128, 77, 77, 3, 1, 1, 1), (64, 1, 1, 1, 1, 1, 1),
+                                 (128, 130, 63, 2, 2, 1, 0), (64, 257, 257, 2, 1, 3, 1), (128, 16, 1000, 8, 8, 1, 0)])
+def test_prefill_ragged_shapes(cfg, dtype):
+    got, ref, _ = prefill_case(*cfg, dtype, seed=7)
+    assert max_rel_err(got, ref) <= tolerance(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_closed_forms(dtype):
+    D, S, H = 128, 320, 4
+    got, ref, (q, k, v) = prefill_case(D, S, S, H, H, 1, 1, dtype, seed=3)
+    vv = v.reshape(1, H, S, D)
+    assert np.array_equal(got[0, :, 0], vv[0, :, 0])          # causal row 0 returns V[0] exactly
+    # Identical keys -> mean of V.
+    kc = np.broadcast_to(k.reshape(1, H, S, D)[:, :, :1], (1, H, S, D)).copy()
+    _, Kc = rounded(kc.reshape(-1), dtype)
+    _, Q = rounded(q, dtype)
+    _, V = rounded(v, dtype)
+    O = torch.empty_like(Q)
+    cdna4.prefill(Q, Kc, V, O, cdna4.PrefillCfg(D, S, S, H, H, 1, 0))
+    mean = vv.astype(np.float64).mean(axis=2, keepdims=True)
+    assert max_rel_err(host(O).reshape(1, H, S, D), np.broadcast_to(mean, (1, H, S, D))) <= tolerance(dtype)
+
+
+def test_prefill_full_size_config_subsample():
+    # BASELINE config 3 shape (B4 H32 S8192 D128 causal bf16). Heads are independent, so the
+    # oracle-generated heads below are checked inside otherwise random full-size tensors.
+    B, H, S, D = 4, 32, 8192, 128
+    torch.manual_seed(0)
+    Q = torch.randn(B, H, S, D, device=DEV, dtype=torch.bfloat16)
+    K = torch.randn(B, H, S, D, device=DEV, dtype=torch.bfloat16)
+    V = torch.randn(B, H, S, D, device=DEV, dtype=torch.bfloat16)
+    heads = [(0, 0), (0, 31), (3, 5), (3, 31)]
+    host_heads = {}
+    for i, (b, h) in enumerate(heads):
+        qkv = []
+        for j, T in enumerate((Q, K, V)):
+            vals, t = rounded(oracle.normal(1000 + 3 * i + j, S * D), torch.bfloat16)
+            T[b, h] = t.reshape(S, D)
+            qkv.append(vals.reshape(1, 1, S, D))
+        host_heads[(b, h)] = qkv
+    O = torch.empty_like(Q)
+    cdna4.prefill(Q, K, V, O, cdna4.PrefillCfg(D, S, S, H, H, B, 1))
+    rows = [0, 1, 63, 64, 127, 128, 4095, 4096, 8190, 8191] + list(oracle.integers(5, 10, 0, S - 1))
+    worst = 0.0
+    for (b, h), (q, k, v) in host_heads.items():
+        want = oracle.prefill_rows(q, k, v, D, S, S, 1, 1, 1, 1, np.array([[0, 0, r] for r in rows], np.int32))
+        got = host(O[b, h, rows])
+        worst = max(worst, max_rel_err(got, want))
+    print(f"config-3 subsample: err {worst:.2e}")
+    assert worst <= tolerance(torch.bfloat16)
+    assert torch.isfinite(O.float()).all()
+
+
+def decode_case(D, N, HQ, HK, B, dtype, seed=7, stride=0, std=0.5, workspace=None):
+    st = stride or N
+    q, qt = rounded(oracle.normal(seed, B * HQ * D, 0.0, std), dtype)
+    k, K = rounded(oracle.normal(seed + 1, B * HK * st * D, 0.0, std), dtype)
+    v, V = rounded(oracle.normal(seed + 2, B * HK * st * D, 0.0, std), dtype)
+    o = torch.empty_like(qt)
+    cdna4.decode(qt, K, V, o, cdna4.DecodeCfg(D, N, HQ, HK, B, stride), workspace=workspace)
+    ref = oracle.decode(q, k, v, D, N, HQ, HK, B, stride)
+    return host(o).reshape(ref.shape), ref
+
+
+# The reference's decode validation set (validate_attention_api.hip:166-172).
+REF_DECODE = [(128, 128, 8, 8), (64, 128, 8, 8), (128, 512, 32, 8), (128, 1024, 32, 8), (128, 4096, 32, 8),
+              (128, 8192, 32, 8)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("cfg", REF_DECODE)
+def test_decode_reference_validation_set(cfg, dtype):
+    got, ref = decode_case(*cfg, 1, dtype)
+    err = max_rel_err(got, ref)
+    print(f"decode {cfg} {dtype}: err {err:.2e}")
+    assert err <= tolerance(dtype)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("group", [1, 2, 3, 4, 7, 8, 16])
+@pytest.mark.parametrize("N", [1, 2, 17, 100, 1000])
+def test_decode_gqa_groups_and_lengths(D, group, N):
+    HK = 2
+    got, ref = decode_case(D, N, HK * group, HK, 3, torch.float16, seed=N + group)
+    assert max_rel_err(got, ref) <= tolerance(torch.float16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_strided_cache(dtype):
+    # decode_dme's layout: [nKVH][stride_kv][D] with stride_kv = max_seq > N.
+    got, ref = decode_case(128, 300, 32, 8, 2, dtype, stride=512)
+    assert max_rel_err(got, ref) <= tolerance(dtype)
+    got, ref = decode_case(64, 37, 8, 8, 1, dtype, stride=64)
+    assert max_rel_err(got, ref) <= tolerance(dtype)
+
+
+def test_decode_full_size_config_and_split_invariance():
+    # batch 32, 32 q heads / 8 kv heads, D128, N8192, fp16 N(0,1).
+    B, HQ, HK, D, N = 32, 32, 8, 128, 8192
+    torch.manual_seed(1)
+    q = torch.randn(B, HQ, D, device=DEV, dtype=torch.float16)
+    K = torch.randn(B, HK, N, D, device=DEV, dtype=torch.float16)
+    V = torch.randn(B, HK, N, D, device=DEV, dtype=torch.float16)
+    checked = [0, 13, 31]
+    hostv = {}
+    for i, b in enumerate(checked):
+        vals = []
+        for j, (T, shape) in enumerate(((q, (HQ, D)), (K, (HK, N, D)), (V, (HK, N, D)))):
+            x, t = rounded(oracle.normal(500 + 3 * i + j, int(np.prod(shape))), torch.float16)
+            T[b] = t.reshape(shape)
+            vals.append(x)
+        hostv[b] = vals
+    ws = torch.empty(cdna4.decode_workspace_size(cdna4.DecodeCfg(D, N, HQ, HK, B)), dtype=torch.uint8, device=DEV)
+    o = torch.empty_like(q)
+    cdna4.decode(q, K, V, o, cdna4.DecodeCfg(D, N, HQ, HK, B), workspace=ws)
+    worst = 0.0
+    for b, (qq, kk, vv) in hostv.items():
+        ref = oracle.decode(qq, kk, vv, D, N, HQ, HK, 1)
+        worst = max(worst, max_rel_err(host(o[b]), ref[0]))
+    print(f"config-4 checked batches: err {worst:.2e}")
+    assert worst <= tolerance(torch.float16)
+    # A batch-1 call splits the keys of one sequence into many more partials; same result.
+    for b in (0, 31):
+        o1 = torch.empty_like(q[b:b + 1])
+        cdna4.decode(q[b:b + 1].contiguous(), K[b:b + 1].contiguous(), V[b:b + 1].contiguous(), o1,
+                     cdna4.DecodeCfg(D, N, HQ, HK, 1))
+        assert max_rel_err(host(o1[0]), host(o[b]).astype(np.float64)) <= 2e-3
+    assert torch.isfinite(o.float()).all()
+
+
+def test_torch_op_mirrors():
+    D, S, HQ, HK = 128, 192, 8, 2
+    q, Q = rounded(oracle.normal(1, HQ * S * D, 0, 0.5), torch.float16)
+    k, K = rounded(oracle.normal(2, HK * S * D, 0, 0.5), torch.float16)
+    v, V = rounded(oracle.normal(3, HK * S * D, 0, 0.5), torch.float16)
+    o = cdna4.flash_attn(Q.reshape(HQ, S, D), K.reshape(HK, S, D), V.reshape(HK, S, D))
+    ref = oracle.prefill(q, k, v, D, S, S, HQ, HK, 1, 1)[0]
+    assert max_rel_err(host(o), ref) <= tolerance(torch.float16)
+    od = cdna4.flash_attn_decode(Q.reshape(HQ, S, D)[:, -1].contiguous(), K.reshape(HK, S, D), V.reshape(HK, S, D))
+    assert max_rel_err(host(od), ref[:, -1]) <= tolerance(torch.float16)
+
+
+def test_cpp_dropin_validation_program():
+    exe = os.path.join(ROOT, "tests", "native", "validate_attention_api")
+    assert os.path.exists(exe), "tests/native not built"
+    r = subprocess.run([exe, os.path.join(ROOT, "oracle", "liboracle.so")], capture_output=True, text=True,
+                       timeout=300)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "Result: 13/13 PASS" in r.stdout

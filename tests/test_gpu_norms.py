@@ -1,0 +1,54 @@
+"""RMSNorm, two-pass LayerNorm, RoPE and the RoPE table on gfx950 against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+import cdna4
+import oracle
+from gpu_util import DEV
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("M,H", [(1, 768), (512, 768), (65536 // 64, 64), (300, 512), (7, 4096), (5, 1000), (3, 5000), (2, 3)])
+def test_rmsnorm(M, H):
+    X = oracle.normal(M * 7 + H, M * H, 0.0, 2.0).reshape(M, H)
+    wv, wb = oracle.round16(oracle.normal(H, H, 1.0, 0.1), oracle.F16)
+    Xt = torch.from_numpy(X).to(DEV)
+    Wt = torch.from_numpy(wb.view(np.int16)).view(torch.float16).to(DEV)
+    got = cdna4.rmsnorm_f32(Xt, Wt, 1e-6).cpu().numpy()
+    np.testing.assert_allclose(got, oracle.rmsnorm(X, wb, 1e-6), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("M,H", [(65536 // 32, 64), (2048, 512), (512, 768), (4, 4096), (3, 6000), (5, 100), (9, 1)])
+def test_layernorm(M, H):
+    # The reference's input generator for its LayerNorm benchmark (bench_layernorm.hip:131).
+    i = np.arange(M * H, dtype=np.uint64)
+    X = ((((i * 1103515245 + 12345) & 0xFF).astype(np.float32)) / 32.0 - 4.0).reshape(M, H)
+    g, b = oracle.uniform(1, H, 0.5, 1.5), oracle.uniform(2, H)
+    got = cdna4.layernorm_f32(torch.from_numpy(X).to(DEV), torch.from_numpy(g).to(DEV), torch.from_numpy(b).to(DEV),
+                              1e-5).cpu().numpy()
+    np.testing.assert_allclose(got, oracle.layernorm(X, g, b, 1e-5), rtol=1e-4, atol=2e-5)
+    if H >= 64:
+        ones, zeros = torch.ones(H, device=DEV), torch.zeros(H, device=DEV)
+        y = cdna4.layernorm_f32(torch.from_numpy(X).to(DEV), ones, zeros, 1e-5).double().cpu().numpy()
+        np.testing.assert_allclose(y.mean(1), 0.0, atol=1e-4)      # bench_layernorm.hip:137-150
+        np.testing.assert_allclose(y.var(1), 1.0, atol=1e-2)
+
+
+@pytest.mark.parametrize("seq,heads,D,pos0", [(512, 12, 64, 0), (1, 12, 64, 511), (33, 8, 128, 1000), (4, 2, 10, 3)])
+def test_rope_table_and_rope(seq, heads, D, pos0):
+    cos, sin = cdna4.rope_table_f32(pos0, seq, D, 10000.0)
+    c_ref, s_ref = oracle.rope_table(pos0, seq, D, 10000.0)
+    c_got, s_got = cos.cpu().numpy(), sin.cpu().numpy()
+    # Device cosf/sinf/powf differ from glibc by a few ulp of the angle (pos up to ~1500 rad).
+    np.testing.assert_allclose(c_got, c_ref, atol=2e-4)
+    np.testing.assert_allclose(s_got, s_ref, atol=2e-4)
+    vals, bits = oracle.round16(oracle.normal(seq + D, seq * heads * D), oracle.F16)
+    T = torch.from_numpy(bits.view(np.int16)).view(torch.float16).to(DEV)
+    ct, st = torch.from_numpy(c_ref).to(DEV), torch.from_numpy(s_ref).to(DEV)
+    cdna4.rope_f16(T, ct, st, seq, heads, D)
+    got = oracle.widen(T.view(torch.int16).cpu().numpy().view(np.uint16), oracle.F16)
+    want = oracle.widen(oracle.rope(bits, c_ref, s_ref, seq, heads, D), oracle.F16)
+    # Same fp32 formula and RNE; only FMA contraction may move a result by one fp16 ulp.
+    np.testing.assert_allclose(got, want, rtol=2.0 ** -10, atol=2.0 ** -24)

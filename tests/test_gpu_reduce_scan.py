@@ -1,0 +1,104 @@
+"""Device-wide reduce / inclusive scan (cdna3_reduce, cdna3_scan_inclusive) against the oracle:
+bit-exact for integers (two's-complement wrap), rel 1e-3 (or tighter) for floats, over ragged
+and edge sizes, misaligned inputs, every op and dtype, and the full 2^26-element sweep."""
+import numpy as np
+import pytest
+import torch
+
+import cdna4
+import oracle
+from gpu_util import DEV
+
+pytestmark = pytest.mark.gpu
+
+TORCH = {oracle.F32: torch.float32, oracle.F64: torch.float64, oracle.I32: torch.int32, oracle.I64: torch.int64,
+         oracle.F16: torch.float16, oracle.BF16: torch.bfloat16}
+SIZES = [0, 1, 2, 63, 64, 65, 255, 1023, 4095, 4096, 4097, 8193, 100003, (1 << 20) + 7]
+
+
+def make(dtype, n, seed, offset=0):
+    """Host values (what the oracle reads) and a device tensor view starting `offset` elements in."""
+    if dtype == oracle.I32:
+        h = oracle.integers(seed, n + offset, -1000, 1000)
+    elif dtype == oracle.I64:
+        h = oracle.integers(seed, n + offset, -1000, 1000, np.int64)
+    elif dtype == oracle.F64:
+        h = oracle.uniform_f64(seed, n + offset)
+    elif dtype == oracle.F32:
+        h = oracle.uniform(seed, n + offset)
+    else:
+        h = oracle.round16(oracle.uniform(seed, n + offset), dtype)[1]
+    t = torch.from_numpy(h.view(np.int16) if dtype in (oracle.F16, oracle.BF16) else h).to(DEV)
+    if dtype in (oracle.F16, oracle.BF16):
+        t = t.view(TORCH[dtype])
+    return h[offset:], t[offset:]
+
+
+def check_scalar(dtype, op, got, want, n):
+    if dtype in (oracle.I32, oracle.I64):
+        assert int(got) == int(want)
+    elif op != oracle.SUM:
+        assert float(got) == float(want)
+    else:
+        # fp32 accumulation: rel 1e-3 (the sweep's bound); fp64: n * 1e-13 absolute for n values
+        # in [-1, 1] (the a-priori bound n * eps * sum|x| is far larger).
+        tol = 1e-13 * max(1, n) if dtype == oracle.F64 else max(1e-6, 1e-3 * abs(want))
+        assert abs(float(got) - want) <= tol, (got, want)
+
+
+@pytest.mark.parametrize("dtype", [oracle.I32, oracle.I64, oracle.F32, oracle.F64, oracle.F16, oracle.BF16])
+@pytest.mark.parametrize("op", [oracle.SUM, oracle.MAX, oracle.MIN])
+def test_reduce_sizes(dtype, op):
+    for i, n in enumerate(SIZES):
+        h, t = make(dtype, n, 100 + i, offset=i % 3)    # offsets 1, 2 exercise the unaligned path
+        got = cdna4.reduce(t, op).cpu().numpy()[0]
+        check_scalar(dtype, op, got, oracle.reduce(op, dtype, h), n)
+
+
+@pytest.mark.parametrize("dtype", [oracle.I32, oracle.I64, oracle.F32, oracle.F64, oracle.F16, oracle.BF16])
+@pytest.mark.parametrize("op", [oracle.SUM, oracle.MAX, oracle.MIN])
+def test_scan_sizes(dtype, op):
+    for i, n in enumerate(SIZES[1:]):
+        h, t = make(dtype, n, 200 + i, offset=i % 2)
+        got = cdna4.scan_inclusive(t, op).cpu().numpy()
+        want = oracle.scan_inclusive(op, dtype, h)
+        if dtype in (oracle.I32, oracle.I64) or op != oracle.SUM:
+            assert np.array_equal(got.astype(np.float64) if got.dtype.kind == "f" else got, want)
+        else:
+            tol = 1e-13 * n if dtype == oracle.F64 else 2e-5 * max(1.0, np.sqrt(n))
+            assert np.max(np.abs(got.astype(np.float64) - want)) <= tol
+
+
+def test_scan_repeated_calls_reuse_workspace():
+    # Flags in the workspace are cleared by each call: the same workspace serves many calls.
+    n = 300007
+    h, t = make(oracle.I32, n, 5)
+    ws = torch.empty(cdna4.scan_workspace_size(n, cdna4.I32), dtype=torch.uint8, device=DEV)
+    want = oracle.scan_inclusive(oracle.SUM, oracle.I32, h)
+    for _ in range(5):
+        assert np.array_equal(cdna4.scan_inclusive(t, "sum", workspace=ws).cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("dtype", [oracle.I32, oracle.I64, oracle.F32, oracle.F64, oracle.F16, oracle.BF16])
+def test_full_sweep_2_26(dtype):
+    n = 1 << 26
+    h, t = make(dtype, n, 7)
+    for op in (oracle.SUM, oracle.MAX, oracle.MIN):
+        got = cdna4.reduce(t, op).cpu().numpy()[0]
+        want = oracle.reduce(op, dtype, h)
+        if dtype in (oracle.I32, oracle.I64) or op != oracle.SUM:
+            assert float(got) == float(want) if dtype not in (oracle.I32, oracle.I64) else int(got) == int(want)
+        else:
+            assert abs(float(got) - want) <= 1e-3 * max(1.0, abs(want))
+    got = cdna4.scan_inclusive(t, "sum")
+    want = oracle.scan_inclusive(oracle.SUM, dtype, h)
+    if dtype in (oracle.I32, oracle.I64):
+        assert np.array_equal(got.cpu().numpy(), want)
+    else:
+        g = got.cpu().numpy().astype(np.float64)
+        # rel 1e-3 of the running magnitude (the prefix of U(-1,1) wanders ~sqrt(i))
+        scale = np.maximum(1.0, np.sqrt(np.arange(1, n + 1, dtype=np.float64)))
+        assert np.max(np.abs(g - want) / scale) <= 1e-3
+    # Checksum of checksums: the last prefix equals the total.
+    if dtype in (oracle.I32, oracle.I64):
+        assert int(got[-1].item()) == int(cdna4.reduce(t, "sum").item())
