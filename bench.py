@@ -8,7 +8,9 @@ Also reported in the same line:
   decode: BASELINE config 4 (batch 32, 32 q heads / 8 kv heads, D 128, N 8192 fp16) in GB/s of
           algorithmic KV + q/o bytes, with its HBM roofline fraction;
   dpp:    BASELINE config 2 sample (device-wide f32 reduce_sum and inclusive scan_sum over 2^26
-          elements, four rotating inputs so the 256 MB Infinity Cache cannot serve repeats) in GB/s.
+          elements, four rotating inputs so the 256 MB Infinity Cache cannot serve repeats) in GB/s;
+  copy_1GiB: a plain device copy, the achievable-bandwidth reference and the known-size kernel
+          that calibrates the HBM traffic counters.
 Kernel durations come from HIP events recorded on the stream the kernels run on (torch's current
 stream). The CPU baseline times the reference's own fp32 cpu_prefill (built from the reference
 sources into oracle/_ref) on one (batch, head) of config 3, one thread; the oracle's restatement
@@ -35,28 +37,25 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["all", "prefill", "decode", "dpp"], default="all")
+    p.add_argument("--only", choices=["all", "prefill", "decode", "dpp", "copy"], default="all")
     return p.parse_args()
 
 
 def time_launches(torch, fn, steps, warmup):
-    """Average per-launch duration (ms) from events around each launch, and the total (ms)."""
+    """Average duration of one step (ms) and the total (ms): HIP events recorded on the launch
+    stream around `steps` back-to-back steps (no events between steps, which would add their own
+    gaps), after `warmup` untimed steps, with the device synchronised on both sides."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0.record()
     for i in range(steps):
-        starts[i].record()
         fn(i)
-        ends[i].record()
     t1.record()
     torch.cuda.synchronize()
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return sum(per) / len(per), t0.elapsed_time(t1)
+    total = t0.elapsed_time(t1)
+    return total / steps, total
 
 
 def load_traffic(name):
@@ -146,6 +145,17 @@ def bench_dpp(torch, cdna4, steps, warmup):
             "config": {"workload": "BASELINE config 2 sample: f32, n = 2^26, 4 rotating inputs"}}
 
 
+def bench_copy(torch, steps, warmup):
+    """Plain 1 GiB device copy (torch copy_): the known-size kernel that calibrates the HBM traffic
+    counters (FETCH_SIZE / WRITE_SIZE) and the achievable copy bandwidth on this box."""
+    n = 1 << 28
+    src = torch.rand(n, device="cuda")
+    dst = torch.empty_like(src)
+    avg_ms, _ = time_launches(torch, lambda i=0: dst.copy_(src), steps, warmup)
+    return {"value": 2.0 * 4 * n / (avg_ms * 1e-3) / 1e9, "unit": "GB/s", "avg_us": avg_ms * 1e3,
+            "bytes_read": 4 * n, "bytes_written": 4 * n}
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -172,6 +182,8 @@ def main():
                            "config": d["config"], "roofline": d["roofline"], "dtype": "fp16"})
     if args.only in ("all", "dpp"):
         result["dpp"] = bench_dpp(torch, cdna4, args.steps, args.warmup)
+    if args.only in ("all", "copy"):
+        result["copy_1GiB"] = bench_copy(torch, args.steps, args.warmup)
     if args.only in ("all", "prefill") and not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_prefill()
     print(json.dumps(result), flush=True)
