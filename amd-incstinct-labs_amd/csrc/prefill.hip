@@ -56,26 +56,42 @@ __device__ __forceinline__ f32x4 mfma(const u32x4& a, const u32x4& b, const f32x
     else
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 values -> one dword of two 16-bit values, round to nearest even
+// (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 on gfx950).
 template <bool kBf16>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-    if constexpr (kBf16) return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
-    else return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+    const f32x2 v = {a, b};
+    if constexpr (kBf16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
 }
 
-// XOR swizzle of the 16-byte chunks of key row r inside a K/V tile (see file comment).
+// XOR swizzle of the 16-byte chunks of key row r inside a K/V tile. Requirements:
+//   * K operand reads (ds_read_b128): the 16 rows one lane group reads, r = 8*(m/4) + 4u + m%4
+//     (bits 0, 1, 3, 4 vary), land on 16 different chunk positions;
+//   * V^T operand reads (ds_read_b64_tr_b16): a lane group reads rows 8g + x (x = 0..3) at two
+//     adjacent chunks; the 4 rows must land on distinct chunk pairs, and lane groups g, g+1 (one
+//     32-lane LDS pass) on different 128-byte halves.
+// D = 128 (16 chunks per 256-byte row): bit 0 <- r4, bits 1-2 <- r0-r1, bit 3 <- r3.
+// D = 64 (8 chunks per 128-byte row, two rows per 256-byte bank window): bit 0 <- r4,
+// bit 1 <- r1, bit 2 <- r3.
 template <int D>
 __device__ __forceinline__ int swz(int r) {
     if constexpr (D == 128)
-        return ((r >> 3) & 1) | ((r & 1) << 1) | (((r >> 1) & 1) << 2) | (((r >> 4) & 1) << 3);
+        return ((r >> 4) & 1) | ((r & 3) << 1) | (((r >> 3) & 1) << 3);
     else
-        return ((r >> 3) & 1) | (((r >> 1) & 1) << 1) | (((r >> 4) & 1) << 2);
+        return ((r >> 4) & 1) | (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
 }
 
 struct PrefillArgs {
     const uint16_t* Q; const uint16_t* K; const uint16_t* V; uint16_t* O;
     int seqQ, seqK, nQH, nKVH, batch, causal;
     int nqb;          // q blocks per (batch, head)
-    int xcd_map;      // 1: (batch, head) -> XCD-aware block order
+    int xcd_map;      // 1: all q blocks of a (batch, head) on one XCD, heads in sequence
     float sc;         // log2(e) / sqrt(D)
 };
 
@@ -97,6 +113,112 @@ __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ head, int
     }
 }
 
+// Softmax reference maxima are refreshed only when a new maximum exceeds them by more than
+// kTau (base-2 units): p = 2^(s - m) then stays <= 2^kTau, and O and l, accumulated against the
+// same reference, give the exact O / l; most tiles skip the rescale of O entirely.
+constexpr float kTau = 8.f;
+
+// One 32-key half (kc) of a K/V tile: S^T MFMAs, masking, lazy rescale, P, P.V MFMAs.
+template <int D, int QT, bool kBf16, bool kMask>
+__device__ __forceinline__ void chunk_body(const uint16_t* Kt, const uint16_t* Vt, const u32x4 (&qb)[QT][D / 32],
+                                           f32x4 (&o)[QT][D / 16], float (&m)[QT], float (&l)[QT], int kc,
+                                           int k0, int qw0, int seqK, int causal, float sc, int li, int g) {
+    constexpr int ND = D / 32;
+    constexpr int NDT = D / 16;
+    // ---- S^T = K Q^T: s[t][u][e] is key k0 + 32kc + 8g + 4u + e for query qw0 + 16t + li.
+    f32x4 s[QT][2];
+#pragma unroll
+    for (int t = 0; t < QT; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) s[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < ND; ++c) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int r = kc * 32 + (li >> 2) * 8 + u * 4 + (li & 3);
+            const int lc = c * 4 + g;
+            const u32x4 ka = *(const u32x4*)(Kt + r * D + ((lc ^ swz<D>(r)) * 8));
+#pragma unroll
+            for (int t = 0; t < QT; ++t) s[t][u] = mfma<kBf16>(ka, qb[t][c], s[t][u]);
+        }
+    }
+    // ---- chunk maxima (raw scores; sc > 0 commutes with max), masked entries -> -inf.
+    float mx[QT];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+        float v = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (kMask) {
+                    const int key = k0 + kc * 32 + g * 8 + u * 4 + e;
+                    const int q = qw0 + t * 16 + li;
+                    if (key >= seqK || (causal && key > q)) s[t][u][e] = -INFINITY;
+                }
+                v = fmaxf(v, s[t][u][e]);
+            }
+        mx[t] = cross_row_allreduce(v, Max{}) * sc;
+    }
+    // ---- lazy rescale, skipped by the whole wave when no query needs it.
+    bool need = false;
+#pragma unroll
+    for (int t = 0; t < QT; ++t) need |= mx[t] > m[t] + kTau;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+        for (int t = 0; t < QT; ++t) {
+            const float mn = (mx[t] > m[t] + kTau) ? mx[t] : m[t];
+            const float alpha = (m[t] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[t] - mn);
+            m[t] = mn;
+            l[t] *= alpha;
+#pragma unroll
+            for (int d = 0; d < NDT; ++d) o[t][d] *= alpha;
+        }
+    }
+    // ---- P = 2^(s sc - m), packed into the B operands of the P.V MFMA; l += row sums.
+    u32x4 pb[QT];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+        const float mref = (m[t] == -INFINITY) ? 0.f : m[t];
+        float p[8], ps = 0.f;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                p[u * 4 + e] = __builtin_amdgcn_exp2f(fmaf(s[t][u][e], sc, -mref));
+                ps += p[u * 4 + e];
+            }
+        pb[t] = u32x4{pack2<kBf16>(p[0], p[1]), pack2<kBf16>(p[2], p[3]), pack2<kBf16>(p[4], p[5]),
+                      pack2<kBf16>(p[6], p[7])};
+        l[t] += ps;
+    }
+    // ---- O^T += V^T P^T: A = V^T rows d, 8 consecutive keys per lane via transpose reads.
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+        const int lc = dt * 2 + ((li & 3) >> 1);
+        const int r0 = kc * 32 + g * 8 + (li >> 2);
+        const int r1 = r0 + 4;
+        const int off = (li & 1) * 4;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (LDS_AS s16x4*)(Vt + r0 * D + ((lc ^ swz<D>(r0)) * 8) + off));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (LDS_AS s16x4*)(Vt + r1 * D + ((lc ^ swz<D>(r1)) * 8) + off));
+        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+        const u32x4 va = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
+#pragma unroll
+        for (int t = 0; t < QT; ++t) o[t][dt] = mfma<kBf16>(va, pb[t], o[t][dt]);
+    }
+}
+
+template <int D, int QT, bool kBf16, bool kMask>
+__device__ __forceinline__ void tile_body(const uint16_t* Kt, const uint16_t* Vt, const u32x4 (&qb)[QT][D / 32],
+                                          f32x4 (&o)[QT][D / 16], float (&m)[QT], float (&l)[QT],
+                                          int k0, int qw0, int seqK, int causal, float sc, int li, int g) {
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+        chunk_body<D, QT, kBf16, kMask>(Kt, Vt, qb, o, m, l, kc, k0, qw0, seqK, causal, sc, li, g);
+}
+
 template <int D, int QT, bool kBf16>
 __global__ __launch_bounds__(256) void fa_mfma(PrefillArgs a) {
     constexpr int ND = D / 32;    // 32-wide d chunks (K dimension of S^T)
@@ -108,13 +230,16 @@ __global__ __launch_bounds__(256) void fa_mfma(PrefillArgs a) {
     const int wave = (int)(threadIdx.x >> 6);
     const int li = lane & 15, g = lane >> 4;
 
-    // Block -> (batch, head, q block).
+    // Block -> (batch, head, q block). Workgroups are dispatched round-robin over the 8 XCDs
+    // (blockIdx % 8). With xcd_map, XCD x owns heads x, x + 8, ... and walks them one at a time,
+    // the q blocks of a head heaviest (causal) first, so the workgroups resident on an XCD share
+    // one head's K/V in that XCD's L2.
     const int nbh = a.batch * a.nQH;
     int bh, qrev;
     if (a.xcd_map) {
-        const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = nbh >> 3;
-        bh = (slot % per) * 8 + xcd;
-        qrev = slot / per;
+        const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+        bh = (slot / a.nqb) * 8 + xcd;
+        qrev = slot % a.nqb;
     } else {
         bh = blockIdx.x % nbh;
         qrev = blockIdx.x / nbh;
@@ -164,93 +289,13 @@ __global__ __launch_bounds__(256) void fa_mfma(PrefillArgs a) {
         }
         const int k0 = it * kBc;
         if (!(a.causal && k0 > wave_qmax)) {
-            const uint16_t* Kt = lds[buf][0];
-            const uint16_t* Vt = lds[buf][1];
-            // ---- S^T = K Q^T: s[t][kc][u] holds keys k0 + 32kc + 8g + 4u + e for query li.
-            f32x4 s[QT][2][2];
-#pragma unroll
-            for (int t = 0; t < QT; ++t)
-#pragma unroll
-                for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-                    for (int u = 0; u < 2; ++u) s[t][kc][u] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kc = 0; kc < 2; ++kc) {
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const int r = kc * 32 + (li >> 2) * 8 + u * 4 + (li & 3);
-#pragma unroll
-                    for (int c = 0; c < ND; ++c) {
-                        const int lc = c * 4 + g;
-                        const u32x4 ka = *(const u32x4*)(Kt + r * D + ((lc ^ swz<D>(r)) * 8));
-#pragma unroll
-                        for (int t = 0; t < QT; ++t) s[t][kc][u] = mfma<kBf16>(ka, qb[t][c], s[t][kc][u]);
-                    }
-                }
-            }
-            // ---- online softmax (base 2) for each query tile.
             const bool need_mask = (a.causal && k0 + kBc - 1 > qw0) || (k0 + kBc > a.seqK);
-            u32x4 pb[QT][2];
-#pragma unroll
-            for (int t = 0; t < QT; ++t) {
-                const int q = qw0 + t * 16 + li;
-                float mx = -INFINITY;
-#pragma unroll
-                for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-                    for (int u = 0; u < 2; ++u)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            float v = s[t][kc][u][e] * a.sc;
-                            if (need_mask) {
-                                const int key = k0 + kc * 32 + g * 8 + u * 4 + e;
-                                if (key >= a.seqK || (a.causal && key > q)) v = -INFINITY;
-                            }
-                            s[t][kc][u][e] = v;
-                            mx = fmaxf(mx, v);
-                        }
-                mx = cross_row_allreduce(mx, Max{});
-                const float mnew = fmaxf(m[t], mx);
-                const float mref = (mnew == -INFINITY) ? 0.f : mnew;
-                const float alpha = exp2f(m[t] - mref);
-                m[t] = mnew;
-                float ps = 0.f;
-#pragma unroll
-                for (int kc = 0; kc < 2; ++kc) {
-                    float p[8];
-#pragma unroll
-                    for (int u = 0; u < 2; ++u)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            p[u * 4 + e] = exp2f(s[t][kc][u][e] - mref);
-                            ps += p[u * 4 + e];
-                        }
-                    pb[t][kc] = u32x4{pack2<kBf16>(p[0], p[1]), pack2<kBf16>(p[2], p[3]),
-                                      pack2<kBf16>(p[4], p[5]), pack2<kBf16>(p[6], p[7])};
-                }
-                l[t] = l[t] * alpha + ps;
-#pragma unroll
-                for (int d = 0; d < NDT; ++d) o[t][d] *= alpha;
-            }
-            // ---- O^T += V^T P^T: A = V^T rows d, 8 consecutive keys per lane via transpose reads.
-#pragma unroll
-            for (int kc = 0; kc < 2; ++kc) {
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) {
-                    const int lc = dt * 2 + ((li & 3) >> 1);
-                    const int r0 = kc * 32 + g * 8 + (li >> 2);
-                    const int r1 = r0 + 4;
-                    const int off = (li & 1) * 4;
-                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (LDS_AS s16x4*)(Vt + r0 * D + ((lc ^ swz<D>(r0)) * 8) + off));
-                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (LDS_AS s16x4*)(Vt + r1 * D + ((lc ^ swz<D>(r1)) * 8) + off));
-                    const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
-                    const u32x4 va = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
-#pragma unroll
-                    for (int t = 0; t < QT; ++t) o[t][dt] = mfma<kBf16>(va, pb[t][kc], o[t][dt]);
-                }
-            }
+            if (need_mask)
+                tile_body<D, QT, kBf16, true>(lds[buf][0], lds[buf][1], qb, o, m, l, k0, qw0, a.seqK, a.causal, a.sc,
+                                              li, g);
+            else
+                tile_body<D, QT, kBf16, false>(lds[buf][0], lds[buf][1], qb, o, m, l, k0, qw0, a.seqK, a.causal, a.sc,
+                                               li, g);
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -379,9 +424,9 @@ int launch_mfma(const cdna3_prefill_cfg& c, const void* Q, const void* K, const 
 
 template <int D, bool kBf16>
 int dispatch_mfma(const cdna3_prefill_cfg& c, const void* Q, const void* K, const void* V, void* O, hipStream_t s) {
-    // Two q tiles per wave when that still gives >= 2 workgroups per CU, else one.
-    const long long big_blocks = (long long)c.batch * c.nQHeads * ((c.seqQ + 127) / 128);
-    if (big_blocks >= 512) return launch_mfma<D, 2, kBf16>(c, Q, K, V, O, s);
+    // 64 queries per wave when that still fills the GPU (>= 2 workgroups per CU), else 16.
+    const long long big_blocks = (long long)c.batch * c.nQHeads * ((c.seqQ + 255) / 256);
+    if (big_blocks >= 512) return launch_mfma<D, 4, kBf16>(c, Q, K, V, O, s);
     return launch_mfma<D, 1, kBf16>(c, Q, K, V, O, s);
 }
 

@@ -67,10 +67,25 @@ __device__ __forceinline__ T dpp(T old, T v) {
 }
 
 // DPP move for patterns with a source lane for every lane (quad_perm, mirrors,
-// newbcast): `old` is never read, so it is left to the compiler.
+// newbcast): `old` is never read. bound_ctrl is set so the compiler can fuse the move
+// into the consuming VALU op (v_add_f32_dpp, v_max_f32_dpp, ...).
 template <int Ctrl, typename T>
 __device__ __forceinline__ T dpp_full(T v) {
-    return dpp<Ctrl>(v, v);
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "dpp_full: 32- or 64-bit types");
+    if constexpr (sizeof(T) == 4) {
+        return join<T>(__builtin_amdgcn_update_dpp(0u, lo32(v), Ctrl, 0xf, 0xf, true), 0);
+    } else {
+        uint32_t lo = __builtin_amdgcn_update_dpp(0u, lo32(v), Ctrl, 0xf, 0xf, true);
+        uint32_t hi = __builtin_amdgcn_update_dpp(0u, hi32(v), Ctrl, 0xf, 0xf, true);
+        return join<T>(lo, hi);
+    }
+}
+
+// DPP move whose out-of-row lanes read zero (bound_ctrl): the identity of a sum, and a form
+// the compiler fuses into v_add_*_dpp.
+template <int Ctrl, typename T>
+__device__ __forceinline__ T dpp_zero(T v) {
+    return dpp_full<Ctrl>(v);
 }
 
 // Pair-of-rows exchange. Returns the pair's even-row value in `ev`, odd-row in `od`.
@@ -200,10 +215,18 @@ __device__ __forceinline__ T lane63(T v) {
 template <typename Op, typename T>
 __device__ __forceinline__ T scan_with_carry(T v, Op op, T& carry) {
     const T id = Op::template identity<T>();
-    v = op(v, dpp<kRowShr1>(id, v));
-    v = op(v, dpp<kRowShr2>(id, v));
-    v = op(v, dpp<kRowShr4>(id, v));
-    v = op(v, dpp<kRowShr8>(id, v));
+    if constexpr (std::is_same<Op, Sum>::value) {
+        // Sum: out-of-row lanes read 0 through bound_ctrl, which fuses into v_add_*_dpp.
+        v = op(v, dpp_zero<kRowShr1>(v));
+        v = op(v, dpp_zero<kRowShr2>(v));
+        v = op(v, dpp_zero<kRowShr4>(v));
+        v = op(v, dpp_zero<kRowShr8>(v));
+    } else {
+        v = op(v, dpp<kRowShr1>(id, v));
+        v = op(v, dpp<kRowShr2>(id, v));
+        v = op(v, dpp<kRowShr4>(id, v));
+        v = op(v, dpp<kRowShr8>(id, v));
+    }
     const T rt = dpp_full<kRowNewBcast15>(v);   // this row's total on every lane
     T ev, od;
     rows_pair(rt, ev, od);                       // pair's even / odd row totals
