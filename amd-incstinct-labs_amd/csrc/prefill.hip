@@ -47,7 +47,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBc = 64;       // keys per K/V tile
-constexpr int kWaves = 4;     // waves per workgroup
+
 
 template <bool kBf16>
 __device__ __forceinline__ f32x4 mfma(const u32x4& a, const u32x4& b, const f32x4& c) {
@@ -96,14 +96,15 @@ struct PrefillArgs {
 };
 
 // Issue the asynchronous copy of keys [k0, k0 + kBc) of one head into an LDS tile.
-template <int D>
+template <int D, int W>
 __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ head, int k0, int seqK,
                                           uint16_t* tile, int wave, int lane) {
     constexpr int CPR = D / 8;                       // 16-byte chunks per key row
-    constexpr int NI = kBc * CPR / (64 * kWaves);    // wave instructions per tile
+    constexpr int NI = kBc * CPR / (64 * W);         // wave instructions per tile
+    static_assert(NI >= 1 && NI * 64 * W == kBc * CPR, "tile copy must split evenly over the waves");
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
-        const int p0 = (j * kWaves + wave) * 64;
+        const int p0 = (j * W + wave) * 64;
         const int p = p0 + lane;
         const int r = p / CPR;
         const int lc = (p % CPR) ^ swz<D>(r);
@@ -117,6 +118,10 @@ __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ head, int
 // kTau (base-2 units): p = 2^(s - m) then stays <= 2^kTau, and O and l, accumulated against the
 // same reference, give the exact O / l; most tiles skip the rescale of O entirely.
 constexpr float kTau = 8.f;
+// Initial reference maximum: finite, so no -inf - -inf can arise; the first chunk with a visible
+// key always exceeds it by more than kTau and replaces it (alpha = 2^(kInitM - m) = 0), and masked
+// scores (-inf) give p = 0 against it.
+constexpr float kInitM = -1e30f;
 
 // One 32-key half (kc) of a K/V tile: S^T MFMAs, masking, lazy rescale, P, P.V MFMAs.
 template <int D, int QT, bool kBf16, bool kMask>
@@ -168,7 +173,7 @@ __device__ __forceinline__ void chunk_body(const uint16_t* Kt, const uint16_t* V
 #pragma unroll
         for (int t = 0; t < QT; ++t) {
             const float mn = (mx[t] > m[t] + kTau) ? mx[t] : m[t];
-            const float alpha = (m[t] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[t] - mn);
+            const float alpha = __builtin_amdgcn_exp2f(m[t] - mn);   // 0 while m is kInitM
             m[t] = mn;
             l[t] *= alpha;
 #pragma unroll
@@ -179,7 +184,7 @@ __device__ __forceinline__ void chunk_body(const uint16_t* Kt, const uint16_t* V
     u32x4 pb[QT];
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-        const float mref = (m[t] == -INFINITY) ? 0.f : m[t];
+        const float mref = m[t];
         float p[8], ps = 0.f;
 #pragma unroll
         for (int u = 0; u < 2; ++u)
@@ -219,11 +224,11 @@ __device__ __forceinline__ void tile_body(const uint16_t* Kt, const uint16_t* Vt
         chunk_body<D, QT, kBf16, kMask>(Kt, Vt, qb, o, m, l, kc, k0, qw0, seqK, causal, sc, li, g);
 }
 
-template <int D, int QT, bool kBf16>
-__global__ __launch_bounds__(256) void fa_mfma(PrefillArgs a) {
+template <int D, int W, int QT, bool kBf16>
+__global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
     constexpr int ND = D / 32;    // 32-wide d chunks (K dimension of S^T)
     constexpr int NDT = D / 16;   // 16-wide d tiles (M dimension of O^T)
-    constexpr int BM = kWaves * QT * 16;
+    constexpr int BM = W * QT * 16;
     __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBc * D];   // [buffer][K|V]
 
     const int lane = (int)(threadIdx.x & 63u);
@@ -260,32 +265,36 @@ __global__ __launch_bounds__(256) void fa_mfma(PrefillArgs a) {
     for (int t = 0; t < QT; ++t) {
         const int q = min(qw0 + t * 16 + li, a.seqQ - 1);
 #pragma unroll
-        for (int c = 0; c < ND; ++c) qb[t][c] = *(const u32x4*)(Qh + (size_t)q * D + c * 32 + g * 8);
+        for (int c = 0; c < ND; ++c) {
+            qb[t][c] = *(const u32x4*)(Qh + (size_t)q * D + c * 32 + g * 8);
+        }
     }
 
     f32x4 o[QT][NDT];
     float m[QT], l[QT];
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-        m[t] = -INFINITY; l[t] = 0.f;
+        m[t] = kInitM; l[t] = 0.f;
 #pragma unroll
-        for (int d = 0; d < NDT; ++d) o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int d = 0; d < NDT; ++d) {
+            o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
     }
 
     int ntiles = (a.seqK + kBc - 1) / kBc;
     if (a.causal) ntiles = min(ntiles, (min(q0 + BM, a.seqQ) - 1) / kBc + 1);
     const int wave_qmax = min(qw0 + QT * 16, a.seqQ) - 1;   // last real query of this wave
 
-    load_tile<D>(Kh, 0, a.seqK, lds[0][0], wave, lane);
-    load_tile<D>(Vh, 0, a.seqK, lds[0][1], wave, lane);
+    load_tile<D, W>(Kh, 0, a.seqK, lds[0][0], wave, lane);
+    load_tile<D, W>(Vh, 0, a.seqK, lds[0][1], wave, lane);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     for (int it = 0; it < ntiles; ++it) {
         const int buf = it & 1;
         if (it + 1 < ntiles) {
-            load_tile<D>(Kh, (it + 1) * kBc, a.seqK, lds[buf ^ 1][0], wave, lane);
-            load_tile<D>(Vh, (it + 1) * kBc, a.seqK, lds[buf ^ 1][1], wave, lane);
+            load_tile<D, W>(Kh, (it + 1) * kBc, a.seqK, lds[buf ^ 1][0], wave, lane);
+            load_tile<D, W>(Vh, (it + 1) * kBc, a.seqK, lds[buf ^ 1][1], wave, lane);
         }
         const int k0 = it * kBc;
         if (!(a.causal && k0 > wave_qmax)) {
@@ -405,9 +414,9 @@ __global__ __launch_bounds__(64) void fa_f32(const float* __restrict__ Q, const 
     }
 }
 
-template <int D, int QT, bool kBf16>
+template <int D, int W, int QT, bool kBf16>
 int launch_mfma(const cdna3_prefill_cfg& c, const void* Q, const void* K, const void* V, void* O, hipStream_t s) {
-    constexpr int BM = kWaves * QT * 16;
+    constexpr int BM = W * QT * 16;
     PrefillArgs a;
     a.Q = (const uint16_t*)Q; a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.O = (uint16_t*)O;
     a.seqQ = c.seqQ; a.seqK = c.seqK; a.nQH = c.nQHeads; a.nKVH = c.nKVHeads; a.batch = c.batch;
@@ -418,16 +427,17 @@ int launch_mfma(const cdna3_prefill_cfg& c, const void* Q, const void* K, const 
     a.sc = kLog2e / sqrtf((float)D);
     const long long blocks = nbh * a.nqb;
     if (blocks > 0x7fffffffLL) return CDNA4_ERR_INVALID_VALUE;
-    fa_mfma<D, QT, kBf16><<<(unsigned)blocks, 256, 0, s>>>(a);
+    fa_mfma<D, W, QT, kBf16><<<(unsigned)blocks, 64 * W, 0, s>>>(a);
     return launch_status();
 }
 
 template <int D, bool kBf16>
 int dispatch_mfma(const cdna3_prefill_cfg& c, const void* Q, const void* K, const void* V, void* O, hipStream_t s) {
-    // 64 queries per wave when that still fills the GPU (>= 2 workgroups per CU), else 16.
+    // 8 waves x 32 queries (two waves per SIMD) when that gives >= 2 workgroups per CU, else
+    // 4 waves x 16 queries for small problems.
     const long long big_blocks = (long long)c.batch * c.nQHeads * ((c.seqQ + 255) / 256);
-    if (big_blocks >= 512) return launch_mfma<D, 4, kBf16>(c, Q, K, V, O, s);
-    return launch_mfma<D, 1, kBf16>(c, Q, K, V, O, s);
+    if (big_blocks >= 512) return launch_mfma<D, 8, 2, kBf16>(c, Q, K, V, O, s);
+    return launch_mfma<D, 4, 1, kBf16>(c, Q, K, V, O, s);
 }
 
 }  // namespace
