@@ -108,7 +108,7 @@ __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ head, int
         const int p = p0 + lane;
         const int r = p / CPR;
         const int lc = (p % CPR) ^ swz<D>(r);
-        const int key = min(k0 + r, seqK - 1);
+        const int key = min(k0 + r, seqK - 1);   // rows past the end re-read the last key (masked)
         __builtin_amdgcn_global_load_lds((const void*)(head + (size_t)key * D + lc * 8),
                                          (LDS_AS void*)(tile + p0 * 8), 16, 0, 0);
     }
@@ -123,10 +123,34 @@ constexpr float kTau = 8.f;
 // scores (-inf) give p = 0 against it.
 constexpr float kInitM = -1e30f;
 
+// Per-lane byte offsets of the LDS operand reads within one K or V tile. The swizzle of a row
+// depends only on bits 0, 1, 3, 4 of its index, which come from the lane alone, so the offsets of
+// every sub-tile u, key chunk kc and (for V) row r + 4 differ from these by a compile-time
+// constant (folded into the ds_read immediate). Within a row, d chunk c of the K operand sits at
+// k ^ (c << 6) and d tile dt of the V^T operand at v ^ (dt << 5): the chunk index occupies offset
+// bits that the row base and the swizzled low bits do not touch.
+struct LdsOffsets {
+    uint32_t k;   // K operand: d chunk 0, sub-tile 0, key chunk 0
+    uint32_t v;   // first V^T transpose read: d tile 0, key chunk 0
+    __device__ __forceinline__ uint32_t kc(int c) const { return k ^ ((uint32_t)c << 6); }
+    __device__ __forceinline__ uint32_t vd(int dt) const { return v ^ ((uint32_t)dt << 5); }
+};
+
+template <int D>
+__device__ __forceinline__ LdsOffsets lds_offsets(int li, int g) {
+    LdsOffsets off;
+    const int rk = (li >> 2) * 8 + (li & 3);                 // K row of A-row li, sub-tile 0
+    off.k = (uint32_t)(rk * D + ((g ^ swz<D>(rk)) * 8)) * 2u;
+    const int rv = g * 8 + (li >> 2);                        // V row of the first transpose read
+    off.v = (uint32_t)(rv * D + ((((li & 3) >> 1) ^ swz<D>(rv)) * 8) + (li & 1) * 4) * 2u;
+    return off;
+}
+
 // One 32-key half (kc) of a K/V tile: S^T MFMAs, masking, lazy rescale, P, P.V MFMAs.
 template <int D, int QT, bool kBf16, bool kMask>
-__device__ __forceinline__ void chunk_body(const uint16_t* Kt, const uint16_t* Vt, const u32x4 (&qb)[QT][D / 32],
-                                           f32x4 (&o)[QT][D / 16], float (&m)[QT], float (&l)[QT], int kc,
+__device__ __forceinline__ void chunk_body(const char* Kt, const char* Vt, const LdsOffsets& off,
+                                           const u32x4 (&qb)[QT][D / 32],
+                                           f32x4 (&o)[QT][D / 16], float (&m)[QT], f32x4 (&lacc)[QT], int kc,
                                            int k0, int qw0, int seqK, int causal, float sc, int li, int g) {
     constexpr int ND = D / 32;
     constexpr int NDT = D / 16;
@@ -140,15 +164,18 @@ __device__ __forceinline__ void chunk_body(const uint16_t* Kt, const uint16_t* V
     for (int c = 0; c < ND; ++c) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int r = kc * 32 + (li >> 2) * 8 + u * 4 + (li & 3);
-            const int lc = c * 4 + g;
-            const u32x4 ka = *(const u32x4*)(Kt + r * D + ((lc ^ swz<D>(r)) * 8));
+            // row kc*32 + 8*(li/4) + 4u + li%4, d chunk 4c + g (swizzled)
+            const u32x4 ka = *(const u32x4*)(Kt + off.kc(c) + (kc * 32 + u * 4) * D * 2);
 #pragma unroll
             for (int t = 0; t < QT; ++t) s[t][u] = mfma<kBf16>(ka, qb[t][c], s[t][u]);
         }
     }
-    // ---- chunk maxima (raw scores; sc > 0 commutes with max), masked entries -> -inf.
-    float mx[QT];
+    // ---- per-lane maxima of the raw scores (sc > 0 commutes with max), masked entries -> -inf.
+    // Each lane checks its own scores against its query's reference maximum; only when some lane
+    // of the wave sees one more than kTau above it does the wave form the cross-lane maxima
+    // (uniform over the four lanes of a query) and rescale O and l.
+    float lm[QT];
+    bool need = false;
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
         float v = -INFINITY;
@@ -163,51 +190,46 @@ __device__ __forceinline__ void chunk_body(const uint16_t* Kt, const uint16_t* V
                 }
                 v = fmaxf(v, s[t][u][e]);
             }
-        mx[t] = cross_row_allreduce(v, Max{}) * sc;
+        lm[t] = v;
+        need |= v * sc > m[t] + kTau;
     }
-    // ---- lazy rescale, skipped by the whole wave when no query needs it.
-    bool need = false;
-#pragma unroll
-    for (int t = 0; t < QT; ++t) need |= mx[t] > m[t] + kTau;
     if (__builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
         for (int t = 0; t < QT; ++t) {
-            const float mn = (mx[t] > m[t] + kTau) ? mx[t] : m[t];
+            const float mx = cross_row_allreduce(lm[t], Max{}) * sc;
+            const float mn = (mx > m[t] + kTau) ? mx : m[t];
             const float alpha = __builtin_amdgcn_exp2f(m[t] - mn);   // 0 while m is kInitM
             m[t] = mn;
-            l[t] *= alpha;
+            lacc[t] *= alpha;
 #pragma unroll
             for (int d = 0; d < NDT; ++d) o[t][d] *= alpha;
         }
     }
-    // ---- P = 2^(s sc - m), packed into the B operands of the P.V MFMA; l += row sums.
+    // ---- P = 2^(s sc - m), packed into the B operands of the P.V MFMA; l += row sums of exactly
+    // the (rounded) weights the product uses, as an MFMA with an all-ones A operand: every lane
+    // of a query's column receives the full sum over the chunk's 32 keys.
     u32x4 pb[QT];
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
         const float mref = m[t];
-        float p[8], ps = 0.f;
+        float p[8];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                p[u * 4 + e] = __builtin_amdgcn_exp2f(fmaf(s[t][u][e], sc, -mref));
-                ps += p[u * 4 + e];
-            }
+            for (int e = 0; e < 4; ++e) p[u * 4 + e] = __builtin_amdgcn_exp2f(fmaf(s[t][u][e], sc, -mref));
         pb[t] = u32x4{pack2<kBf16>(p[0], p[1]), pack2<kBf16>(p[2], p[3]), pack2<kBf16>(p[4], p[5]),
                       pack2<kBf16>(p[6], p[7])};
-        l[t] += ps;
+        const uint32_t one2 = kBf16 ? 0x3F803F80u : 0x3C003C00u;   // two 16-bit 1.0
+        lacc[t] = mfma<kBf16>(u32x4{one2, one2, one2, one2}, pb[t], lacc[t]);
     }
     // ---- O^T += V^T P^T: A = V^T rows d, 8 consecutive keys per lane via transpose reads.
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-        const int lc = dt * 2 + ((li & 3) >> 1);
-        const int r0 = kc * 32 + g * 8 + (li >> 2);
-        const int r1 = r0 + 4;
-        const int off = (li & 1) * 4;
+        // rows r0 = kc*32 + 8g + li/4 and r0 + 4, d chunk 2dt + (li%4)/2 (swizzled), half li%2
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (LDS_AS s16x4*)(Vt + r0 * D + ((lc ^ swz<D>(r0)) * 8) + off));
+            (LDS_AS s16x4*)(Vt + off.vd(dt) + (kc * 32) * D * 2));
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (LDS_AS s16x4*)(Vt + r1 * D + ((lc ^ swz<D>(r1)) * 8) + off));
+            (LDS_AS s16x4*)(Vt + off.vd(dt) + (kc * 32 + 4) * D * 2));
         const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
         const u32x4 va = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
 #pragma unroll
@@ -216,12 +238,36 @@ __device__ __forceinline__ void chunk_body(const uint16_t* Kt, const uint16_t* V
 }
 
 template <int D, int QT, bool kBf16, bool kMask>
-__device__ __forceinline__ void tile_body(const uint16_t* Kt, const uint16_t* Vt, const u32x4 (&qb)[QT][D / 32],
-                                          f32x4 (&o)[QT][D / 16], float (&m)[QT], float (&l)[QT],
+__device__ __forceinline__ void tile_body(const char* Kt, const char* Vt, const LdsOffsets& off,
+                                          const u32x4 (&qb)[QT][D / 32],
+                                          f32x4 (&o)[QT][D / 16], float (&m)[QT], f32x4 (&lacc)[QT],
                                           int k0, int qw0, int seqK, int causal, float sc, int li, int g) {
 #pragma unroll
     for (int kc = 0; kc < 2; ++kc)
-        chunk_body<D, QT, kBf16, kMask>(Kt, Vt, qb, o, m, l, kc, k0, qw0, seqK, causal, sc, li, g);
+        chunk_body<D, QT, kBf16, kMask>(Kt, Vt, off, qb, o, m, lacc, kc, k0, qw0, seqK, causal, sc, li, g);
+}
+
+// One K/V tile: issue the asynchronous copy of the next tile into (kn, vn), then compute the
+// current tile from (kt, vt). The four buffers are distinct, and saying so with __restrict__
+// lets the compiler skip the wait for the copy before every read of the current tile.
+template <int D, int W, int QT, bool kBf16>
+__device__ __forceinline__ void tile_step(const uint16_t* __restrict__ kt, const uint16_t* __restrict__ vt,
+                                          uint16_t* __restrict__ kn, uint16_t* __restrict__ vn, bool load_next,
+                                          const uint16_t* Kh, const uint16_t* Vh, int k0, int wave_qmax,
+                                          const PrefillArgs& a, const LdsOffsets& off, const u32x4 (&qb)[QT][D / 32],
+                                          f32x4 (&o)[QT][D / 16], float (&m)[QT], f32x4 (&lacc)[QT], int qw0,
+                                          int wave, int lane, int li, int g) {
+    if (load_next) {
+        load_tile<D, W>(Kh, k0 + kBc, a.seqK, kn, wave, lane);
+        load_tile<D, W>(Vh, k0 + kBc, a.seqK, vn, wave, lane);
+    }
+    if (!(a.causal && k0 > wave_qmax)) {
+        const bool need_mask = (a.causal && k0 + kBc - 1 > qw0) || (k0 + kBc > a.seqK);
+        if (need_mask)
+            tile_body<D, QT, kBf16, true>((const char*)kt, (const char*)vt, off, qb, o, m, lacc, k0, qw0, a.seqK, a.causal, a.sc, li, g);
+        else
+            tile_body<D, QT, kBf16, false>((const char*)kt, (const char*)vt, off, qb, o, m, lacc, k0, qw0, a.seqK, a.causal, a.sc, li, g);
+    }
 }
 
 template <int D, int W, int QT, bool kBf16>
@@ -270,17 +316,19 @@ __global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
         }
     }
 
-    f32x4 o[QT][NDT];
-    float m[QT], l[QT];
+    f32x4 o[QT][NDT], lacc[QT];
+    float m[QT];
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-        m[t] = kInitM; l[t] = 0.f;
+        m[t] = kInitM;
+        lacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int d = 0; d < NDT; ++d) {
             o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     }
 
+    const LdsOffsets off = lds_offsets<D>(li, g);
     int ntiles = (a.seqK + kBc - 1) / kBc;
     if (a.causal) ntiles = min(ntiles, (min(q0 + BM, a.seqQ) - 1) / kBc + 1);
     const int wave_qmax = min(qw0 + QT * 16, a.seqQ) - 1;   // last real query of this wave
@@ -292,29 +340,17 @@ __global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
 
     for (int it = 0; it < ntiles; ++it) {
         const int buf = it & 1;
-        if (it + 1 < ntiles) {
-            load_tile<D, W>(Kh, (it + 1) * kBc, a.seqK, lds[buf ^ 1][0], wave, lane);
-            load_tile<D, W>(Vh, (it + 1) * kBc, a.seqK, lds[buf ^ 1][1], wave, lane);
-        }
-        const int k0 = it * kBc;
-        if (!(a.causal && k0 > wave_qmax)) {
-            const bool need_mask = (a.causal && k0 + kBc - 1 > qw0) || (k0 + kBc > a.seqK);
-            if (need_mask)
-                tile_body<D, QT, kBf16, true>(lds[buf][0], lds[buf][1], qb, o, m, l, k0, qw0, a.seqK, a.causal, a.sc,
-                                              li, g);
-            else
-                tile_body<D, QT, kBf16, false>(lds[buf][0], lds[buf][1], qb, o, m, l, k0, qw0, a.seqK, a.causal, a.sc,
-                                               li, g);
-        }
+        tile_step<D, W, QT, kBf16>(lds[buf][0], lds[buf][1], lds[buf ^ 1][0], lds[buf ^ 1][1], it + 1 < ntiles, Kh, Vh,
+                                   it * kBc, wave_qmax, a, off, qb, o, m, lacc, qw0, wave, lane, li, g);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
 
-    // ---- O = O^T / l: lane holds d = 16dt + 4g + e of query li.
+    // ---- O = O^T / l: lane holds d = 16dt + 4g + e of query li, and its query's full l.
     uint16_t* Oh = a.O + ((size_t)b * a.nQH + h) * (size_t)a.seqQ * D;
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-        const float lt = cross_row_allreduce(l[t], Sum{});
+        const float lt = lacc[t][0];
         const float inv = (lt > 0.f) ? 1.f / lt : 1.f;
         const int q = qw0 + t * 16 + li;
         if (q < a.seqQ) {
