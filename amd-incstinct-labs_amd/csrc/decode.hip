@@ -6,19 +6,17 @@
 // accumulation.
 //
 // MI355X design (not the reference's structure):
-//   * Each wave streams its own contiguous range of keys of one (batch, kv head) and
-//     serves every query head of the GQA group from registers, so K/V bytes are read from
-//     HBM exactly once (the reference re-reads a kv head once per query head).
-//   * A key row is D*2 bytes = D/8 lanes x 16 bytes: every load is a fully coalesced 128-bit
-//     global load, 64 lanes cover 64*16 bytes of consecutive keys, U loads of K and of V are
-//     in flight per lane.
-//   * q.k uses v_dot2_f32_{f16,bf16} (fp32 accumulation), the per-key lane-group sum is the
-//     DPP row butterfly; softmax runs in base 2 with a log2(e)-prescaled scale.
-//   * Each wave merges its lane groups with the permlane swaps and writes one (m, l, O)
-//     partial per query head; a second kernel merges the partials of each query head, with
-//     the max and the denominator formed by the wave butterfly. No LDS is used anywhere.
-#include "common.hpp"
-#include "wave_primitives/detail/xlane.hpp"
+//   * Split-K: each single-wave workgroup streams one contiguous range of keys of one (batch,
+//     kv head) and serves all query heads of the GQA group (up to 16 per wave) at once, so K/V
+//     bytes are read from HBM exactly once (the reference re-reads a kv head once per query
+//     head). The q.K and P.V products run on the matrix cores with the prefill tile machinery
+//     (the heads take the place of the 16 query columns), which leaves the VALU only the
+//     softmax: the kernel is bound by HBM, not by per-element dot products.
+//   * K/V chunks go HBM -> LDS by asynchronous global_load_lds copies into a ring of stages,
+//     three chunks per wave in flight.
+//   * A second kernel merges the (m, l, O) partials of each query head, with the max and the
+//     denominator formed by the wave butterfly.
+#include "attn_tile.hpp"
 #include <mutex>
 #include <math.h>
 
@@ -26,162 +24,157 @@ namespace cdna4 {
 namespace {
 
 using wave::xlane::allreduce;
-using wave::xlane::cross_row_allreduce;
-using wave::xlane::dpp_full;
 using wave::xlane::Sum;
 using wave::xlane::Max;
+using tile::f32x4;
 
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
-
-constexpr int kDecodeU = 4;           // keys per lane group per iteration (loads in flight)
-constexpr int kDecodeWaves = 4;       // independent waves per 256-thread workgroup
-constexpr int kTargetWaves = 4096;    // 16 waves per CU on 256 CUs
-constexpr int kMaxHeadsPerWave = 8;   // query heads served from one pass over K/V
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <bool kBf16>
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-    if constexpr (kBf16) return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2_t, a), __builtin_bit_cast(b2_t, b), c, false);
-    else return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a), __builtin_bit_cast(h2_t, b), c, false);
-}
-template <bool kBf16>
-__device__ __forceinline__ void unpack8(const u32x4& v, float (&o)[8]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if constexpr (kBf16) { o[2 * i] = bf16_bits_to_f32(v[i] & 0xffffu); o[2 * i + 1] = bf16_bits_to_f32(v[i] >> 16); }
-        else { o[2 * i] = f16_bits_to_f32(v[i] & 0xffffu); o[2 * i + 1] = f16_bits_to_f32(v[i] >> 16); }
-    }
-}
 template <bool kBf16>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
     if constexpr (kBf16) return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
     else return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
 }
 
-// Sum over the D/8 lanes that share one key row (16 lanes at D=128, 8 at D=64).
-template <int D>
-__device__ __forceinline__ float keyrow_sum(float v) {
-    v += dpp_full<wave::xlane::kQuadXor1>(v);
-    v += dpp_full<wave::xlane::kQuadXor2>(v);
-    v += dpp_full<wave::xlane::kRowHalfMirror>(v);
-    if constexpr (D == 128) v += dpp_full<wave::xlane::kRowMirror>(v);
-    return v;
-}
-
-// Combine the per-lane-group values of one lane position over all lane groups of the wave.
-template <int D, class Op>
-__device__ __forceinline__ float across_groups(float v, Op op) {
-    if constexpr (D == 64) v = op(v, dpp_full<0x128>(v));   // row_ror:8 pairs the two 8-lane groups of a row
-    return cross_row_allreduce(v, op);
-}
-
 struct DecodeArgs {
     const void* q; const void* K; const void* V;
     float* part_ml;   // [batch][nQH][P][2]
     float* part_o;    // [batch][nQH][P][D]
-    int N, nQH, nKVH, stride, G, HB, KPW, P;
+    int N, nQH, nKVH, stride, G, HB, KPW, P;   // HB: groups of <= 16 query heads per kv head
     float sc;         // log2(e) / sqrt(D)
 };
 
-template <int D, int HB, bool kBf16>
-__global__ __launch_bounds__(256) void decode_partial(DecodeArgs a) {
-    constexpr int LPK = D / 8;            // lanes per key row
-    constexpr int KPL = 64 / LPK;         // key rows per wave load
-    const unsigned lane = threadIdx.x & 63u;
-    const int wave_split = blockIdx.x * kDecodeWaves + (int)(threadIdx.x >> 6);
-    if (wave_split >= a.P) return;
-    const int kvh = blockIdx.y / (a.G / HB);
-    const int sub = blockIdx.y % (a.G / HB);
+// ---- matrix-core split-K partial -----------------------------------------------------------
+//
+// One single-wave workgroup per (key split, batch, kv head, group of up to 16 query heads). The
+// query heads of the GQA group are the 16 "query" columns of the prefill tile machinery
+// (S^T = K Q^T, O^T = V^T P^T on 16x16x32 MFMAs, lazy base-2 softmax), so each K/V byte is
+// read from HBM once for all heads of its group, and the per-byte VALU work is the softmax of
+// 16 columns instead of a dot product per element. Keys stream in 32-key chunks through a ring
+// of NS LDS stages filled by asynchronous global->LDS copies (16 bytes per lane, no VGPRs): the
+// copy of chunk c + NS - 1 is issued before chunk c is computed, so NS - 1 chunks per wave are
+// in flight while the matrix cores work. A single wave needs no barrier: it waits (vmcnt) for
+// its own copies, and a stage is refilled only after the wave's reads of it have completed.
+constexpr int kDecT = 32;       // keys per chunk / ring stage
+constexpr int kDecStages = 2;   // ring depth: one chunk in flight while the wave computes one
+constexpr int kDecPerCU = 4;    // resident single-wave workgroups per CU the grid is sized for
+
+// One asynchronous copy, 16 bytes per lane: lane i's bytes at gsrc land at LDS lds_dst + 16 i
+// (lds_dst wave-uniform, in M0). Issued as inline assembly so that the compiler does not track
+// it (it would otherwise wait for every copy before any LDS read); the kernel waits itself.
+__device__ __forceinline__ void dma16(const void* gsrc, const void* lds_dst) {
+    const uint32_t base = (uint32_t)(uintptr_t)(const tile::LDS_AS_T*)lds_dst;
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "{m0}"(base) : "memory");
+}
+
+// Wait until at most Y of this wave's newest copy groups (kCopies copies each) are in flight.
+template <int kCopies>
+__device__ __forceinline__ void wait_copies_younger(int y) {
+    switch (y) {
+        case 0: asm volatile("s_waitcnt vmcnt(0)" : : : "memory"); break;
+        case 1: asm volatile("s_waitcnt vmcnt(%0)" : : "n"(kCopies) : "memory"); break;
+        case 2: asm volatile("s_waitcnt vmcnt(%0)" : : "n"(2 * kCopies) : "memory"); break;
+        default: asm volatile("s_waitcnt vmcnt(%0)" : : "n"(3 * kCopies) : "memory"); break;
+    }
+}
+
+// Copy keys [k0, k0 + kDecT) of one head (rows past N re-read key N-1; they are masked) into a
+// ring stage, 16-byte chunks of a row XOR-swizzled as the tile reads expect.
+template <int D>
+__device__ __forceinline__ void load_stage(const uint16_t* __restrict__ head, int k0, int N, uint16_t* stage,
+                                           int lane) {
+    constexpr int CPR = D / 8;
+    constexpr int NI = kDecT * CPR / 64;
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        const int p = j * 64 + lane;
+        const int r = p / CPR;
+        const int lc = (p % CPR) ^ tile::swz<D>(r);
+        const int key = min(k0 + r, N - 1);
+        dma16(head + (size_t)key * D + lc * 8, stage + j * 64 * 8);
+    }
+}
+
+template <int D, bool kBf16, int NS>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void decode_mfma(DecodeArgs a) {
+    static_assert(NS >= 2 && NS <= 4, "ring depth");
+    constexpr int ND = D / 32, NDT = D / 16;
+    constexpr int kStage = kDecT * D;                 // elements per K (or V) stage
+    constexpr int kCopies = 2 * kDecT * (D / 8) / 64;  // copies per stage (K and V)
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[NS * kStage];
+    __shared__ __attribute__((aligned(16))) uint16_t v_lds[NS * kStage];
+
+    const int lane = (int)threadIdx.x;
+    const int li = lane & 15, g = lane >> 4;
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y / a.HB;                // HB = head groups of 16 per kv head
+    const int sub = blockIdx.y % a.HB;
     const int b = blockIdx.z;
-    const int qh0 = kvh * a.G + sub * HB;
-    const int row = (int)lane / LPK, c = (int)lane % LPK;
+    const int qh0 = kvh * a.G + sub * 16;
+    const int nrows = min(16, a.G - sub * 16);
 
-    const int kbeg = wave_split * a.KPW;
+    const int kbeg = split * a.KPW;
     const int kend = min(a.N, kbeg + a.KPW);
+    const int nch = (kend - kbeg + kDecT - 1) / kDecT;
     const size_t head_off = ((size_t)b * a.nKVH + kvh) * (size_t)a.stride * D;
-    const uint16_t* Kh = (const uint16_t*)a.K + head_off + c * 8;
-    const uint16_t* Vh = (const uint16_t*)a.V + head_off + c * 8;
+    const uint16_t* Kh = (const uint16_t*)a.K + head_off;
+    const uint16_t* Vh = (const uint16_t*)a.V + head_off;
 
-    u32x4 q[HB];
+    // Query heads as B operands: lane holds q[head qh0 + li][32c + 8g .. +8], zero past the group.
+    u32x4 qb[1][ND];
 #pragma unroll
-    for (int h = 0; h < HB; ++h)
-        q[h] = *(const u32x4*)((const uint16_t*)a.q + ((size_t)b * a.nQH + qh0 + h) * D + c * 8);
+    for (int c = 0; c < ND; ++c) {
+        qb[0][c] = u32x4{0u, 0u, 0u, 0u};
+        if (li < nrows)
+            qb[0][c] = *(const u32x4*)((const uint16_t*)a.q + ((size_t)b * a.nQH + qh0 + li) * D + c * 32 + g * 8);
+        asm volatile("" : : "v"(qb[0][c]));   // the loads complete before the first copy is issued
+    }
+    f32x4 o[1][NDT], lacc[1];
+    float m[1] = {tile::kInitM};
+    lacc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < NDT; ++d) o[0][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const tile::LdsOffsets off = tile::lds_offsets<D>(li, g);
 
-    float m[HB], l[HB], o[HB][8];
 #pragma unroll
-    for (int h = 0; h < HB; ++h) {
-        m[h] = -INFINITY; l[h] = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+    for (int i = 0; i < NS - 1; ++i)
+        if (i < nch) {
+            load_stage<D>(Kh, kbeg + i * kDecT, a.N, k_lds + i * kStage, lane);
+            load_stage<D>(Vh, kbeg + i * kDecT, a.N, v_lds + i * kStage, lane);
+        }
+    int st = 0;   // stage of chunk ch
+    for (int ch = 0; ch < nch; ++ch) {
+        const int ahead = ch + NS - 1;
+        if (ahead < nch) {
+            const int sa = (st == 0) ? NS - 1 : st - 1;   // stage of chunk ch - 1, already consumed
+            load_stage<D>(Kh, kbeg + ahead * kDecT, a.N, k_lds + sa * kStage, lane);
+            load_stage<D>(Vh, kbeg + ahead * kDecT, a.N, v_lds + sa * kStage, lane);
+        }
+        wait_copies_younger<kCopies>(min(NS - 1, nch - 1 - ch));
+        const char* Kt = (const char*)(k_lds + st * kStage);
+        const char* Vt = (const char*)(v_lds + st * kStage);
+        const int kb = kbeg + ch * kDecT;
+        f32x4 s[1][2];
+        tile::qk_chunk<D, 1, kBf16>(Kt, off, qb, s, 0);
+        float lm[1];
+        const bool need = (kb + kDecT > kend)
+            ? tile::check_chunk<1, true>(s, m, lm, kb, 0, kend, 0, a.sc, li, g)
+            : tile::check_chunk<1, false>(s, m, lm, kb, 0, kend, 0, a.sc, li, g);
+        if (__builtin_amdgcn_ballot_w64(need)) tile::rescale_rows<D, 1>(lm, m, o, lacc, a.sc);
+        u32x4 pb[1];
+        tile::softmax_chunk<1, kBf16>(s, m, pb, a.sc);
+        tile::pv_chunk<D, 1, kBf16>(Vt, off, pb, o, lacc, 0);
+        st = (st == NS - 1) ? 0 : st + 1;
     }
 
-    for (int k0 = kbeg; k0 < kend; k0 += KPL * kDecodeU) {
-        u32x4 kv[kDecodeU], vv[kDecodeU];
-        bool valid[kDecodeU];
+    // Partial (m, l, O) of each head of the group: lane holds O^T[16dt + 4g + e][head li].
+    if (li < nrows) {
+        const size_t pidx = ((size_t)b * a.nQH + qh0 + li) * a.P + split;
+        float* dst = a.part_o + pidx * D + g * 4;
 #pragma unroll
-        for (int j = 0; j < kDecodeU; ++j) {
-            const int key = k0 + row + KPL * j;
-            valid[j] = key < kend;
-            const int kk = valid[j] ? key : kbeg;     // in-bounds address for masked rows
-            kv[j] = __builtin_nontemporal_load((const u32x4*)(Kh + (size_t)kk * D));
-            vv[j] = __builtin_nontemporal_load((const u32x4*)(Vh + (size_t)kk * D));
-        }
-        float s[kDecodeU][HB];
-#pragma unroll
-        for (int j = 0; j < kDecodeU; ++j) {
-#pragma unroll
-            for (int h = 0; h < HB; ++h) {
-                float t = dot2<kBf16>(q[h][0], kv[j][0], 0.f);
-                t = dot2<kBf16>(q[h][1], kv[j][1], t);
-                t = dot2<kBf16>(q[h][2], kv[j][2], t);
-                t = dot2<kBf16>(q[h][3], kv[j][3], t);
-                t = keyrow_sum<D>(t);
-                s[j][h] = valid[j] ? t * a.sc : -INFINITY;
-            }
-        }
-        float vf[kDecodeU][8];
-#pragma unroll
-        for (int j = 0; j < kDecodeU; ++j) unpack8<kBf16>(vv[j], vf[j]);
-#pragma unroll
-        for (int h = 0; h < HB; ++h) {
-            float mx = s[0][h];
-#pragma unroll
-            for (int j = 1; j < kDecodeU; ++j) mx = fmaxf(mx, s[j][h]);
-            const float mnew = fmaxf(m[h], mx);
-            const float mref = (mnew == -INFINITY) ? 0.f : mnew;
-            const float alpha = exp2f(m[h] - mref);
-            float p[kDecodeU], ps = 0.f;
-#pragma unroll
-            for (int j = 0; j < kDecodeU; ++j) { p[j] = exp2f(s[j][h] - mref); ps += p[j]; }
-            l[h] = l[h] * alpha + ps;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float acc = o[h][e] * alpha;
-#pragma unroll
-                for (int j = 0; j < kDecodeU; ++j) acc = fmaf(p[j], vf[j][e], acc);
-                o[h][e] = acc;
-            }
-            m[h] = mnew;
-        }
-    }
-
-    // Merge the lane groups of this wave, then lane group 0 writes the wave's partial.
-#pragma unroll
-    for (int h = 0; h < HB; ++h) {
-        const float M = across_groups<D>(m[h], Max{});
-        const float w = (M == -INFINITY) ? 0.f : exp2f(m[h] - M);
-        const float L = across_groups<D>(l[h] * w, Sum{});
-        float ov[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ov[e] = across_groups<D>(o[h][e] * w, Sum{});
-        const size_t pidx = ((size_t)b * a.nQH + qh0 + h) * a.P + wave_split;
-        if (row == 0) {
-            float4* dst = (float4*)(a.part_o + pidx * D + c * 8);
-            dst[0] = make_float4(ov[0], ov[1], ov[2], ov[3]);
-            dst[1] = make_float4(ov[4], ov[5], ov[6], ov[7]);
-            if (c == 0) *(float2*)(a.part_ml + pidx * 2) = make_float2(M, L);
-        }
+        for (int dt = 0; dt < NDT; ++dt)
+            *(float4*)(dst + dt * 16) = make_float4(o[0][dt][0], o[0][dt][1], o[0][dt][2], o[0][dt][3]);
+        if (g == 0) *(float2*)(a.part_ml + pidx * 2) = make_float2(m[0], lacc[0][0]);
     }
 }
 
@@ -218,8 +211,25 @@ __global__ __launch_bounds__(64) void decode_merge(const float* __restrict__ par
     }
 }
 
-struct Plan { int G, HB, subgroups, KPW, P; size_t ws_bytes; };
+struct Plan { int G, HB, KPW, P; size_t ws_bytes; };
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// HB: groups of up to 16 query heads per kv head (one MFMA column block each); KPW: keys per
+// split, a multiple of the 32-key chunk, sized so that the whole grid is one round of resident
+// workgroups (kDecPerCU per CU): every workgroup streams from start to end with no second round
+// and no tail of stragglers, which measured markedly faster than many short splits.
 bool plan_decode(const cdna3_decode_cfg& c, Plan& p) {
     if (c.D != 64 && c.D != 128) return false;
     if (c.N < 1 || c.nQHeads < 1 || c.nKVHeads < 1 || c.batch < 1) return false;
@@ -227,19 +237,16 @@ bool plan_decode(const cdna3_decode_cfg& c, Plan& p) {
     const int stride = c.stride_kv == 0 ? c.N : c.stride_kv;
     if (stride < c.N) return false;
     p.G = c.nQHeads / c.nKVHeads;
-    p.HB = 1;
-    for (int hb = kMaxHeadsPerWave; hb >= 1; --hb)
-        if (p.G % hb == 0) { p.HB = hb; break; }
-    p.subgroups = p.G / p.HB;
-    const int kpl = 64 / (c.D / 8);
-    const int step = kpl * kDecodeU;
-    const double rows = (double)c.batch * c.nKVHeads * p.subgroups;
-    long long kpw = (long long)ceil((double)c.N * rows / kTargetWaves);
-    if (kpw < 2 * step) kpw = 2 * step;
-    kpw = (kpw + step - 1) / step * step;
-    if (kpw > c.N) kpw = ((long long)c.N + step - 1) / step * step;
+    p.HB = (p.G + 15) / 16;
+    const double rows = (double)c.batch * c.nKVHeads * p.HB;
+    const double slots = (double)device_cus() * kDecPerCU;
+    long long kpw = (long long)ceil((double)c.N * rows / slots);
+    if (kpw < 4 * kDecT) kpw = 4 * kDecT;
+    kpw = (kpw + kDecT - 1) / kDecT * kDecT;
+    if (kpw > c.N) kpw = ((long long)c.N + kDecT - 1) / kDecT * kDecT;
     p.KPW = (int)kpw;
     p.P = (int)((c.N + kpw - 1) / kpw);
+    if (p.P > 65535) return false;
     p.ws_bytes = (size_t)c.batch * c.nQHeads * p.P * (size_t)(c.D + 2) * sizeof(float) + 256;
     return true;
 }
@@ -255,18 +262,10 @@ int launch_decode(const cdna3_decode_cfg& c, const Plan& p, const void* q, const
     a.N = c.N; a.nQH = c.nQHeads; a.nKVH = c.nKVHeads; a.stride = c.stride_kv == 0 ? c.N : c.stride_kv;
     a.G = p.G; a.HB = p.HB; a.KPW = p.KPW; a.P = p.P;
     a.sc = kLog2e / sqrtf((float)D);
-    dim3 grid(ceil_div(p.P, kDecodeWaves), c.nKVHeads * p.subgroups, c.batch);
-    switch (p.HB) {
-        case 1: decode_partial<D, 1, kBf16><<<grid, 256, 0, s>>>(a); break;
-        case 2: decode_partial<D, 2, kBf16><<<grid, 256, 0, s>>>(a); break;
-        case 3: decode_partial<D, 3, kBf16><<<grid, 256, 0, s>>>(a); break;
-        case 4: decode_partial<D, 4, kBf16><<<grid, 256, 0, s>>>(a); break;
-        case 5: decode_partial<D, 5, kBf16><<<grid, 256, 0, s>>>(a); break;
-        case 6: decode_partial<D, 6, kBf16><<<grid, 256, 0, s>>>(a); break;
-        case 7: decode_partial<D, 7, kBf16><<<grid, 256, 0, s>>>(a); break;
-        case 8: decode_partial<D, 8, kBf16><<<grid, 256, 0, s>>>(a); break;
-        default: return CDNA4_ERR_INVALID_VALUE;
-    }
+    const long long gy = (long long)c.nKVHeads * p.HB;
+    if (gy > 65535 || c.batch > 65535) return CDNA4_ERR_INVALID_VALUE;
+    dim3 grid((unsigned)p.P, (unsigned)gy, (unsigned)c.batch);
+    decode_mfma<D, kBf16, kDecStages><<<grid, 64, 0, s>>>(a);
     decode_merge<D, kBf16><<<(unsigned)((size_t)c.batch * c.nQHeads), 64, 0, s>>>(a.part_ml, a.part_o, o, p.P);
     return launch_status();
 }

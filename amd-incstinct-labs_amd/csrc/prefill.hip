@@ -26,9 +26,7 @@
 //     of a (batch, head) on the same XCD so its K/V stay in that XCD's L2.
 // The fp32 kernel (fa_f32) is a plain VALU kernel for the fp32 arm of the reference
 // configuration (fp32 in and out, accuracy 1e-4).
-#include "common.hpp"
-#include "wave_primitives/detail/xlane.hpp"
-#include <math.h>
+#include "attn_tile.hpp"
 
 namespace cdna4 {
 namespace {
@@ -38,54 +36,8 @@ using wave::xlane::cross_row_allreduce;
 using wave::xlane::Max;
 using wave::xlane::Sum;
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-#define LDS_AS __attribute__((address_space(3)))
-
-constexpr float kLog2e = 1.4426950408889634f;
+using namespace tile;
 constexpr int kBc = 64;       // keys per K/V tile
-
-
-template <bool kBf16>
-__device__ __forceinline__ f32x4 mfma(const u32x4& a, const u32x4& b, const f32x4& c) {
-    if constexpr (kBf16)
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-    else
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
-
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-// Two fp32 values -> one dword of two 16-bit values, round to nearest even
-// (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 on gfx950).
-template <bool kBf16>
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-    const f32x2 v = {a, b};
-    if constexpr (kBf16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
-    else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
-}
-
-// XOR swizzle of the 16-byte chunks of key row r inside a K/V tile. Requirements:
-//   * K operand reads (ds_read_b128): the 16 rows one lane group reads, r = 8*(m/4) + 4u + m%4
-//     (bits 0, 1, 3, 4 vary), land on 16 different chunk positions;
-//   * V^T operand reads (ds_read_b64_tr_b16): a lane group reads rows 8g + x (x = 0..3) at two
-//     adjacent chunks; the 4 rows must land on distinct chunk pairs, and lane groups g, g+1 (one
-//     32-lane LDS pass) on different 128-byte halves.
-// D = 128 (16 chunks per 256-byte row): bit 0 <- r4, bits 1-2 <- r0-r1, bit 3 <- r3.
-// D = 64 (8 chunks per 128-byte row, two rows per 256-byte bank window): bit 0 <- r4,
-// bit 1 <- r1, bit 2 <- r3.
-template <int D>
-__device__ __forceinline__ int swz(int r) {
-    if constexpr (D == 128)
-        return ((r >> 4) & 1) | ((r & 3) << 1) | (((r >> 3) & 1) << 3);
-    else
-        return ((r >> 4) & 1) | (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
-}
 
 struct PrefillArgs {
     const uint16_t* Q; const uint16_t* K; const uint16_t* V; uint16_t* O;
@@ -112,38 +64,6 @@ __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ head, int
         __builtin_amdgcn_global_load_lds((const void*)(head + (size_t)key * D + lc * 8),
                                          (LDS_AS void*)(tile + p0 * 8), 16, 0, 0);
     }
-}
-
-// Softmax reference maxima are refreshed only when a new maximum exceeds them by more than
-// kTau (base-2 units): p = 2^(s - m) then stays <= 2^kTau, and O and l, accumulated against the
-// same reference, give the exact O / l; most tiles skip the rescale of O entirely.
-constexpr float kTau = 8.f;
-// Initial reference maximum: finite, so no -inf - -inf can arise; the first chunk with a visible
-// key always exceeds it by more than kTau and replaces it (alpha = 2^(kInitM - m) = 0), and masked
-// scores (-inf) give p = 0 against it.
-constexpr float kInitM = -1e30f;
-
-// Per-lane byte offsets of the LDS operand reads within one K or V tile. The swizzle of a row
-// depends only on bits 0, 1, 3, 4 of its index, which come from the lane alone, so the offsets of
-// every sub-tile u, key chunk kc and (for V) row r + 4 differ from these by a compile-time
-// constant (folded into the ds_read immediate). Within a row, d chunk c of the K operand sits at
-// k ^ (c << 6) and d tile dt of the V^T operand at v ^ (dt << 5): the chunk index occupies offset
-// bits that the row base and the swizzled low bits do not touch.
-struct LdsOffsets {
-    uint32_t k;   // K operand: d chunk 0, sub-tile 0, key chunk 0
-    uint32_t v;   // first V^T transpose read: d tile 0, key chunk 0
-    __device__ __forceinline__ uint32_t kc(int c) const { return k ^ ((uint32_t)c << 6); }
-    __device__ __forceinline__ uint32_t vd(int dt) const { return v ^ ((uint32_t)dt << 5); }
-};
-
-template <int D>
-__device__ __forceinline__ LdsOffsets lds_offsets(int li, int g) {
-    LdsOffsets off;
-    const int rk = (li >> 2) * 8 + (li & 3);                 // K row of A-row li, sub-tile 0
-    off.k = (uint32_t)(rk * D + ((g ^ swz<D>(rk)) * 8)) * 2u;
-    const int rv = g * 8 + (li >> 2);                        // V row of the first transpose read
-    off.v = (uint32_t)(rv * D + ((((li & 3) >> 1) ^ swz<D>(rv)) * 8) + (li & 1) * 4) * 2u;
-    return off;
 }
 
 // One 32-key half (kc) of a K/V tile: S^T MFMAs, masking, lazy rescale, P, P.V MFMAs.
