@@ -130,16 +130,34 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_stage1(const void* __re
     if ((threadIdx.x & 63u) == 0) ((Acc*)part_)[blockIdx.x * (kReduceThreads / 64) + threadIdx.x / 64] = a;
 }
 
+// Stage 2: 16 waves fold the partials with independent loads in flight (one memory round trip
+// instead of a dependent chain), each wave writes one value after the partials, and after the
+// workgroup barrier wave 0 folds those 16. Deterministic order, no LDS.
+constexpr int kReduce2Threads = 1024;
+
 template <int DT, class Op>
-__global__ __launch_bounds__(64) void reduce_stage2(const void* __restrict__ part_, int count,
-                                                     void* __restrict__ out_) {
+__global__ __launch_bounds__(kReduce2Threads) void reduce_stage2(void* __restrict__ part_, int count,
+                                                                  void* __restrict__ out_) {
     using Acc = typename Elem<DT>::Acc;
-    const Acc* part = (const Acc*)part_;
+    Acc* part = (Acc*)part_;
     Op op;
-    Acc a = Op::template identity<Acc>();
-    for (int i = threadIdx.x; i < count; i += 64) a = op(a, part[i]);
-    a = allreduce(a, op);
-    if (threadIdx.x == 0) *(Acc*)out_ = a;
+    const Acc id = Op::template identity<Acc>();
+    Acc acc[4] = {id, id, id, id};
+    int i = threadIdx.x;
+    for (; i + 3 * kReduce2Threads < count; i += 4 * kReduce2Threads) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[u] = op(acc[u], part[i + u * kReduce2Threads]);
+    }
+    for (; i < count; i += kReduce2Threads) acc[0] = op(acc[0], part[i]);
+    Acc a = allreduce(op(op(acc[0], acc[1]), op(acc[2], acc[3])), op);
+    Acc* wave_vals = part + count;   // kReduce2Threads / 64 slots after the partials
+    if ((threadIdx.x & 63u) == 0) wave_vals[threadIdx.x >> 6] = a;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        Acc v = (threadIdx.x < kReduce2Threads / 64) ? wave_vals[threadIdx.x] : id;
+        v = allreduce(v, op);
+        if (threadIdx.x == 0) *(Acc*)out_ = v;
+    }
 }
 
 unsigned reduce_blocks(size_t n, int vec) {
@@ -159,21 +177,30 @@ int reduce_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) 
         reduce_stage1<DT, Op, true><<<blocks, kReduceThreads, 0, s>>>(in, n, ws);
     else
         reduce_stage1<DT, Op, false><<<blocks, kReduceThreads, 0, s>>>(in, n, ws);
-    reduce_stage2<DT, Op><<<1, 64, 0, s>>>(ws, (int)(blocks * (kReduceThreads / 64)), out);
+    reduce_stage2<DT, Op><<<1, kReduce2Threads, 0, s>>>(ws, (int)(blocks * (kReduceThreads / 64)), out);
     return launch_status();
 }
 
 // ---- scan (decoupled look-back, single-wave workgroups) ------------------------------
 template <int DT> struct ScanTile { static constexpr int U = (Elem<DT>::VEC == 8) ? 8 : 16; };
 
+// Per-tile look-back state. A tile publishes its aggregate into agg and, once known, its inclusive
+// prefix into pre. Every 64-bit word carries a tag in its upper half (1 = aggregate, 2 = prefix)
+// and 32 value bits in its lower half; 64-bit values use two words (low, high half), and a reader
+// accepts a slot only when all its words carry the tag, so a torn read is just "not ready". Value
+// and tag travel in one atomic word, so relaxed device-scope atomics suffice: no release/acquire
+// fences, which on this multi-XCD part would write back / invalidate the L2 on every publish and
+// every poll.
 struct ScanState {
-    uint32_t* flag;   // per tile: 0 = nothing, 1 = aggregate published, 2 = prefix published
-    uint64_t* agg;    // per tile: aggregate bits
-    uint64_t* pre;    // per tile: inclusive prefix bits
+    uint64_t* agg;    // per tile: NW words
+    uint64_t* pre;    // per tile: NW words
     uint32_t* error;  // set when a look-back wait exceeds its bound
 };
 
 constexpr uint32_t kSpinLimit = 1u << 22;
+constexpr uint64_t kTagAgg = 1, kTagPre = 2;
+
+template <typename Acc> struct Words { static constexpr int NW = sizeof(Acc) / 4; };
 
 template <typename Acc> __device__ __forceinline__ uint64_t to_bits(Acc v) {
     if constexpr (sizeof(Acc) == 4) return (uint64_t)__builtin_bit_cast(uint32_t, v);
@@ -184,22 +211,49 @@ template <typename Acc> __device__ __forceinline__ Acc from_bits(uint64_t b) {
     else return __builtin_bit_cast(Acc, b);
 }
 
-__global__ __launch_bounds__(256) void scan_clear_flags(uint32_t* flag, size_t ntiles, uint32_t* error) {
+__device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_word(uint64_t* p, uint64_t w) {
+    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ __launch_bounds__(256) void scan_clear(uint64_t* words, size_t nwords, uint32_t* error) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < ntiles) flag[i] = 0u;
+    if (i < nwords) words[i] = 0ull;
     if (i == 0) *error = 0u;
 }
 
+// Lanes 0 .. NW-1 each write one word of tile t's slot.
 template <typename Acc>
-__device__ __forceinline__ void publish(const ScanState& st, size_t t, Acc v, uint32_t status) {
-    if (threadIdx.x == 0) {
-        uint64_t* slot = (status == 1u) ? st.agg + t : st.pre + t;
-        __hip_atomic_store(slot, to_bits(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(st.flag + t, status, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void publish(uint64_t* slots, size_t t, Acc v, uint64_t tag) {
+    constexpr int NW = Words<Acc>::NW;
+    const unsigned lane = threadIdx.x;
+    if (lane < (unsigned)NW) {
+        const uint64_t bits = to_bits(v);
+        const uint32_t half = (uint32_t)(lane == 0 ? bits : bits >> 32);
+        st_word(slots + t * NW + lane, (tag << 32) | half);
     }
 }
 
-// Combined value of all tiles before `tile`, on every lane.
+// Reads tile t's slot: true and the value when every word carries the tag.
+template <typename Acc>
+__device__ __forceinline__ bool read_slot(const uint64_t* slots, long long t, uint64_t tag, Acc& v) {
+    constexpr int NW = Words<Acc>::NW;
+    const uint64_t w0 = ld_word(slots + t * NW);
+    uint64_t bits = (uint32_t)w0;
+    bool ok = (w0 >> 32) == tag;
+    if constexpr (NW == 2) {
+        const uint64_t w1 = ld_word(slots + t * NW + 1);
+        ok = ok && (w1 >> 32) == tag;
+        bits |= (uint64_t)(uint32_t)w1 << 32;
+    }
+    v = from_bits<Acc>(bits);
+    return ok;
+}
+
+// Combined value of all tiles before `tile`, on every lane. Lane i examines tile pos - i; the
+// window moves back 64 tiles at a time until it contains a published prefix.
 template <typename Acc, class Op>
 __device__ Acc look_back(const ScanState& st, size_t tile, Op op) {
     const unsigned lane = threadIdx.x;
@@ -208,10 +262,17 @@ __device__ Acc look_back(const ScanState& st, size_t tile, Op op) {
     long long pos = (long long)tile - 1;
     while (true) {
         const long long t = pos - (long long)lane;
-        uint32_t s = 2u;
+        Acc v = id;
+        uint32_t s = 2u;                 // lanes before tile 0 act as an (identity) prefix
         uint64_t mzero = 0, mpre = 0;
         for (uint32_t spin = 0;; ++spin) {
-            s = (t >= 0) ? __hip_atomic_load(st.flag + t, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) : 2u;
+            if (t >= 0) {
+                Acc pv, av;
+                const bool p = read_slot<Acc>(st.pre, t, kTagPre, pv);
+                const bool q = read_slot<Acc>(st.agg, t, kTagAgg, av);
+                s = p ? 2u : (q ? 1u : 0u);
+                v = p ? pv : (q ? av : id);
+            }
             mpre = __ballot(s == 2u);
             mzero = __ballot(s == 0u);
             const uint64_t below = mpre ? ((mpre & (~mpre + 1ull)) - 1ull) : ~0ull;  // lanes before first prefix
@@ -223,12 +284,7 @@ __device__ Acc look_back(const ScanState& st, size_t tile, Op op) {
             __builtin_amdgcn_s_sleep(1);
         }
         const int first_pre = mpre ? __builtin_ctzll(mpre) : 64;
-        Acc v = id;
-        if ((int)lane < first_pre && s == 1u) {
-            v = from_bits<Acc>(__hip_atomic_load(st.agg + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        } else if ((int)lane == first_pre && t >= 0) {
-            v = from_bits<Acc>(__hip_atomic_load(st.pre + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        }
+        if ((int)lane > first_pre || (t < 0 && (int)lane != first_pre)) v = id;
         acc = op(allreduce(v, op), acc);
         if (first_pre < 64) break;
         pos -= 64;
@@ -281,11 +337,11 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
     const Acc tile_total = run;
     Acc excl = id;
     if (tile == 0) {
-        publish(st, tile, tile_total, 2u);
+        publish(st.pre, tile, tile_total, kTagPre);
     } else {
-        publish(st, tile, tile_total, 1u);
+        publish(st.agg, tile, tile_total, kTagAgg);
         excl = look_back<Acc>(st, tile, op);
-        publish(st, tile, op(excl, tile_total), 2u);
+        publish(st.pre, tile, op(excl, tile_total), kTagPre);
     }
 #pragma unroll
     for (int j = 0; j < U; ++j) {
@@ -327,24 +383,25 @@ size_t scan_ntiles(size_t n, int dtype) {
     }
 }
 
-// Workspace layout: [error:u32 pad to 256][flag: ntiles u32, pad 256][agg: ntiles u64][pre: ntiles u64]
+// Workspace layout: [error: u32, padded to 256 B][agg: ntiles x 2 words][pre: ntiles x 2 words]
+// (64-bit values use both words of a tile, 32-bit values the first).
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-size_t scan_ws_bytes(size_t ntiles) {
-    return 256 + align256(ntiles * 4) + align256(ntiles * 8) * 2;
-}
+size_t scan_ws_bytes(size_t ntiles) { return 256 + 2 * align256(ntiles * 16); }
 
 template <int DT, class Op>
 int scan_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
+    using Acc = typename Elem<DT>::Acc;
     const size_t ntiles = scan_tiles_for<DT>(n);
     if (ntiles == 0) return 0;
     if (ntiles > 0x7fffffffull) return CDNA4_ERR_INVALID_VALUE;
     char* w = (char*)ws;
     ScanState st;
     st.error = (uint32_t*)w;
-    st.flag = (uint32_t*)(w + 256);
-    st.agg = (uint64_t*)(w + 256 + align256(ntiles * 4));
-    st.pre = (uint64_t*)(w + 256 + align256(ntiles * 4) + align256(ntiles * 8));
-    scan_clear_flags<<<ceil_div(ntiles, 256), 256, 0, s>>>(st.flag, ntiles, st.error);
+    st.agg = (uint64_t*)(w + 256);
+    st.pre = (uint64_t*)(w + 256 + align256(ntiles * 16));
+    // Both slot arrays are cleared in one pass (the pre array directly follows the agg array).
+    const size_t nwords = (align256(ntiles * 16) + ntiles * Words<Acc>::NW * 8) / 8;
+    scan_clear<<<ceil_div(nwords, 256), 256, 0, s>>>(st.agg, nwords, st.error);
     const bool vec = ((uintptr_t)in % 16) == 0 && ((uintptr_t)out % 16) == 0;
     if (vec)
         scan_tiles<DT, Op, true><<<(unsigned)ntiles, 64, 0, s>>>(in, n, out, st);
@@ -386,7 +443,7 @@ bool valid_op(int op) { return op >= CDNA4_OP_SUM && op <= CDNA4_OP_MIN; }
 using namespace cdna4;
 
 extern "C" size_t cdna3_reduce_workspace_size(size_t /*n*/, int /*dtype*/) {
-    return (size_t)kReduceMaxBlocks * (kReduceThreads / 64) * 8;
+    return ((size_t)kReduceMaxBlocks * (kReduceThreads / 64) + kReduce2Threads / 64) * 8;
 }
 
 extern "C" int cdna3_reduce(int op, int dtype, const void* in, size_t n, void* out, void* workspace,
