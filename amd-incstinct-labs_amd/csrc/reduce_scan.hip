@@ -182,7 +182,7 @@ int reduce_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) 
 }
 
 // ---- scan (decoupled look-back, single-wave workgroups) ------------------------------
-template <int DT> struct ScanTile { static constexpr int U = (Elem<DT>::VEC == 8) ? 8 : 16; };
+template <int DT> struct ScanTile { static constexpr int U = (Elem<DT>::VEC == 8) ? 12 : 24; };   // 16-byte loads per lane (tile = 64 U 16 B)
 
 // Per-tile look-back state. A tile publishes its aggregate into agg and, once known, its inclusive
 // prefix into pre. Every 64-bit word carries a tag in its upper half (1 = aggregate, 2 = prefix)

@@ -7,8 +7,10 @@ cdna3_attn_prefill launch over the whole batch, inputs resident in HBM.
 Also reported in the same line:
   decode: BASELINE config 4 (batch 32, 32 q heads / 8 kv heads, D 128, N 8192 fp16) in GB/s of
           algorithmic KV + q/o bytes, with its HBM roofline fraction;
-  dpp:    BASELINE config 2 sample (device-wide f32 reduce_sum and inclusive scan_sum over 2^26
-          elements, four rotating inputs so the 256 MB Infinity Cache cannot serve repeats) in GB/s;
+  dpp:    BASELINE config 2 (device-wide reduce_{sum,max,min} and inclusive scan_sum over 2^26
+          elements of f32, f64, i32, i64, f16, bf16, rotating >= 1 GiB of inputs so the 256 MB
+          Infinity Cache cannot serve repeats) in GB/s of algorithmic bytes;
+  cfg1:   BASELINE config 1, the reference's FA2 configuration, fp32 and fp16 arms;
   copy_1GiB: a plain device copy, the achievable-bandwidth reference and the known-size kernel
           that calibrates the HBM traffic counters.
 Kernel durations come from HIP events recorded on the stream the kernels run on (torch's current
@@ -29,6 +31,7 @@ sys.path.insert(0, os.path.join(ROOT, "amd-incstinct-labs_amd"))
 METRIC = "FA prefill TFLOPS (% MFMA peak) + decode KV GB/s (% HBM peak), D=64/128"
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+PEAK_FP32_TFLOPS = 157.3      # MI355X fp32
 
 
 def parse():
@@ -37,7 +40,7 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["all", "prefill", "decode", "dpp", "copy"], default="all")
+    p.add_argument("--only", choices=["all", "prefill", "decode", "dpp", "cfg1", "copy"], default="all")
     return p.parse_args()
 
 
@@ -127,22 +130,62 @@ def bench_decode(torch, cdna4, steps, warmup):
 
 
 def bench_dpp(torch, cdna4, steps, warmup):
+    """device-wide reduce_{sum,max,min} and inclusive scan_sum over n = 2^26
+    elements of each dtype (floats U(-1,1), integers uniform on [-1000, 1000]; fp16/bf16 accumulate
+    and scan into fp32). Inputs rotate over >= 1 GiB of buffers so the 256 MB Infinity Cache cannot
+    serve repeats. Algorithmic bytes: reduce n*sizeof(in); scan n*sizeof(in) + n*sizeof(out)."""
     n = 1 << 26
     g = torch.Generator(device="cuda").manual_seed(2)
-    xs = [torch.rand(n, device="cuda", generator=g) * 2 - 1 for _ in range(4)]
-    out1 = torch.empty(1, device="cuda")
-    outn = torch.empty(n, device="cuda")
-    wr = torch.empty(cdna4.reduce_workspace_size(n, cdna4.F32), dtype=torch.uint8, device="cuda")
-    wsn = torch.empty(cdna4.scan_workspace_size(n, cdna4.F32), dtype=torch.uint8, device="cuda")
-    r_ms, _ = time_launches(torch, lambda i=0: cdna4.reduce(xs[i % 4], "sum", out=out1, workspace=wr), steps, warmup)
-    s_ms, _ = time_launches(torch, lambda i=0: cdna4.scan_inclusive(xs[i % 4], "sum", out=outn, workspace=wsn),
-                            steps, warmup)
-    rb, sb = 4.0 * n, 8.0 * n
-    return {"reduce_sum_f32": {"value": rb / (r_ms * 1e-3) / 1e9, "unit": "GB/s", "avg_us": r_ms * 1e3,
-                               "frac": rb / (r_ms * 1e-3) / 1e9 / PEAK_HBM_GBS},
-            "scan_inclusive_sum_f32": {"value": sb / (s_ms * 1e-3) / 1e9, "unit": "GB/s", "avg_us": s_ms * 1e3,
-                                       "frac": sb / (s_ms * 1e-3) / 1e9 / PEAK_HBM_GBS},
-            "config": {"workload": "BASELINE config 2 sample: f32, n = 2^26, 4 rotating inputs"}}
+    dtypes = [("f32", torch.float32), ("f64", torch.float64), ("i32", torch.int32), ("i64", torch.int64),
+              ("f16", torch.float16), ("bf16", torch.bfloat16)]
+    result = {"config": {"workload": "BASELINE config 2: n = 2^26 per dtype, >= 1 GiB of rotating inputs"}}
+    for name, dt in dtypes:
+        esize = torch.empty(0, dtype=dt).element_size()
+        nbuf = max(2, (1 << 30) // (n * esize))
+        if dt.is_floating_point:
+            xs = [(torch.rand(n, device="cuda", generator=g) * 2 - 1).to(dt) for _ in range(nbuf)]
+        else:
+            xs = [torch.randint(-1000, 1001, (n,), device="cuda", generator=g, dtype=dt) for _ in range(nbuf)]
+        acc = torch.float32 if dt in (torch.float16, torch.bfloat16) else dt
+        osize = torch.empty(0, dtype=acc).element_size()
+        out1 = torch.empty(1, device="cuda", dtype=acc)
+        outn = torch.empty(n, device="cuda", dtype=acc)
+        code = cdna4._TORCH_DTYPES[dt]
+        wr = torch.empty(cdna4.reduce_workspace_size(n, code), dtype=torch.uint8, device="cuda")
+        wsn = torch.empty(cdna4.scan_workspace_size(n, code), dtype=torch.uint8, device="cuda")
+        entry = {}
+        for op in ("sum", "max", "min"):
+            ms, _ = time_launches(torch, lambda i=0, op=op: cdna4.reduce(xs[i % nbuf], op, out=out1, workspace=wr),
+                                  steps, warmup)
+            gbs = n * esize / (ms * 1e-3) / 1e9
+            entry[f"reduce_{op}"] = {"GBs": round(gbs, 1), "us": round(ms * 1e3, 2), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        ms, _ = time_launches(torch, lambda i=0: cdna4.scan_inclusive(xs[i % nbuf], "sum", out=outn, workspace=wsn),
+                              steps, warmup)
+        gbs = n * (esize + osize) / (ms * 1e-3) / 1e9
+        entry["scan_sum"] = {"GBs": round(gbs, 1), "us": round(ms * 1e3, 2), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        result[name] = entry
+        del xs, outn
+        torch.cuda.empty_cache()
+    return result
+
+
+def bench_cfg1(torch, cdna4, steps, warmup):
+    """BASELINE config 1 (the reference's FA2 configuration): B1, H8, S512, D64, non-causal;
+    fp32 arm (fp32 in/out, VALU kernel) and fp16 arm (MFMA kernel). 4*B*H*S^2*D FLOP."""
+    B, H, S, D = 1, 8, 512, 64
+    flop = 4.0 * B * H * S * S * D
+    g = torch.Generator(device="cuda").manual_seed(42)
+    out = {"config": {"workload": "FA2 reference config (BASELINE config 1)", "batch": B, "heads": H, "seq_len": S,
+                      "head_dim": D, "causal": False}}
+    for name, dt, peak in (("fp32", torch.float32, PEAK_FP32_TFLOPS), ("fp16", torch.float16, PEAK_BF16_TFLOPS)):
+        Q, K, V = ((torch.rand(B, H, S, D, device="cuda", generator=g) * 2 - 1).to(dt) for _ in range(3))
+        O = torch.empty_like(Q)
+        cfg = cdna4.PrefillCfg(D, S, S, H, H, B, 0)
+        ms, _ = time_launches(torch, lambda i=0: cdna4.prefill(Q, K, V, O, cfg), steps, warmup)
+        tf = flop / (ms * 1e-3) / 1e12
+        out[name] = {"us": round(ms * 1e3, 2), "TFLOPS": round(tf, 2), "frac": round(tf / peak, 4),
+                     "peak": peak, "peak_unit": "TFLOP/s"}
+    return out
 
 
 def bench_copy(torch, steps, warmup):
@@ -182,6 +225,8 @@ def main():
                            "config": d["config"], "roofline": d["roofline"], "dtype": "fp16"})
     if args.only in ("all", "dpp"):
         result["dpp"] = bench_dpp(torch, cdna4, args.steps, args.warmup)
+    if args.only in ("all", "cfg1"):
+        result["cfg1"] = bench_cfg1(torch, cdna4, args.steps, args.warmup)
     if args.only in ("all", "copy"):
         result["copy_1GiB"] = bench_copy(torch, args.steps, args.warmup)
     if args.only in ("all", "prefill") and not args.no_cpu_baseline:
