@@ -27,6 +27,21 @@ int check_device() {
     return a == 1 ? 0 : CDNA4_ERR_INVALID_DEVICE_FUNCTION;
 }
 
+namespace {
+std::atomic<int> g_cus[kMaxDevices];
+}
+
+int device_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int n = g_cus[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        g_cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 }  // namespace cdna4
 
 extern "C" int cdna3_abi_version(void) { return CDNA4_ABI_VERSION; }

@@ -32,6 +32,9 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
 // runtime error. The answer is cached per device ordinal.
 int check_device();
 
+// Compute units of the current device (cached per device ordinal; 256 if the query fails).
+int device_cus();
+
 inline int launch_status() {
     hipError_t e = hipGetLastError();
     return (int)e;

@@ -213,19 +213,6 @@ __global__ __launch_bounds__(64) void decode_merge(const float* __restrict__ par
 
 struct Plan { int G, HB, KPW, P; size_t ws_bytes; };
 
-// Compute units of the current device (cached per device).
-int device_cus() {
-    static int cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev] = n;
-    }
-    return cus[dev];
-}
-
 // HB: groups of up to 16 query heads per kv head (one MFMA column block each); KPW: keys per
 // split, a multiple of the 32-key chunk, sized so that the whole grid is one round of resident
 // workgroups (kDecPerCU per CU): every workgroup streams from start to end with no second round

@@ -201,86 +201,93 @@ __global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
     const int wave = (int)(threadIdx.x >> 6);
     const int li = lane & 15, g = lane >> 4;
 
-    // Block -> (batch, head, q block). Workgroups are dispatched round-robin over the 8 XCDs
-    // (blockIdx % 8). With xcd_map, XCD x owns heads x, x + 8, ... and walks them one at a time,
-    // the q blocks of a head heaviest (causal) first, so the workgroups resident on an XCD share
-    // one head's K/V in that XCD's L2.
+    // Persistent grid: workgroup i takes work items i, i + gridDim.x, ... Item -> (batch, head,
+    // q block): workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8) and the grid
+    // is a multiple of 8, so item % 8 is the workgroup's XCD. With xcd_map, XCD x owns heads
+    // x, x + 8, ... and its workgroups walk one head at a time, so they share that head's K/V in
+    // the XCD's L2; within a head the q blocks go heaviest (causal) first, and the order flips
+    // for every other head so that each workgroup's total work evens out.
     const int nbh = a.batch * a.nQH;
-    int bh, qrev;
-    if (a.xcd_map) {
-        const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-        bh = (slot / a.nqb) * 8 + xcd;
-        qrev = slot % a.nqb;
-    } else {
-        bh = blockIdx.x % nbh;
-        qrev = blockIdx.x / nbh;
-    }
-    const int qblk = a.causal ? (a.nqb - 1 - qrev) : qrev;
-    const int b = bh / a.nQH, h = bh % a.nQH;
-    const int kvh = h / (a.nQH / a.nKVH);
-    const int q0 = qblk * BM;
-    const int qw0 = q0 + wave * QT * 16;   // first query row of this wave
-
-    const uint16_t* Kh = a.K + ((size_t)b * a.nKVH + kvh) * (size_t)a.seqK * D;
-    const uint16_t* Vh = a.V + ((size_t)b * a.nKVH + kvh) * (size_t)a.seqK * D;
-    const uint16_t* Qh = a.Q + ((size_t)b * a.nQH + h) * (size_t)a.seqQ * D;
-
-    // Q as B operands: lane holds Q[q = qw0 + t*16 + li][32*c + 8*g .. +8].
-    u32x4 qb[QT][ND];
-#pragma unroll
-    for (int t = 0; t < QT; ++t) {
-        const int q = min(qw0 + t * 16 + li, a.seqQ - 1);
-#pragma unroll
-        for (int c = 0; c < ND; ++c) {
-            qb[t][c] = *(const u32x4*)(Qh + (size_t)q * D + c * 32 + g * 8);
+    const int nitems = nbh * a.nqb;
+    for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+        int bh, qrev;
+        if (a.xcd_map) {
+            const int xcd = item & 7, slot = item >> 3;
+            bh = (slot / a.nqb) * 8 + xcd;
+            qrev = slot % a.nqb;
+            if ((slot / a.nqb) & 1) qrev = a.nqb - 1 - qrev;
+        } else {
+            bh = item % nbh;
+            qrev = item / nbh;
         }
-    }
+        const int qblk = a.causal ? (a.nqb - 1 - qrev) : qrev;
+        const int b = bh / a.nQH, h = bh % a.nQH;
+        const int kvh = h / (a.nQH / a.nKVH);
+        const int q0 = qblk * BM;
+        const int qw0 = q0 + wave * QT * 16;   // first query row of this wave
 
-    f32x4 o[QT][NDT], lacc[QT];
-    float m[QT];
+        const uint16_t* Kh = a.K + ((size_t)b * a.nKVH + kvh) * (size_t)a.seqK * D;
+        const uint16_t* Vh = a.V + ((size_t)b * a.nKVH + kvh) * (size_t)a.seqK * D;
+        const uint16_t* Qh = a.Q + ((size_t)b * a.nQH + h) * (size_t)a.seqQ * D;
+
+        // Q as B operands: lane holds Q[q = qw0 + t*16 + li][32*c + 8*g .. +8].
+        u32x4 qb[QT][ND];
 #pragma unroll
-    for (int t = 0; t < QT; ++t) {
-        m[t] = kInitM;
-        lacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < QT; ++t) {
+            const int q = min(qw0 + t * 16 + li, a.seqQ - 1);
 #pragma unroll
-        for (int d = 0; d < NDT; ++d) {
-            o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-
-    const LdsOffsets off = lds_offsets<D>(li, g);
-    int ntiles = (a.seqK + kBc - 1) / kBc;
-    if (a.causal) ntiles = min(ntiles, (min(q0 + BM, a.seqQ) - 1) / kBc + 1);
-    const int wave_qmax = min(qw0 + QT * 16, a.seqQ) - 1;   // last real query of this wave
-
-    load_tile<D, W>(Kh, 0, a.seqK, lds[0][0], wave, lane);
-    load_tile<D, W>(Vh, 0, a.seqK, lds[0][1], wave, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
-    for (int it = 0; it < ntiles; ++it) {
-        const int buf = it & 1;
-        tile_step<D, W, QT, kBf16>(lds[buf][0], lds[buf][1], lds[buf ^ 1][0], lds[buf ^ 1][1], it + 1 < ntiles, Kh, Vh,
-                                   it * kBc, wave_qmax, a, off, qb, o, m, lacc, qw0, wave, lane, li, g);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-    }
-
-    // ---- O = O^T / l: lane holds d = 16dt + 4g + e of query li, and its query's full l.
-    uint16_t* Oh = a.O + ((size_t)b * a.nQH + h) * (size_t)a.seqQ * D;
-#pragma unroll
-    for (int t = 0; t < QT; ++t) {
-        const float lt = lacc[t][0];
-        const float inv = (lt > 0.f) ? 1.f / lt : 1.f;
-        const int q = qw0 + t * 16 + li;
-        if (q < a.seqQ) {
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-                const u32x2 w = u32x2{pack2<kBf16>(o[t][dt][0] * inv, o[t][dt][1] * inv),
-                                      pack2<kBf16>(o[t][dt][2] * inv, o[t][dt][3] * inv)};
-                *(u32x2*)(Oh + (size_t)q * D + dt * 16 + g * 4) = w;
+            for (int c = 0; c < ND; ++c) {
+                qb[t][c] = *(const u32x4*)(Qh + (size_t)q * D + c * 32 + g * 8);
             }
         }
+
+        f32x4 o[QT][NDT], lacc[QT];
+        float m[QT];
+#pragma unroll
+        for (int t = 0; t < QT; ++t) {
+            m[t] = kInitM;
+            lacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int d = 0; d < NDT; ++d) {
+                o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+
+        const LdsOffsets off = lds_offsets<D>(li, g);
+        int ntiles = (a.seqK + kBc - 1) / kBc;
+        if (a.causal) ntiles = min(ntiles, (min(q0 + BM, a.seqQ) - 1) / kBc + 1);
+        const int wave_qmax = min(qw0 + QT * 16, a.seqQ) - 1;   // last real query of this wave
+
+        load_tile<D, W>(Kh, 0, a.seqK, lds[0][0], wave, lane);
+        load_tile<D, W>(Vh, 0, a.seqK, lds[0][1], wave, lane);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+
+        for (int it = 0; it < ntiles; ++it) {
+            const int buf = it & 1;
+            tile_step<D, W, QT, kBf16>(lds[buf][0], lds[buf][1], lds[buf ^ 1][0], lds[buf ^ 1][1], it + 1 < ntiles, Kh, Vh,
+                                       it * kBc, wave_qmax, a, off, qb, o, m, lacc, qw0, wave, lane, li, g);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
+
+        // ---- O = O^T / l: lane holds d = 16dt + 4g + e of query li, and its query's full l.
+        uint16_t* Oh = a.O + ((size_t)b * a.nQH + h) * (size_t)a.seqQ * D;
+#pragma unroll
+        for (int t = 0; t < QT; ++t) {
+            const float lt = lacc[t][0];
+            const float inv = (lt > 0.f) ? 1.f / lt : 1.f;
+            const int q = qw0 + t * 16 + li;
+            if (q < a.seqQ) {
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const u32x2 w = u32x2{pack2<kBf16>(o[t][dt][0] * inv, o[t][dt][1] * inv),
+                                          pack2<kBf16>(o[t][dt][2] * inv, o[t][dt][3] * inv)};
+                    *(u32x2*)(Oh + (size_t)q * D + dt * 16 + g * 4) = w;
+                }
+            }
+        }
+        __syncthreads();   // every wave is done with the LDS buffers before the next item's first copy
     }
 }
 
@@ -383,7 +390,13 @@ int launch_mfma(const cdna3_prefill_cfg& c, const void* Q, const void* K, const 
     a.sc = kLog2e / sqrtf((float)D);
     const long long blocks = nbh * a.nqb;
     if (blocks > 0x7fffffffLL) return CDNA4_ERR_INVALID_VALUE;
-    fa_mfma<D, W, QT, kBf16><<<(unsigned)blocks, 64 * W, 0, s>>>(a);
+    // One resident workgroup per CU at W = 8 (LDS and VGPRs allow no second), so a grid of one
+    // workgroup per CU (a multiple of 8, see the item mapping) runs every item without relaunch
+    // gaps between workgroups.
+    long long grid = blocks;
+    const int cus = device_cus() & ~7;
+    if (W == 8 && cus >= 8 && grid > cus) grid = cus;
+    fa_mfma<D, W, QT, kBf16><<<(unsigned)grid, 64 * W, 0, s>>>(a);
     return launch_status();
 }
 
