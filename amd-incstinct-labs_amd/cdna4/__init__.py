@@ -100,6 +100,9 @@ def _declare(l: ctypes.CDLL) -> None:
         "cdna3_layernorm_f32": (c_int, [vp, vp, vp, vp, c_int, c_int, c_float, vp]),
         "cdna3_rope_f16": (c_int, [vp, vp, vp, c_int, c_int, c_int, vp]),
         "cdna3_rope_table_f32": (c_int, [vp, vp, c_int, c_int, c_int, c_float, vp]),
+        "cdna3_scatter_kv_f16": (c_int, [vp, vp] + [c_int] * 5 + [vp]),
+        "cdna3_repack_f16": (c_int, [vp, vp] + [c_int] * 4 + [vp]),
+        "cdna3_rope_append_kv_f16": (c_int, [vp] * 8 + [c_int] * 6 + [vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(l, name)
@@ -300,6 +303,34 @@ def rope_table_f32(pos0: int, T: int, D: int, theta: float = 10000.0, device=Non
     _check(lib().cdna3_rope_table_f32(_ptr(cos), _ptr(sin), pos0, T, D, theta, _stream(stream)),
            "cdna3_rope_table_f32")
     return cos, sin
+
+
+# ---- KV cache and layouts of the runtime layer loop -----------------------------------------
+
+def scatter_kv_f16(src: torch.Tensor, cache: torch.Tensor, T: int, heads: int, D: int, pos0: int, max_seq: int,
+                   stream=None) -> None:
+    """scatter_kv_kernel: cache [heads][max_seq][D] rows pos0 .. pos0+T-1 <- src [T][heads][D]."""
+    _dev(src, cache)
+    _check(lib().cdna3_scatter_kv_f16(_ptr(src), _ptr(cache), T, heads, D, pos0, max_seq, _stream(stream)),
+           "cdna3_scatter_kv_f16")
+
+
+def repack_f16(src: torch.Tensor, dst: torch.Tensor, seq: int, heads: int, D: int, direction: int,
+               stream=None) -> None:
+    """repack_kernel: direction 0 token-major [seq][heads][D] -> head-major [heads][seq][D], 1 back."""
+    _dev(src, dst)
+    _check(lib().cdna3_repack_f16(_ptr(src), _ptr(dst), seq, heads, D, direction, _stream(stream)),
+           "cdna3_repack_f16")
+
+
+def rope_append_kv_f16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out: torch.Tensor,
+                       K_cache: torch.Tensor, V_cache: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, T: int,
+                       nQH: int, nKVH: int, D: int, pos0: int, max_seq: int, stream=None) -> None:
+    """RoPE(q) -> q_out [nQH][T][D]; RoPE(k), v -> K_cache / V_cache [nKVH][max_seq][D] at pos0."""
+    _dev(q, k, v, q_out, K_cache, V_cache, cos, sin)
+    _check(lib().cdna3_rope_append_kv_f16(_ptr(q), _ptr(k), _ptr(v), _ptr(q_out), _ptr(K_cache), _ptr(V_cache),
+                                          _ptr(cos), _ptr(sin), T, nQH, nKVH, D, pos0, max_seq, _stream(stream)),
+           "cdna3_rope_append_kv_f16")
 
 
 # ---- the reference's torch-op contracts, as plain functions ------------------------------

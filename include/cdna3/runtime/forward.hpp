@@ -34,5 +34,28 @@ inline hipError_t rope_table_f32(float* cos, float* sin, int pos0, int T, int D,
     return (hipError_t)cdna3_rope_table_f32(cos, sin, pos0, T, D, theta, (cdna4_stream_t)stream);
 }
 
+// KV cache and layouts (forward.hpp:190-220 of the reference; Session::append_kv):
+//   hipLaunchKernelGGL(scatter_kv_kernel, grid, 256, 0, s, src, cache, T, heads, D, pos0, max_seq)
+//     -> cdna3::runtime::scatter_kv_f16(src, cache, T, heads, D, pos0, max_seq, s)
+//   hipLaunchKernelGGL(repack_kernel, grid, 256, 0, s, src, dst, seq, heads, D, dir)
+//     -> cdna3::runtime::repack_f16(src, dst, seq, heads, D, dir, s)
+// and the layer loop's rope_kernel x 2 + Q repack + append_kv in one launch:
+//     -> cdna3::runtime::rope_append_kv_f16(q, k, v, q_head, K_layer, V_layer, cos, sin, T, nQH,
+//                                            nKVH, D, pos0, max_seq, s)
+inline hipError_t scatter_kv_f16(const __half* src, __half* cache, int T, int heads, int D, int pos0, int max_seq,
+                                 hipStream_t stream = nullptr) {
+    return (hipError_t)cdna3_scatter_kv_f16(src, cache, T, heads, D, pos0, max_seq, (cdna4_stream_t)stream);
+}
+inline hipError_t repack_f16(const __half* src, __half* dst, int seq, int heads, int D, int dir,
+                             hipStream_t stream = nullptr) {
+    return (hipError_t)cdna3_repack_f16(src, dst, seq, heads, D, dir, (cdna4_stream_t)stream);
+}
+inline hipError_t rope_append_kv_f16(const __half* q, const __half* k, const __half* v, __half* q_head,
+                                     __half* K_cache, __half* V_cache, const float* cos, const float* sin, int T,
+                                     int nQH, int nKVH, int D, int pos0, int max_seq, hipStream_t stream = nullptr) {
+    return (hipError_t)cdna3_rope_append_kv_f16(q, k, v, q_head, K_cache, V_cache, cos, sin, T, nQH, nKVH, D, pos0,
+                                                max_seq, (cdna4_stream_t)stream);
+}
+
 }  // namespace runtime
 }  // namespace cdna3

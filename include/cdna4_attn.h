@@ -150,6 +150,30 @@ int cdna3_rope_f16(void* T, const float* cos_tab, const float* sin_tab, int seq,
 int cdna3_rope_table_f32(float* cos_tab, float* sin_tab, int pos0, int T, int D,
                          float theta, cdna4_stream_t stream);
 
+/*
+ * KV cache and layout kernels of the runtime layer loop (all fp16, device pointers).
+ * cdna3_scatter_kv_f16 replaces scatter_kv_kernel (cdna3-prims/include/cdna3/runtime/
+ * forward.hpp:209-220, launched by Session::append_kv, session.hpp:240-250):
+ * cache[h][pos0 + s][d] = src[s][h][d] for s < T, cache [heads][max_seq][D]; requires
+ * pos0 + T <= max_seq (the reference wrote past the slot otherwise).
+ * cdna3_repack_f16 replaces repack_kernel (forward.hpp:190-205): dir 0 turns token-major
+ * [seq][heads][D] into head-major [heads][seq][D], dir 1 the reverse.
+ * cdna3_rope_append_kv_f16 fuses what the reference's layer loop does with two rope_kernel
+ * launches, append_kv and the Q repack (session.hpp:170-199): q, k, v are token-major
+ * [T][nQH][D], [T][nKVH][D], [T][nKVH][D]; it writes rotate-half RoPE(q) head-major to
+ * q_out [nQH][T][D], RoPE(k) to K_cache[h][pos0 + s] and v to V_cache[h][pos0 + s]
+ * ([nKVH][max_seq][D] caches), with cos/sin [T][D] for positions pos0 .. pos0 + T - 1
+ * (cdna3_rope_table_f32). Inputs are not modified.
+ */
+int cdna3_scatter_kv_f16(const void* src, void* cache, int T, int heads, int D, int pos0,
+                         int max_seq, cdna4_stream_t stream);
+int cdna3_repack_f16(const void* src, void* dst, int seq, int heads, int D, int dir,
+                     cdna4_stream_t stream);
+int cdna3_rope_append_kv_f16(const void* q, const void* k, const void* v, void* q_out,
+                             void* K_cache, void* V_cache, const float* cos_tab,
+                             const float* sin_tab, int T, int nQH, int nKVH, int D, int pos0,
+                             int max_seq, cdna4_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -59,6 +59,9 @@ def lib() -> ctypes.CDLL:
         l.orc_layernorm_f32.argtypes = [_f32p, _f32p, _f32p, _f32p, c_int, c_int, c_float]
         l.orc_rope_table.argtypes = [_f32p, _f32p, c_int, c_int, c_int, c_float]
         l.orc_rope_f16.argtypes = [_u16p, _f32p, _f32p, c_int, c_int, c_int]
+        l.orc_scatter_kv_f16.argtypes = [_u16p, _u16p] + [c_int] * 5
+        l.orc_repack_f16.argtypes = [_u16p, _u16p] + [c_int] * 4
+        l.orc_rope_append_kv_f16.argtypes = [_u16p] * 6 + [_f32p, _f32p] + [c_int] * 6
         _LIB = l
     return _LIB
 
@@ -198,6 +201,37 @@ def rope(T_bits: np.ndarray, cos: np.ndarray, sin: np.ndarray, seq: int, heads: 
     lib().orc_rope_f16(t.reshape(-1), np.ascontiguousarray(cos, np.float32).reshape(-1),
                        np.ascontiguousarray(sin, np.float32).reshape(-1), seq, heads, D)
     return t
+
+
+def scatter_kv(src_bits: np.ndarray, cache_bits: np.ndarray, T: int, heads: int, D: int, pos0: int,
+               max_seq: int) -> np.ndarray:
+    """scatter_kv_kernel on fp16 bits: a copy of cache [heads][max_seq][D] with src [T][heads][D]
+    written at token offset pos0."""
+    out = np.ascontiguousarray(cache_bits, np.uint16).copy()
+    lib().orc_scatter_kv_f16(np.ascontiguousarray(src_bits, np.uint16).reshape(-1), out.reshape(-1), T, heads, D,
+                             pos0, max_seq)
+    return out
+
+
+def repack(src_bits: np.ndarray, seq: int, heads: int, D: int, direction: int) -> np.ndarray:
+    """repack_kernel on fp16 bits: 0 token-major -> head-major, 1 the reverse."""
+    out = np.empty(seq * heads * D, np.uint16)
+    lib().orc_repack_f16(np.ascontiguousarray(src_bits, np.uint16).reshape(-1), out, seq, heads, D, direction)
+    return out
+
+
+def rope_append_kv(q_bits, k_bits, v_bits, K_cache_bits, V_cache_bits, cos, sin, T: int, nQH: int, nKVH: int,
+                   D: int, pos0: int, max_seq: int):
+    """The layer loop's RoPE + Q repack + K/V append: (q_out [nQH][T][D], K cache, V cache) bits."""
+    q_out = np.empty(nQH * T * D, np.uint16)
+    Kc = np.ascontiguousarray(K_cache_bits, np.uint16).copy().reshape(-1)
+    Vc = np.ascontiguousarray(V_cache_bits, np.uint16).copy().reshape(-1)
+    lib().orc_rope_append_kv_f16(np.ascontiguousarray(q_bits, np.uint16).reshape(-1),
+                                 np.ascontiguousarray(k_bits, np.uint16).reshape(-1),
+                                 np.ascontiguousarray(v_bits, np.uint16).reshape(-1), q_out, Kc, Vc,
+                                 np.ascontiguousarray(cos, np.float32).reshape(-1),
+                                 np.ascontiguousarray(sin, np.float32).reshape(-1), T, nQH, nKVH, D, pos0, max_seq)
+    return q_out, Kc, Vc
 
 
 # ---- the reference's own CPU references (oracle/_ref) ------------------------------------------

@@ -23,6 +23,11 @@
  *   orc_rope_table    cdna3-prims/include/cdna3/runtime/session.hpp:120-135 (fill_rope)
  *   orc_rope_f16      cdna3-prims/include/cdna3/runtime/forward.hpp:135-148 (rope_kernel),
  *                     reading every input element before any is written
+ *   orc_scatter_kv_f16 cdna3-prims/include/cdna3/runtime/forward.hpp:209-220 (scatter_kv_kernel)
+ *   orc_repack_f16    cdna3-prims/include/cdna3/runtime/forward.hpp:190-205 (repack_kernel)
+ *   orc_rope_append_kv_f16  the layer-loop sequence of cdna3-prims/include/cdna3/runtime/
+ *                     session.hpp:170-199: rope_kernel on Q and K, repack of Q to head-major,
+ *                     scatter_kv_kernel of K and V into the cache at pos0
  *   generators        splitmix64 (Steele, Lea, Flood 2014), counter-based; Box-Muller normals
  */
 #include <math.h>
@@ -376,4 +381,44 @@ void orc_rope_f16(uint16_t* T, const float* cosv, const float* sinv, int seq, in
             }
         }
     free(row);
+}
+
+/* ---- KV cache and layouts ---------------------------------------------------------------- */
+
+/* forward.hpp:209-220: cache[h][pos0 + s][d] = src[s][h][d], cache [heads][max_seq][D]. */
+void orc_scatter_kv_f16(const uint16_t* src, uint16_t* cache, int T, int heads, int D, int pos0, int max_seq) {
+    for (int s = 0; s < T; ++s)
+        for (int h = 0; h < heads; ++h)
+            for (int d = 0; d < D; ++d)
+                cache[((size_t)h * max_seq + pos0 + s) * D + d] = src[((size_t)s * heads + h) * D + d];
+}
+
+/* forward.hpp:190-205: dir 0 token-major [seq][heads][D] -> head-major [heads][seq][D], dir 1 back. */
+void orc_repack_f16(const uint16_t* src, uint16_t* dst, int seq, int heads, int D, int dir) {
+    for (int s = 0; s < seq; ++s)
+        for (int h = 0; h < heads; ++h)
+            for (int d = 0; d < D; ++d) {
+                const size_t tok = ((size_t)s * heads + h) * D + d;
+                const size_t hm = ((size_t)h * seq + s) * D + d;
+                if (dir == 0) dst[hm] = src[tok]; else dst[tok] = src[hm];
+            }
+}
+
+/* session.hpp:170-199 in sequence: RoPE on copies of q and k (orc_rope_f16), q repacked to
+ * head-major q_out, k and v scattered into the caches at pos0. */
+void orc_rope_append_kv_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* q_out,
+                            uint16_t* Kc, uint16_t* Vc, const float* cosv, const float* sinv, int T, int nQH,
+                            int nKVH, int D, int pos0, int max_seq) {
+    uint16_t* qr = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)T * nQH * D + 2);
+    uint16_t* kr = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)T * nKVH * D + 2);
+    if (!qr || !kr) { free(qr); free(kr); return; }
+    memcpy(qr, q, sizeof(uint16_t) * (size_t)T * nQH * D);
+    memcpy(kr, k, sizeof(uint16_t) * (size_t)T * nKVH * D);
+    orc_rope_f16(qr, cosv, sinv, T, nQH, D);
+    orc_rope_f16(kr, cosv, sinv, T, nKVH, D);
+    orc_repack_f16(qr, q_out, T, nQH, D, 0);
+    orc_scatter_kv_f16(kr, Kc, T, nKVH, D, pos0, max_seq);
+    orc_scatter_kv_f16(v, Vc, T, nKVH, D, pos0, max_seq);
+    free(qr);
+    free(kr);
 }

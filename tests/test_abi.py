@@ -74,6 +74,11 @@ def test_invalid_arguments_rejected_without_gpu():
     assert l.cdna3_rmsnorm_f32(p, p, p, 4, 0, 1e-6, None) == 1
     assert l.cdna3_rope_f16(p, p, p, 4, 2, 63, None) == 1                                   # odd D
     assert l.cdna3_rope_table_f32(p, p, 0, 4, 64, -1.0, None) == 1
+    assert l.cdna3_scatter_kv_f16(p, p, 4, 2, 64, 10, 12, None) == 1                        # pos0 + T > max_seq
+    assert l.cdna3_scatter_kv_f16(p, p, 0, 2, 64, 0, 12, None) == 0                         # T == 0
+    assert l.cdna3_repack_f16(p, p, 4, 2, 64, 2, None) == 1                                 # direction
+    assert l.cdna3_rope_append_kv_f16(p, p, p, p, p, p, p, p, 4, 8, 2, 63, 0, 16, None) == 1  # odd D
+    assert l.cdna3_rope_append_kv_f16(p, p, p, p, p, p, p, p, 4, 8, 2, 64, 14, 16, None) == 1  # past the cache
 
 
 def test_cpp_headers_compile_host_only(tmp_path):
@@ -119,9 +124,9 @@ def test_wave_primitives_use_no_lds_and_no_readlane(tmp_path):
 
 
 def test_library_kernels_avoid_lds_where_designed_to(tmp_path):
-    # Reductions, scans, norms and the decode merge are LDS-free by design; prefill and the
+    # Reductions, scans, norms, KV-cache kernels and the decode merge are LDS-free by design; prefill and the
     # decode partial kernel stage K/V in LDS.
-    for src in ("reduce_scan.hip", "norms.hip", "decode.hip"):
+    for src in ("reduce_scan.hip", "norms.hip", "decode.hip", "kv_cache.hip"):
         asm = _device_asm(os.path.join(ROOT, "amd-incstinct-labs_amd", "csrc", src), tmp_path)
         for name, body in _functions(asm).items():
             assert not re.search(r"v_pk_(add|mul|fma)_f32", body), (src, name)

@@ -296,3 +296,36 @@ def test_rope_table_and_rotation():
     want = np.concatenate([z.real, z.imag], axis=-1)
     np.testing.assert_allclose(out, want, atol=2e-3 * np.abs(want).max())
     assert np.array_equal(out[0], vals.reshape(T, heads, D)[0])  # position 0 is the identity
+
+
+def test_scatter_and_repack_are_the_reference_index_maps():
+    # forward.hpp:190-220 restated; checked against numpy's own indexing and transposes.
+    rng = np.random.default_rng(7)
+    T, heads, D, pos0, max_seq = 5, 3, 10, 2, 9
+    src = rng.integers(0, 1 << 16, T * heads * D, dtype=np.uint16)
+    cache = rng.integers(0, 1 << 16, heads * max_seq * D, dtype=np.uint16)
+    got = oracle.scatter_kv(src, cache, T, heads, D, pos0, max_seq).reshape(heads, max_seq, D)
+    want = cache.reshape(heads, max_seq, D).copy()
+    want[:, pos0:pos0 + T, :] = src.reshape(T, heads, D).transpose(1, 0, 2)
+    assert np.array_equal(got, want)
+    hm = oracle.repack(src, T, heads, D, 0)
+    assert np.array_equal(hm.reshape(heads, T, D), src.reshape(T, heads, D).transpose(1, 0, 2))
+    assert np.array_equal(oracle.repack(hm, T, heads, D, 1), src)
+
+
+def test_rope_append_is_rope_then_layout():
+    # The fused layer-loop step equals rope on token-major copies followed by the layout maps.
+    T, nQH, nKVH, D, pos0, max_seq = 6, 4, 2, 16, 3, 12
+    c, s = oracle.rope_table(pos0, T, D, 10000.0)
+    _, q = oracle.round16(oracle.normal(1, T * nQH * D), oracle.F16)
+    _, k = oracle.round16(oracle.normal(2, T * nKVH * D), oracle.F16)
+    _, v = oracle.round16(oracle.normal(3, T * nKVH * D), oracle.F16)
+    Kc0 = np.full(nKVH * max_seq * D, 0x7e00, np.uint16)    # a NaN pattern outside the slot
+    Vc0 = np.full(nKVH * max_seq * D, 0x7e00, np.uint16)
+    q_out, Kc, Vc = oracle.rope_append_kv(q, k, v, Kc0, Vc0, c, s, T, nQH, nKVH, D, pos0, max_seq)
+    qr = oracle.rope(q, c, s, T, nQH, D).reshape(T, nQH, D)
+    kr = oracle.rope(k, c, s, T, nKVH, D).reshape(T, nKVH, D)
+    assert np.array_equal(q_out.reshape(nQH, T, D), qr.transpose(1, 0, 2))
+    Kw = Kc0.reshape(nKVH, max_seq, D).copy(); Kw[:, pos0:pos0 + T] = kr.transpose(1, 0, 2)
+    Vw = Vc0.reshape(nKVH, max_seq, D).copy(); Vw[:, pos0:pos0 + T] = v.reshape(T, nKVH, D).transpose(1, 0, 2)
+    assert np.array_equal(Kc.reshape(nKVH, max_seq, D), Kw) and np.array_equal(Vc.reshape(nKVH, max_seq, D), Vw)
