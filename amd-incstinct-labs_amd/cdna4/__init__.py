@@ -32,7 +32,8 @@ __all__ = [
     "PrefillCfg", "DecodeCfg", "DecodeDmeCfg", "library_path", "lib", "abi_version", "error_string",
     "prefill", "decode", "decode_dme", "decode_workspace_size", "reduce", "reduce_workspace_size",
     "scan_inclusive", "scan_workspace_size", "rmsnorm_f32", "layernorm_f32", "rope_f16",
-    "rope_table_f32", "flash_attn", "flash_attn_decode", "CDNA4Error",
+    "rope_table_f32", "flash_attn", "flash_attn_decode", "CDNA4Error", "PrefillStrides", "prefill_strided",
+    "scatter_kv_f16", "repack_f16", "rope_append_kv_f16",
 ]
 
 # Element types and operators (include/cdna4_attn.h).
@@ -58,6 +59,12 @@ class PrefillCfg(ctypes.Structure):
     _fields_ = [("D", ctypes.c_int), ("seqQ", ctypes.c_int), ("seqK", ctypes.c_int),
                 ("nQHeads", ctypes.c_int), ("nKVHeads", ctypes.c_int), ("batch", ctypes.c_int),
                 ("causal", ctypes.c_int)]
+
+
+class PrefillStrides(ctypes.Structure):
+    """cdna3_prefill_strides: element strides (batch, head, row) of Q, of K and V, and of O."""
+    _fields_ = [(n, ctypes.c_longlong) for n in ("q_batch", "q_head", "q_row", "kv_batch", "kv_head", "kv_row",
+                                                 "o_batch", "o_head", "o_row")]
 
 
 class DecodeCfg(ctypes.Structure):
@@ -90,6 +97,8 @@ def _declare(l: ctypes.CDLL) -> None:
         "cdna3_abi_version": (c_int, []),
         "cdna3_error_string": (ctypes.c_char_p, [c_int]),
         "cdna3_attn_prefill": (c_int, [vp, vp, vp, vp, ctypes.POINTER(PrefillCfg), c_int, vp]),
+        "cdna3_attn_prefill_strided": (c_int, [vp, vp, vp, vp, ctypes.POINTER(PrefillCfg),
+                                               ctypes.POINTER(PrefillStrides), c_int, vp]),
         "cdna3_attn_decode_workspace_size": (c_size, [ctypes.POINTER(DecodeCfg)]),
         "cdna3_attn_decode": (c_int, [vp, vp, vp, vp, ctypes.POINTER(DecodeCfg), c_int, vp, c_size, vp]),
         "cdna3_reduce_workspace_size": (c_size, [c_size, c_int]),
@@ -186,6 +195,18 @@ def prefill(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, O: torch.Tensor, 
         raise ValueError("tensor smaller than the configuration")
     _check(lib().cdna3_attn_prefill(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), ctypes.byref(cfg), dt,
                                     _stream(stream)), "cdna3_attn_prefill")
+
+
+def prefill_strided(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, O: torch.Tensor, cfg: PrefillCfg,
+                    strides: PrefillStrides, stream=None) -> None:
+    """Prefill over strided Q/K/V/O (fp16 or bf16), e.g. K/V in place in a KV cache and O
+    token-major. The caller guarantees the strides stay inside the tensors."""
+    _dev(Q, K, V, O)
+    dt = _dtype(Q)
+    if not (K.dtype == V.dtype == O.dtype == Q.dtype):
+        raise ValueError("Q, K, V, O must share one dtype")
+    _check(lib().cdna3_attn_prefill_strided(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), ctypes.byref(cfg),
+                                            ctypes.byref(strides), dt, _stream(stream)), "cdna3_attn_prefill_strided")
 
 
 def decode_workspace_size(cfg: DecodeCfg) -> int:

@@ -41,6 +41,9 @@ constexpr int kBc = 64;       // keys per K/V tile
 
 struct PrefillArgs {
     const uint16_t* Q; const uint16_t* K; const uint16_t* V; uint16_t* O;
+    // Element strides (batch, head, row) of Q, of K and V, and of O; the contiguous layout is
+    // head = seq * D, batch = heads * seq * D, row = D.
+    long long q_bs, q_hs, q_rs, k_bs, k_hs, k_rs, o_bs, o_hs, o_rs;
     int seqQ, seqK, nQH, nKVH, batch, causal;
     int nqb;          // q blocks per (batch, head)
     int xcd_map;      // 1: all q blocks of a (batch, head) on one XCD, heads in sequence
@@ -49,7 +52,7 @@ struct PrefillArgs {
 
 // Issue the asynchronous copy of keys [k0, k0 + kBc) of one head into an LDS tile.
 template <int D, int W>
-__device__ __forceinline__ void load_tile(const uint16_t* __restrict__ head, int k0, int seqK,
+__device__ __forceinline__ void load_tile(const uint16_t* __restrict__ head, long long row_stride, int k0, int seqK,
                                           uint16_t* tile, int wave, int lane) {
     constexpr int CPR = D / 8;                       // 16-byte chunks per key row
     constexpr int NI = kBc * CPR / (64 * W);         // wave instructions per tile
@@ -61,7 +64,7 @@ __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ head, int
         const int r = p / CPR;
         const int lc = (p % CPR) ^ swz<D>(r);
         const int key = min(k0 + r, seqK - 1);   // rows past the end re-read the last key (masked)
-        __builtin_amdgcn_global_load_lds((const void*)(head + (size_t)key * D + lc * 8),
+        __builtin_amdgcn_global_load_lds((const void*)(head + key * row_stride + lc * 8),
                                          (LDS_AS void*)(tile + p0 * 8), 16, 0, 0);
     }
 }
@@ -178,8 +181,8 @@ __device__ __forceinline__ void tile_step(const uint16_t* __restrict__ kt, const
                                           f32x4 (&o)[QT][D / 16], float (&m)[QT], f32x4 (&lacc)[QT], int qw0,
                                           int wave, int lane, int li, int g) {
     if (load_next) {
-        load_tile<D, W>(Kh, k0 + kBc, a.seqK, kn, wave, lane);
-        load_tile<D, W>(Vh, k0 + kBc, a.seqK, vn, wave, lane);
+        load_tile<D, W>(Kh, a.k_rs, k0 + kBc, a.seqK, kn, wave, lane);
+        load_tile<D, W>(Vh, a.k_rs, k0 + kBc, a.seqK, vn, wave, lane);
     }
     if (!(a.causal && k0 > wave_qmax)) {
         const bool need_mask = (a.causal && k0 + kBc - 1 > qw0) || (k0 + kBc > a.seqK);
@@ -226,9 +229,9 @@ __global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
         const int q0 = qblk * BM;
         const int qw0 = q0 + wave * QT * 16;   // first query row of this wave
 
-        const uint16_t* Kh = a.K + ((size_t)b * a.nKVH + kvh) * (size_t)a.seqK * D;
-        const uint16_t* Vh = a.V + ((size_t)b * a.nKVH + kvh) * (size_t)a.seqK * D;
-        const uint16_t* Qh = a.Q + ((size_t)b * a.nQH + h) * (size_t)a.seqQ * D;
+        const uint16_t* Kh = a.K + b * a.k_bs + kvh * a.k_hs;
+        const uint16_t* Vh = a.V + b * a.k_bs + kvh * a.k_hs;
+        const uint16_t* Qh = a.Q + b * a.q_bs + h * a.q_hs;
 
         // Q as B operands: lane holds Q[q = qw0 + t*16 + li][32*c + 8*g .. +8].
         u32x4 qb[QT][ND];
@@ -237,7 +240,7 @@ __global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
             const int q = min(qw0 + t * 16 + li, a.seqQ - 1);
 #pragma unroll
             for (int c = 0; c < ND; ++c) {
-                qb[t][c] = *(const u32x4*)(Qh + (size_t)q * D + c * 32 + g * 8);
+                qb[t][c] = *(const u32x4*)(Qh + q * a.q_rs + c * 32 + g * 8);
             }
         }
 
@@ -258,8 +261,8 @@ __global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
         if (a.causal) ntiles = min(ntiles, (min(q0 + BM, a.seqQ) - 1) / kBc + 1);
         const int wave_qmax = min(qw0 + QT * 16, a.seqQ) - 1;   // last real query of this wave
 
-        load_tile<D, W>(Kh, 0, a.seqK, lds[0][0], wave, lane);
-        load_tile<D, W>(Vh, 0, a.seqK, lds[0][1], wave, lane);
+        load_tile<D, W>(Kh, a.k_rs, 0, a.seqK, lds[0][0], wave, lane);
+        load_tile<D, W>(Vh, a.k_rs, 0, a.seqK, lds[0][1], wave, lane);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
 
@@ -272,7 +275,7 @@ __global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
         }
 
         // ---- O = O^T / l: lane holds d = 16dt + 4g + e of query li, and its query's full l.
-        uint16_t* Oh = a.O + ((size_t)b * a.nQH + h) * (size_t)a.seqQ * D;
+        uint16_t* Oh = a.O + b * a.o_bs + h * a.o_hs;
 #pragma unroll
         for (int t = 0; t < QT; ++t) {
             const float lt = lacc[t][0];
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
                 for (int dt = 0; dt < NDT; ++dt) {
                     const u32x2 w = u32x2{pack2<kBf16>(o[t][dt][0] * inv, o[t][dt][1] * inv),
                                           pack2<kBf16>(o[t][dt][2] * inv, o[t][dt][3] * inv)};
-                    *(u32x2*)(Oh + (size_t)q * D + dt * 16 + g * 4) = w;
+                    *(u32x2*)(Oh + q * a.o_rs + dt * 16 + g * 4) = w;
                 }
             }
         }
@@ -378,10 +381,14 @@ __global__ __launch_bounds__(64) void fa_f32(const float* __restrict__ Q, const 
 }
 
 template <int D, int W, int QT, bool kBf16>
-int launch_mfma(const cdna3_prefill_cfg& c, const void* Q, const void* K, const void* V, void* O, hipStream_t s) {
+int launch_mfma(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& st, const void* Q, const void* K,
+                const void* V, void* O, hipStream_t s) {
     constexpr int BM = W * QT * 16;
     PrefillArgs a;
     a.Q = (const uint16_t*)Q; a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.O = (uint16_t*)O;
+    a.q_bs = st.q_batch; a.q_hs = st.q_head; a.q_rs = st.q_row;
+    a.k_bs = st.kv_batch; a.k_hs = st.kv_head; a.k_rs = st.kv_row;
+    a.o_bs = st.o_batch; a.o_hs = st.o_head; a.o_rs = st.o_row;
     a.seqQ = c.seqQ; a.seqK = c.seqK; a.nQH = c.nQHeads; a.nKVH = c.nKVHeads; a.batch = c.batch;
     a.causal = c.causal ? 1 : 0;
     a.nqb = (c.seqQ + BM - 1) / BM;
@@ -401,12 +408,34 @@ int launch_mfma(const cdna3_prefill_cfg& c, const void* Q, const void* K, const 
 }
 
 template <int D, bool kBf16>
-int dispatch_mfma(const cdna3_prefill_cfg& c, const void* Q, const void* K, const void* V, void* O, hipStream_t s) {
+int dispatch_mfma(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& st, const void* Q, const void* K,
+                  const void* V, void* O, hipStream_t s) {
     // 8 waves x 32 queries (two waves per SIMD) when that gives >= 2 workgroups per CU, else
     // 4 waves x 16 queries for small problems.
     const long long big_blocks = (long long)c.batch * c.nQHeads * ((c.seqQ + 255) / 256);
-    if (big_blocks >= 512) return launch_mfma<D, 8, 2, kBf16>(c, Q, K, V, O, s);
-    return launch_mfma<D, 4, 1, kBf16>(c, Q, K, V, O, s);
+    if (big_blocks >= 512) return launch_mfma<D, 8, 2, kBf16>(c, st, Q, K, V, O, s);
+    return launch_mfma<D, 4, 1, kBf16>(c, st, Q, K, V, O, s);
+}
+
+int check_cfg(const cdna3_prefill_cfg* cfg, const void* Q, const void* K, const void* V, const void* O) {
+    if (!cfg) return CDNA4_ERR_INVALID_VALUE;
+    const cdna3_prefill_cfg& c = *cfg;
+    if (c.D != 64 && c.D != 128) return CDNA4_ERR_INVALID_VALUE;
+    if (c.seqQ < 1 || c.seqK < 1 || c.nQHeads < 1 || c.nKVHeads < 1 || c.batch < 1) return CDNA4_ERR_INVALID_VALUE;
+    if (c.nQHeads % c.nKVHeads) return CDNA4_ERR_INVALID_VALUE;
+    if (c.causal && c.seqQ != c.seqK) return CDNA4_ERR_INVALID_VALUE;
+    if (!Q || !K || !V || !O) return CDNA4_ERR_INVALID_VALUE;
+    return 0;
+}
+
+cdna3_prefill_strides contiguous_strides(const cdna3_prefill_cfg& c) {
+    cdna3_prefill_strides st;
+    st.q_row = st.kv_row = st.o_row = c.D;
+    st.q_head = st.o_head = (long long)c.seqQ * c.D;
+    st.kv_head = (long long)c.seqK * c.D;
+    st.q_batch = st.o_batch = st.q_head * c.nQHeads;
+    st.kv_batch = st.kv_head * c.nKVHeads;
+    return st;
 }
 
 }  // namespace
@@ -416,13 +445,8 @@ using namespace cdna4;
 
 extern "C" int cdna3_attn_prefill(const void* Q, const void* K, const void* V, void* O, const cdna3_prefill_cfg* cfg,
                                   int dtype, cdna4_stream_t stream) {
-    if (!cfg) return CDNA4_ERR_INVALID_VALUE;
+    if (int e = check_cfg(cfg, Q, K, V, O)) return e;
     const cdna3_prefill_cfg& c = *cfg;
-    if (c.D != 64 && c.D != 128) return CDNA4_ERR_INVALID_VALUE;
-    if (c.seqQ < 1 || c.seqK < 1 || c.nQHeads < 1 || c.nKVHeads < 1 || c.batch < 1) return CDNA4_ERR_INVALID_VALUE;
-    if (c.nQHeads % c.nKVHeads) return CDNA4_ERR_INVALID_VALUE;
-    if (c.causal && c.seqQ != c.seqK) return CDNA4_ERR_INVALID_VALUE;
-    if (!Q || !K || !V || !O) return CDNA4_ERR_INVALID_VALUE;
     if (dtype != CDNA4_F16 && dtype != CDNA4_BF16 && dtype != CDNA4_F32) return CDNA4_ERR_INVALID_VALUE;
     if (dtype != CDNA4_F32 && ((((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V) & 15u) || ((uintptr_t)O & 7u)))
         return CDNA4_ERR_INVALID_VALUE;
@@ -440,7 +464,35 @@ extern "C" int cdna3_attn_prefill(const void* Q, const void* K, const void* V, v
                                                       c.seqQ, c.seqK, c.nQHeads, c.nKVHeads, c.causal ? 1 : 0, nqb);
         return launch_status();
     }
+    const cdna3_prefill_strides st = contiguous_strides(c);
     const bool bf = dtype == CDNA4_BF16;
-    if (c.D == 128) return bf ? dispatch_mfma<128, true>(c, Q, K, V, O, s) : dispatch_mfma<128, false>(c, Q, K, V, O, s);
-    return bf ? dispatch_mfma<64, true>(c, Q, K, V, O, s) : dispatch_mfma<64, false>(c, Q, K, V, O, s);
+    if (c.D == 128)
+        return bf ? dispatch_mfma<128, true>(c, st, Q, K, V, O, s) : dispatch_mfma<128, false>(c, st, Q, K, V, O, s);
+    return bf ? dispatch_mfma<64, true>(c, st, Q, K, V, O, s) : dispatch_mfma<64, false>(c, st, Q, K, V, O, s);
+}
+
+extern "C" int cdna3_attn_prefill_strided(const void* Q, const void* K, const void* V, void* O,
+                                          const cdna3_prefill_cfg* cfg, const cdna3_prefill_strides* strides,
+                                          int dtype, cdna4_stream_t stream) {
+    if (int e = check_cfg(cfg, Q, K, V, O)) return e;
+    if (!strides) return CDNA4_ERR_INVALID_VALUE;
+    const cdna3_prefill_cfg& c = *cfg;
+    const cdna3_prefill_strides& st = *strides;
+    if (dtype != CDNA4_F16 && dtype != CDNA4_BF16) return CDNA4_ERR_INVALID_VALUE;
+    // 16-byte row loads of Q, K, V and 8-byte stores of O: every stride a multiple of 8 (4 for O)
+    // elements, rows no shorter than D.
+    const long long in[6] = {st.q_batch, st.q_head, st.q_row, st.kv_batch, st.kv_head, st.kv_row};
+    for (long long x : in)
+        if (x < 0 || (x & 7)) return CDNA4_ERR_INVALID_VALUE;
+    const long long out[3] = {st.o_batch, st.o_head, st.o_row};
+    for (long long x : out)
+        if (x < 0 || (x & 3)) return CDNA4_ERR_INVALID_VALUE;
+    if (st.q_row < c.D || st.kv_row < c.D || st.o_row < c.D) return CDNA4_ERR_INVALID_VALUE;
+    if ((((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V) & 15u) || ((uintptr_t)O & 7u)) return CDNA4_ERR_INVALID_VALUE;
+    if (int e = check_device()) return e;
+    hipStream_t s = (hipStream_t)stream;
+    const bool bf = dtype == CDNA4_BF16;
+    if (c.D == 128)
+        return bf ? dispatch_mfma<128, true>(c, st, Q, K, V, O, s) : dispatch_mfma<128, false>(c, st, Q, K, V, O, s);
+    return bf ? dispatch_mfma<64, true>(c, st, Q, K, V, O, s) : dispatch_mfma<64, false>(c, st, Q, K, V, O, s);
 }

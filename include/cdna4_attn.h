@@ -95,6 +95,26 @@ const char* cdna3_error_string(int code);
 int cdna3_attn_prefill(const void* Q, const void* K, const void* V, void* O,
                        const cdna3_prefill_cfg* cfg, int dtype, cdna4_stream_t stream);
 
+/*
+ * cdna3_attn_prefill_strided: the same computation with explicit element strides, so a caller
+ * can attend over tensors that are not packed [batch][heads][seq][D]: e.g. K/V read in place
+ * from a KV cache [nKVH][max_seq][D] (kv_head = max_seq * D) and O written token-major
+ * [seq][nQH][D] (o_head = D, o_row = nQH * D) for the projection that follows. No counterpart
+ * in the reference, whose layer loop repacked Q, K, V and O around the call
+ * (cdna3-prims/include/cdna3/runtime/session.hpp:190-207). dtype f16 or bf16; every Q/K/V
+ * stride a multiple of 8 elements and every O stride a multiple of 4; rows no shorter than D.
+ */
+typedef struct cdna3_prefill_strides {
+    long long q_batch, q_head, q_row;     /* Q element strides */
+    long long kv_batch, kv_head, kv_row;  /* K and V element strides */
+    long long o_batch, o_head, o_row;     /* O element strides */
+} cdna3_prefill_strides;
+
+int cdna3_attn_prefill_strided(const void* Q, const void* K, const void* V, void* O,
+                               const cdna3_prefill_cfg* cfg,
+                               const cdna3_prefill_strides* strides, int dtype,
+                               cdna4_stream_t stream);
+
 /* ---- attention: decode (one query per sequence, split-K) --------------------
  * Replaces cdna3::attn::decode (attention.hpp:117-137) and cdna3::attn::decode_dme
  * (attention.hpp:152-173); the reference has no batch dimension (batch == 1 here).

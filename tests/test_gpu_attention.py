@@ -203,3 +203,25 @@ def test_cpp_dropin_validation_program():
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "Result: 13/13 PASS" in r.stdout
+
+
+@pytest.mark.parametrize("D,S,HQ,HK,dtype", [(64, 512, 12, 12, torch.float16), (128, 300, 8, 2, torch.bfloat16),
+                                              (64, 2048, 16, 4, torch.float16)])
+def test_prefill_strided_reads_cache_and_writes_token_major(D, S, HQ, HK, dtype):
+    # The layer loop's layout: Q head-major, K/V in place in a [nKVH][max_seq][D] cache, O token-major.
+    max_seq = S + 77 if S % 8 == 0 else S + 3
+    max_seq = (max_seq + 7) // 8 * 8
+    g = torch.Generator(device=DEV).manual_seed(S)
+    Q = torch.randn(HQ, S, D, device=DEV, generator=g).to(dtype)
+    Kc = torch.randn(HK, max_seq, D, device=DEV, generator=g).to(dtype)
+    Vc = torch.randn(HK, max_seq, D, device=DEV, generator=g).to(dtype)
+    O_tok = torch.full((S, HQ, D), float("nan"), device=DEV, dtype=dtype)
+    cfg = cdna4.PrefillCfg(D, S, S, HQ, HK, 1, 1)
+    st = cdna4.PrefillStrides(HQ * S * D, S * D, D, HK * max_seq * D, max_seq * D, D, S * HQ * D, D, HQ * D)
+    cdna4.prefill_strided(Q, Kc, Vc, O_tok, cfg, st)
+    # Same kernel on packed copies: identical bits.
+    K = Kc[:, :S].contiguous()
+    V = Vc[:, :S].contiguous()
+    O = torch.empty(HQ, S, D, device=DEV, dtype=dtype)
+    cdna4.prefill(Q, K, V, O, cfg)
+    assert torch.equal(O_tok.transpose(0, 1), O)
