@@ -7,6 +7,8 @@ cdna3-prims/include/cdna3/runtime/forward.hpp) over the library's C ABI (include
     decode(q, K, V, o, DecodeCfg(...))            cdna3::attn::decode    (attention.hpp:117)
     decode_dme(q, K, V, o, DecodeDmeCfg(...))     cdna3::attn::decode_dme (attention.hpp:152)
     rmsnorm_f32, layernorm_f32, rope_f16, rope_table_f32    runtime entry points
+    Session(model_dir, max_seq).generate(ids, GenerateCfg(...))
+                                                  cdna3::runtime::Session (runtime/session.hpp:47)
     reduce, scan_inclusive                        device-wide wave::dpp reductions / scans
     flash_attn(q, k, v), flash_attn_decode(q, k_cache, v_cache)
                                                   the reference's torch ops (fa_torch_op.hip:36,
@@ -33,7 +35,7 @@ __all__ = [
     "prefill", "decode", "decode_dme", "decode_workspace_size", "reduce", "reduce_workspace_size",
     "scan_inclusive", "scan_workspace_size", "rmsnorm_f32", "layernorm_f32", "rope_f16",
     "rope_table_f32", "flash_attn", "flash_attn_decode", "CDNA4Error", "PrefillStrides", "prefill_strided",
-    "scatter_kv_f16", "repack_f16", "rope_append_kv_f16",
+    "scatter_kv_f16", "repack_f16", "rope_append_kv_f16", "ModelCfg", "GenerateCfg", "Session",
 ]
 
 # Element types and operators (include/cdna4_attn.h).
@@ -77,6 +79,18 @@ class DecodeCfg(ctypes.Structure):
         super().__init__(D, N, nQHeads, nKVHeads, batch, stride_kv)
 
 
+class ModelCfg(ctypes.Structure):
+    """cdna3_model_cfg: the reference's ModelConfig (runtime/model_loader.hpp:52-61) plus the
+    qkv_bias flag and the norm kind and epsilon."""
+    _fields_ = [(n, ctypes.c_int) for n in ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "ffn_dim",
+                                            "vocab_size")] + \
+               [("rope_theta", ctypes.c_float), ("qkv_bias", ctypes.c_int), ("layernorm", ctypes.c_int),
+                ("norm_eps", ctypes.c_float)]
+
+    def as_dict(self) -> dict:
+        return {n: getattr(self, n) for n, _ in self._fields_}
+
+
 def DecodeDmeCfg(D: int, N: int, nQHeads: int, nKVHeads: int, stride_kv: int, batch: int = 1) -> DecodeCfg:
     """The reference's DecodeDmeCfg {D, N, nQHeads, nKVHeads, stride_kv}
     (detail/fa_decode_dme_kernel.hpp:45-48) as a DecodeCfg."""
@@ -112,6 +126,12 @@ def _declare(l: ctypes.CDLL) -> None:
         "cdna3_scatter_kv_f16": (c_int, [vp, vp] + [c_int] * 5 + [vp]),
         "cdna3_repack_f16": (c_int, [vp, vp] + [c_int] * 4 + [vp]),
         "cdna3_rope_append_kv_f16": (c_int, [vp] * 8 + [c_int] * 6 + [vp]),
+        "cdna3_session_create": (c_int, [ctypes.c_char_p, c_int, ctypes.POINTER(vp)]),
+        "cdna3_session_destroy": (None, [vp]),
+        "cdna3_session_config": (c_int, [vp, ctypes.POINTER(ModelCfg)]),
+        "cdna3_session_generate": (c_int, [vp, vp, c_int, c_int, c_int, vp, ctypes.POINTER(c_int), vp,
+                                           ctypes.POINTER(c_float), ctypes.POINTER(c_float)]),
+        "cdna3_session_prefill_logits": (c_int, [vp, vp, c_int, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(l, name)
@@ -381,3 +401,83 @@ def flash_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     o = torch.empty((nqh, D), dtype=q.dtype, device=q.device)
     decode(q, k_cache, v_cache, o, DecodeCfg(D, N, nqh, nkvh, 1, 0))
     return o
+
+
+# ---- small-LLM runtime session ----------------------------------------------------------------
+
+class GenerateCfg:
+    """The reference's GenerateCfg (runtime/session.hpp:42-45)."""
+
+    def __init__(self, max_new_tokens: int = 64, eos_token_id: int = -1):
+        self.max_new_tokens = max_new_tokens
+        self.eos_token_id = eos_token_id
+
+
+class Session:
+    """cdna3::runtime::Session (runtime/session.hpp:47-331) over the C ABI: loads a model
+    directory in the reference's export format onto the current device and runs greedy batch-1
+    generation. The session owns its own HIP stream; calls return after the device is done."""
+
+    def __init__(self, model_dir: str, max_seq: int = 4096):
+        handle = ctypes.c_void_p()
+        _check(lib().cdna3_session_create(os.fsencode(model_dir), max_seq, ctypes.byref(handle)),
+               "cdna3_session_create")
+        self._h = handle
+        self.max_seq = max_seq
+        cfg = ModelCfg()
+        _check(lib().cdna3_session_config(self._h, ctypes.byref(cfg)), "cdna3_session_config")
+        self.cfg = cfg
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) and self._h.value:
+            lib().cdna3_session_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @staticmethod
+    def _ids(ids):
+        import numpy as np
+        a = np.ascontiguousarray(np.asarray(ids, dtype=np.int32).reshape(-1))
+        return a, ctypes.c_void_p(a.ctypes.data)
+
+    def generate_ex(self, input_ids, cfg: Optional[GenerateCfg] = None, with_logits: bool = False) -> dict:
+        """Greedy generation. Returns {"tokens": generated ids, "logits": [steps][vocab] fp32 or
+        None, "ttft_ms": device time of the prompt, "decode_ms": device time of the other steps}."""
+        import numpy as np
+        cfg = cfg or GenerateCfg()
+        ids, ids_p = self._ids(input_ids)
+        n = max(1, cfg.max_new_tokens)
+        out = np.zeros(n, dtype=np.int32)
+        logits = np.zeros((n, self.cfg.vocab_size), dtype=np.float32) if with_logits else None
+        n_out, ttft, dec = ctypes.c_int(0), ctypes.c_float(0), ctypes.c_float(0)
+        _check(lib().cdna3_session_generate(self._h, ids_p, len(ids), cfg.max_new_tokens, cfg.eos_token_id,
+                                            ctypes.c_void_p(out.ctypes.data), ctypes.byref(n_out),
+                                            ctypes.c_void_p(0 if logits is None else logits.ctypes.data),
+                                            ctypes.byref(ttft), ctypes.byref(dec)), "cdna3_session_generate")
+        k = n_out.value
+        return {"tokens": out[:k].tolist(), "logits": None if logits is None else logits[:k],
+                "ttft_ms": ttft.value, "decode_ms": dec.value}
+
+    def generate(self, input_ids, cfg: Optional[GenerateCfg] = None) -> list:
+        """Session::generate: the prompt followed by the generated tokens."""
+        return [int(t) for t in input_ids] + self.generate_ex(input_ids, cfg)["tokens"]
+
+    def prefill_logits(self, input_ids):
+        """Session::prefill_logits: fp32 logits [vocab] of the last prompt token (numpy)."""
+        import numpy as np
+        ids, ids_p = self._ids(input_ids)
+        out = np.zeros(self.cfg.vocab_size, dtype=np.float32)
+        _check(lib().cdna3_session_prefill_logits(self._h, ids_p, len(ids), ctypes.c_void_p(out.ctypes.data)),
+               "cdna3_session_prefill_logits")
+        return out

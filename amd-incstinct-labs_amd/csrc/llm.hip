@@ -1,0 +1,490 @@
+// Layer-loop kernels of the small-LLM runtime (gfx950): embedding gather, fused norm + fp16 cast,
+// HBM-streaming GEMVs with fused epilogues for batch-1 decode, SiLU-gated product, bias add and a
+// device-side argmax.
+//
+// Reference behaviour restated (cdna3-prims/include/cdna3/runtime/forward.hpp): embed_gather_f32
+// (:174-187), rmsnorm_f32_kernel (:34-56) followed by rocBLAS's f32 -> f16 cast
+// (rocblas_gemm.hpp:36-41), the GEMM family Y = X W^T with W row-major [N][K] (:70-131,
+// rocblas_gemm.hpp:8-20), silu_mul_f32 (:154-160), add_f32 (:165-168), argmax (:244-262).
+//
+// MI355X design: a decode step of a 768-wide model is ~111 small launches that each stream one
+// weight matrix once, so every kernel here reads its weights with 16-byte loads and fuses what
+// the reference ran as separate passes (norm + cast; GEMV + bias; GEMV + residual add; gate and
+// up GEMVs + SiLU product). The next token id stays on the device (argmax writes it, the
+// embedding gather reads it), so decode steps queue back to back without a host round trip.
+// Cross-lane sums use the wave64 DPP butterfly; nothing uses LDS.
+#include "common.hpp"
+#include "wave_primitives/detail/xlane.hpp"
+#include <math.h>
+
+namespace cdna4 {
+namespace {
+
+using wave::xlane::allreduce;
+using wave::xlane::Max;
+using wave::xlane::Min;
+using wave::xlane::Sum;
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a), __builtin_bit_cast(h2_t, b), c, false);
+}
+__device__ __forceinline__ float dot8(const u32x4& a, const u32x4& b, float c) {
+    c = dot2(a[0], b[0], c);
+    c = dot2(a[1], b[1], c);
+    c = dot2(a[2], b[2], c);
+    return dot2(a[3], b[3], c);
+}
+
+// out[t][:] = float(embed[ids[t]][:]), one workgroup per token, 8 elements per lane step.
+__global__ __launch_bounds__(256) void embed_gather(const uint16_t* __restrict__ embed, const int* __restrict__ ids,
+                                                    float* __restrict__ out, int H, int V) {
+    const int t = blockIdx.x;
+    int id = ids[t];
+    id = id < 0 ? 0 : (id >= V ? V - 1 : id);
+    const uint16_t* src = embed + (size_t)id * H;
+    float* dst = out + (size_t)t * H;
+    if ((H & 7) == 0) {
+        for (int c = threadIdx.x; c < H / 8; c += 256) {
+            const u32x4 v = *(const u32x4*)(src + c * 8);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                dst[c * 8 + 2 * i] = f16_bits_to_f32(v[i] & 0xffffu);
+                dst[c * 8 + 2 * i + 1] = f16_bits_to_f32(v[i] >> 16);
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < H; i += 256) dst[i] = f16_bits_to_f32(src[i]);
+    }
+}
+
+// ---- a wave's share of one row ---------------------------------------------------------------
+// A row of K elements (K % 8 == 0) is C = K / 8 chunks of 8; lane l holds chunks c = l + 64 j for
+// j < J (zero past C). Every load is clamped to the row instead of branched around, so all of a
+// lane's loads are in flight together: one memory latency per kernel, not one per chunk.
+
+__device__ __forceinline__ int chunk(int lane, int j, int C) { return min(lane + 64 * j, C - 1); }
+
+template <int J>
+__device__ __forceinline__ void load_f16_row(const uint16_t* __restrict__ p, int C, int lane, u32x4 (&v)[J]) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) v[j] = __builtin_nontemporal_load((const u32x4*)p + chunk(lane, j, C));
+}
+
+template <int J>
+__device__ __forceinline__ void load_f32_row(const float* __restrict__ p, int C, int lane, f32x4 (&lo)[J],
+                                             f32x4 (&hi)[J]) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const f32x4* q = (const f32x4*)p + 2 * chunk(lane, j, C);
+        lo[j] = q[0];
+        hi[j] = q[1];
+    }
+}
+
+__device__ __forceinline__ float elem(const f32x4& lo, const f32x4& hi, int e) { return e < 4 ? lo[e] : hi[e - 4]; }
+__device__ __forceinline__ float half_of(const u32x4& v, int e) {
+    return f16_bits_to_f32(e & 1 ? v[e >> 1] >> 16 : v[e >> 1] & 0xffffu);
+}
+
+// Statistics of a row held as above: LayerNorm (kLayer) mean and 1/sqrt(var + eps) with var the
+// mean squared deviation from the mean (two passes over the registers); RMSNorm mean 0 and
+// 1/sqrt(mean(x^2) + eps). Cross-lane sums use the DPP butterfly.
+template <int J, bool kLayer>
+__device__ __forceinline__ void row_stats(const f32x4 (&lo)[J], const f32x4 (&hi)[J], int C, int lane, int K,
+                                          float eps, float& mean, float& inv) {
+    mean = 0.f;
+    if constexpr (kLayer) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            if (lane + 64 * j < C)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s += elem(lo[j], hi[j], e);
+        mean = allreduce(s, Sum{}) / (float)K;
+    }
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+        if (lane + 64 * j < C)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = elem(lo[j], hi[j], e) - mean;
+                q += d * d;
+            }
+    inv = 1.f / sqrtf(allreduce(q, Sum{}) / (float)K + eps);
+}
+
+// y = (x - mean) * inv * g (+ b) of element e of chunk j, in fp32.
+template <int J>
+__device__ __forceinline__ float normed(const f32x4 (&lo)[J], const f32x4 (&hi)[J], const u32x4 (&g)[J],
+                                        const u32x4 (&b)[J], bool has_b, int j, int e, float mean, float inv) {
+    float o = (elem(lo[j], hi[j], e) - mean) * inv * half_of(g[j], e);
+    if (has_b) o += half_of(b[j], e);
+    return o;
+}
+
+// Y[r][:] = norm(X[r][:]) * w + b for the prompt path, one wave per row, stored fp16 (the
+// projection input). kLayer = two-pass LayerNorm, else RMSNorm.
+template <int J, bool kLayer>
+__global__ __launch_bounds__(256) void norm_cast(const float* __restrict__ X, const uint16_t* __restrict__ W,
+                                                 const uint16_t* __restrict__ B, uint16_t* __restrict__ Y, int M,
+                                                 int H, float eps) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    const int C = H / 8;
+    f32x4 lo[J], hi[J];
+    u32x4 g[J], b[J];
+    load_f32_row<J>(X + (size_t)row * H, C, lane, lo, hi);
+    load_f16_row<J>(W, C, lane, g);
+    if (B) load_f16_row<J>(B, C, lane, b);
+    float mean, inv;
+    row_stats<J, kLayer>(lo, hi, C, lane, H, eps, mean, inv);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        if (lane + 64 * j >= C) continue;
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
+            o[e >> 1] = f32_to_f16_bits(normed<J>(lo, hi, g, b, B != nullptr, j, e, mean, inv)) |
+                        (f32_to_f16_bits(normed<J>(lo, hi, g, b, B != nullptr, j, e + 1, mean, inv)) << 16);
+        *((u32x4*)(Y + (size_t)row * H) + lane + 64 * j) = o;
+    }
+}
+
+// ---- decode-step GEMVs (batch 1) ---------------------------------------------------------------
+// y = W x with W row-major [rows][K] fp16 and fp32 accumulation. Each wave computes two rows; all
+// W and x loads of the wave are issued before any arithmetic. Variants:
+//   kResidual  x fp16, rows 2u, 2u + 1:  out32[r] += y                    (O and down projections)
+//   kQKV       x = norm(hidden) rounded to fp16 (the fused attention-input norm); unit u of the
+//              Q block (or K, V block) takes rows d and d + D/2 of one head, so the epilogue
+//              rounds y to fp16, adds the bias (rounded again, as the reference's GEMM + bias
+//              kernel do), applies rotate-half RoPE at position pos to Q and K, and writes Q
+//              head-major and K, V straight into the cache rows at pos
+//   kSiluMul   x = norm(hidden) rounded to fp16; rows n (gate) and F + n (up):
+//              act16[n] = fp16(silu(y_gate) * y_up)
+//   kLogits    x = final norm(hidden) in fp32 (unrounded, as the reference's lm_head reads it);
+//              rows 2u, 2u + 1: logits[r] = y, and the wave's (max, first index) pair goes to
+//              the argmax partials
+enum GemvKind { kResidual = 0, kQKV = 1, kSiluMul = 2, kLogits = 3 };
+
+struct GemvArgs {
+    const void* x;            // fp16 input (kResidual) or fp32 hidden row (the others)
+    const uint16_t* W;
+    const uint16_t* bias;     // kQKV: [QD + 2 KVD] or null
+    const uint16_t* gain;     // norm weight
+    const uint16_t* beta;     // norm bias or null
+    float eps;
+    void* out;                // kResidual: f32 [rows]; kSiluMul: f16 [F]; kLogits: f32 logits [V]
+    int units, K, rows;       // units = waves with work; rows = rows of W (kLogits: V)
+    // kQKV
+    uint16_t *q_out, *Kc, *Vc;
+    const float *cos_row, *sin_row;
+    int D, QD, KVD, pos, max_seq;
+    // kLogits
+    unsigned long long* partial;   // one (orderable value, ~index) key per wave
+};
+
+// Orderable 64-bit key of (value, index): a larger value wins, then a smaller index.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
+}
+
+template <int kKind, int J, bool kLayer>
+__global__ __launch_bounds__(256) void gemv2(GemvArgs a) {
+    const int unit = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (unit >= a.units) return;
+    const int K = a.K, C = K / 8;
+    int r0, r1;
+    if constexpr (kKind == kQKV) {
+        const int half = a.D / 2;
+        int base = 0, u = unit;
+        if (u >= a.QD / 2 + a.KVD / 2) { base = a.QD + a.KVD; u -= a.QD / 2 + a.KVD / 2; }
+        else if (u >= a.QD / 2) { base = a.QD; u -= a.QD / 2; }
+        r0 = base + (u / half) * a.D + u % half;
+        r1 = r0 + half;
+    } else if constexpr (kKind == kSiluMul) {
+        r0 = unit;
+        r1 = unit + a.rows / 2;
+    } else {
+        r0 = 2 * unit;
+        r1 = min(2 * unit + 1, a.rows - 1);
+    }
+    u32x4 w0[J], w1[J];
+    load_f16_row<J>(a.W + (size_t)r0 * K, C, lane, w0);
+    load_f16_row<J>(a.W + (size_t)r1 * K, C, lane, w1);
+    float y0 = 0.f, y1 = 0.f;
+    if constexpr (kKind == kResidual) {
+        u32x4 xv[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) xv[j] = ((const u32x4*)a.x)[chunk(lane, j, C)];
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            if (lane + 64 * j < C) {
+                y0 = dot8(w0[j], xv[j], y0);
+                y1 = dot8(w1[j], xv[j], y1);
+            }
+    } else {
+        f32x4 lo[J], hi[J];
+        u32x4 g[J], b[J];
+        load_f32_row<J>((const float*)a.x, C, lane, lo, hi);
+        load_f16_row<J>(a.gain, C, lane, g);
+        if (a.beta) load_f16_row<J>(a.beta, C, lane, b);
+        float mean, inv;
+        row_stats<J, kLayer>(lo, hi, C, lane, K, a.eps, mean, inv);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            if (lane + 64 * j >= C) continue;
+            if constexpr (kKind == kLogits) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float xe = normed<J>(lo, hi, g, b, a.beta != nullptr, j, e, mean, inv);
+                    y0 = fmaf(half_of(w0[j], e), xe, y0);
+                    y1 = fmaf(half_of(w1[j], e), xe, y1);
+                }
+            } else {
+                u32x4 xn;
+#pragma unroll
+                for (int e = 0; e < 8; e += 2)
+                    xn[e >> 1] = f32_to_f16_bits(normed<J>(lo, hi, g, b, a.beta != nullptr, j, e, mean, inv)) |
+                                 (f32_to_f16_bits(normed<J>(lo, hi, g, b, a.beta != nullptr, j, e + 1, mean, inv))
+                                  << 16);
+                y0 = dot8(w0[j], xn, y0);
+                y1 = dot8(w1[j], xn, y1);
+            }
+        }
+    }
+    y0 = allreduce(y0, Sum{});
+    y1 = allreduce(y1, Sum{});
+    if constexpr (kKind == kLogits) {
+        // every lane holds the sums: lane 0 stores, the wave's partial argmax needs no shuffle
+        if (lane == 0) {
+            float* lg = (float*)a.out;
+            lg[r0] = y0;
+            if (r1 != r0) lg[r1] = y1;
+            unsigned long long k0 = argmax_key(y0, r0), k1 = argmax_key(y1, r1);
+            a.partial[unit] = k0 > k1 ? k0 : k1;
+        }
+        return;
+    }
+    if (lane != 0) return;
+    if constexpr (kKind == kResidual) {
+        float* o = (float*)a.out;
+        o[r0] += y0;
+        if (r1 != r0) o[r1] += y1;
+    } else if constexpr (kKind == kSiluMul) {
+        ((uint16_t*)a.out)[r0] = (uint16_t)f32_to_f16_bits(y0 / (1.f + expf(-y0)) * y1);
+    } else {   // kQKV
+        uint32_t h0 = f32_to_f16_bits(y0), h1 = f32_to_f16_bits(y1);
+        if (a.bias) {
+            h0 = f32_to_f16_bits(f16_bits_to_f32(h0) + f16_bits_to_f32(a.bias[r0]));
+            h1 = f32_to_f16_bits(f16_bits_to_f32(h1) + f16_bits_to_f32(a.bias[r1]));
+        }
+        const int half = a.D / 2;
+        if (r0 < a.QD + a.KVD) {   // Q or K: rotate the pair (d, d + D/2)
+            const int d = (r0 % a.D);
+            const float t0 = f16_bits_to_f32(h0), t1 = f16_bits_to_f32(h1);
+            h0 = f32_to_f16_bits(t0 * a.cos_row[d] - t1 * a.sin_row[d]);
+            h1 = f32_to_f16_bits(t1 * a.cos_row[d + half] + t0 * a.sin_row[d + half]);
+        }
+        if (r0 < a.QD) {
+            a.q_out[r0] = (uint16_t)h0;
+            a.q_out[r1] = (uint16_t)h1;
+        } else {
+            const bool is_k = r0 < a.QD + a.KVD;
+            const int rr = r0 - (is_k ? a.QD : a.QD + a.KVD);
+            uint16_t* cache = (is_k ? a.Kc : a.Vc) + ((size_t)(rr / a.D) * a.max_seq + a.pos) * a.D + rr % a.D;
+            cache[0] = (uint16_t)h0;
+            cache[half] = (uint16_t)h1;
+        }
+    }
+}
+
+// Final argmax over the per-wave keys of the logits GEMV: one workgroup of 1024 lanes, each
+// folding a strided share (loads issued 8 at a time), then the DPP butterfly per wave and wave 0
+// over the 16 wave results. Writes the token to ids[0] (the next step's embedding input) and to
+// tokens[step].
+__global__ __launch_bounds__(1024) void argmax_keys(const unsigned long long* __restrict__ keys, int n,
+                                                    unsigned long long* __restrict__ scratch, int* __restrict__ ids,
+                                                    int* __restrict__ tokens, int step) {
+    unsigned long long best = 0;
+    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 1024) {
+        unsigned long long k[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) k[u] = (i0 + u * 1024 < n) ? keys[i0 + u * 1024] : 0ull;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) best = k[u] > best ? k[u] : best;
+    }
+    // wave max of 64-bit keys: high word first, then the low word among lanes holding that high word
+    uint32_t hi = (uint32_t)(best >> 32), lo = (uint32_t)best;
+    const uint32_t mhi = (uint32_t)allreduce((int)(hi ^ 0x80000000u), Max{}) ^ 0x80000000u;
+    const uint32_t mlo = (uint32_t)allreduce((int)((hi == mhi ? lo : 0u) ^ 0x80000000u), Max{}) ^ 0x80000000u;
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) scratch[wave] = ((unsigned long long)mhi << 32) | mlo;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const unsigned long long k = threadIdx.x < 16 ? scratch[threadIdx.x] : 0ull;
+        hi = (uint32_t)(k >> 32);
+        lo = (uint32_t)k;
+        const uint32_t h2 = (uint32_t)allreduce((int)(hi ^ 0x80000000u), Max{}) ^ 0x80000000u;
+        const uint32_t l2 = (uint32_t)allreduce((int)((hi == h2 ? lo : 0u) ^ 0x80000000u), Max{}) ^ 0x80000000u;
+        if (threadIdx.x == 0) {
+            const int tok = (int)(0xffffffffu - l2);
+            ids[0] = tok;
+            if (tokens) tokens[step] = tok;
+        }
+    }
+}
+
+// act[t][n] = fp16(silu(gu[t][n]) * gu[t][F + n]) for the prompt path (gu fp32 [T][2F]).
+__global__ __launch_bounds__(256) void silu_mul(const float* __restrict__ gu, uint16_t* __restrict__ act, int T,
+                                                int F) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)T * F) return;
+    const size_t t = i / F, n = i % F;
+    const float g = gu[t * 2 * F + n], u = gu[t * 2 * F + F + n];
+    act[i] = (uint16_t)f32_to_f16_bits(g / (1.f + expf(-g)) * u);
+}
+
+// Y[t][n] = fp16(Y[t][n] + b[n]) (QKV bias after the prompt GEMM).
+__global__ __launch_bounds__(256) void bias_add_f16(uint16_t* __restrict__ Y, const uint16_t* __restrict__ b, int T,
+                                                    int N) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)T * N) return;
+    Y[i] = (uint16_t)f32_to_f16_bits(f16_bits_to_f32(Y[i]) + f16_bits_to_f32(b[i % N]));
+}
+
+}  // namespace
+
+// ---- host-side launchers used by the runtime (csrc/session.hip) ---------------------------
+
+int llm_embed(const void* embed, const int* ids, float* out, int T, int H, int V, hipStream_t s) {
+    embed_gather<<<T, 256, 0, s>>>((const uint16_t*)embed, ids, out, H, V);
+    return launch_status();
+}
+
+namespace {
+// Smallest supported chunk count per lane for a row of K elements (K % 8 == 0; K <= 4096, or
+// K <= 8192 for the fp16-input GEMV).
+int chunks_per_lane(int K) {
+    const int j = (K / 8 + 63) / 64;
+    return j <= 1 ? 1 : j <= 2 ? 2 : j <= 3 ? 3 : j <= 4 ? 4 : j <= 6 ? 6 : j <= 8 ? 8 : j <= 12 ? 12 : j <= 16 ? 16 : 0;
+}
+
+template <int J>
+void norm_cast_launch(bool layer, const float* X, const void* W, const void* B, void* Y, int M, int H, float eps,
+                      hipStream_t s) {
+    const unsigned grid = ceil_div(M, 4);
+    if (layer)
+        norm_cast<J, true><<<grid, 256, 0, s>>>(X, (const uint16_t*)W, (const uint16_t*)B, (uint16_t*)Y, M, H, eps);
+    else
+        norm_cast<J, false><<<grid, 256, 0, s>>>(X, (const uint16_t*)W, (const uint16_t*)B, (uint16_t*)Y, M, H, eps);
+}
+
+template <int kKind, int J>
+void gemv_launch(bool layer, const GemvArgs& a, hipStream_t s) {
+    const unsigned grid = ceil_div(a.units, 4);
+    if (layer) gemv2<kKind, J, true><<<grid, 256, 0, s>>>(a);
+    else gemv2<kKind, J, false><<<grid, 256, 0, s>>>(a);
+}
+
+template <int kKind>
+int gemv_dispatch(bool layer, const GemvArgs& a, hipStream_t s) {
+    switch (chunks_per_lane(a.K)) {
+        case 1: gemv_launch<kKind, 1>(layer, a, s); break;
+        case 2: gemv_launch<kKind, 2>(layer, a, s); break;
+        case 3: gemv_launch<kKind, 3>(layer, a, s); break;
+        case 4: gemv_launch<kKind, 4>(layer, a, s); break;
+        case 6: gemv_launch<kKind, 6>(layer, a, s); break;
+        case 8: gemv_launch<kKind, 8>(layer, a, s); break;
+        case 12:
+            if constexpr (kKind == kResidual) { gemv_launch<kKind, 12>(layer, a, s); break; }
+            return CDNA4_ERR_INVALID_VALUE;
+        case 16:
+            if constexpr (kKind == kResidual) { gemv_launch<kKind, 16>(layer, a, s); break; }
+            return CDNA4_ERR_INVALID_VALUE;
+        default: return CDNA4_ERR_INVALID_VALUE;
+    }
+    return launch_status();
+}
+
+// Norm-fused kinds hold the fp32 row in registers: K <= 4096. The fp16-input GEMV: K <= 8192.
+bool gemv_shape_ok(int K, bool fp16_input = false) {
+    return K >= 8 && K % 8 == 0 && K <= (fp16_input ? 8192 : 4096);
+}
+}  // namespace
+
+int llm_norm_cast(bool layer, const float* X, const void* W, const void* B, void* Y, int M, int H, float eps,
+                  hipStream_t s) {
+    if (!gemv_shape_ok(H)) return CDNA4_ERR_INVALID_VALUE;
+    switch (chunks_per_lane(H)) {
+        case 1: norm_cast_launch<1>(layer, X, W, B, Y, M, H, eps, s); break;
+        case 2: norm_cast_launch<2>(layer, X, W, B, Y, M, H, eps, s); break;
+        case 3: norm_cast_launch<3>(layer, X, W, B, Y, M, H, eps, s); break;
+        case 4: norm_cast_launch<4>(layer, X, W, B, Y, M, H, eps, s); break;
+        case 6: norm_cast_launch<6>(layer, X, W, B, Y, M, H, eps, s); break;
+        default: norm_cast_launch<8>(layer, X, W, B, Y, M, H, eps, s); break;
+    }
+    return launch_status();
+}
+
+int llm_gemv_residual(const void* x, const void* W, float* out, int N, int K, hipStream_t s) {
+    if (!gemv_shape_ok(K, true) || N < 1) return CDNA4_ERR_INVALID_VALUE;
+    GemvArgs a{};
+    a.x = x; a.W = (const uint16_t*)W; a.out = out; a.K = K; a.rows = N; a.units = (N + 1) / 2;
+    return gemv_dispatch<kResidual>(false, a, s);
+}
+
+int llm_gemv_qkv(bool layer, const float* hidden, const void* gain, const void* beta, float eps, const void* W,
+                 const void* bias, int H, int D, int nH, int nKV, const float* cos_row, const float* sin_row,
+                 void* q_out, void* Kc, void* Vc, int pos, int max_seq, hipStream_t s) {
+    if (!gemv_shape_ok(H) || D % 2) return CDNA4_ERR_INVALID_VALUE;
+    GemvArgs a{};
+    a.x = hidden; a.W = (const uint16_t*)W; a.bias = (const uint16_t*)bias; a.gain = (const uint16_t*)gain;
+    a.beta = (const uint16_t*)beta; a.eps = eps; a.K = H;
+    a.D = D; a.QD = nH * D; a.KVD = nKV * D; a.rows = a.QD + 2 * a.KVD; a.units = a.rows / 2;
+    a.cos_row = cos_row; a.sin_row = sin_row; a.q_out = (uint16_t*)q_out; a.Kc = (uint16_t*)Kc;
+    a.Vc = (uint16_t*)Vc; a.pos = pos; a.max_seq = max_seq;
+    return gemv_dispatch<kQKV>(layer, a, s);
+}
+
+int llm_gemv_silu(bool layer, const float* hidden, const void* gain, const void* beta, float eps, const void* W,
+                  void* act, int F, int H, hipStream_t s) {
+    if (!gemv_shape_ok(H) || F < 1) return CDNA4_ERR_INVALID_VALUE;
+    GemvArgs a{};
+    a.x = hidden; a.W = (const uint16_t*)W; a.gain = (const uint16_t*)gain; a.beta = (const uint16_t*)beta;
+    a.eps = eps; a.out = act; a.K = H; a.rows = 2 * F; a.units = F;
+    return gemv_dispatch<kSiluMul>(layer, a, s);
+}
+
+size_t llm_argmax_partials(int V) { return (size_t)(V + 1) / 2; }
+
+int llm_logits_argmax(bool layer, const float* hidden, const void* gain, const void* beta, float eps,
+                      const void* W, float* logits, int V, int H, unsigned long long* partial,
+                      unsigned long long* scratch16, int* ids, int* tokens, int step, hipStream_t s) {
+    if (!gemv_shape_ok(H) || V < 1) return CDNA4_ERR_INVALID_VALUE;
+    GemvArgs a{};
+    a.x = hidden; a.W = (const uint16_t*)W; a.gain = (const uint16_t*)gain; a.beta = (const uint16_t*)beta;
+    a.eps = eps; a.out = logits; a.K = H; a.rows = V; a.units = (V + 1) / 2; a.partial = partial;
+    if (int e = gemv_dispatch<kLogits>(layer, a, s)) return e;
+    argmax_keys<<<1, 1024, 0, s>>>(partial, a.units, scratch16, ids, tokens, step);
+    return launch_status();
+}
+
+int llm_silu_mul(const float* gu, void* act, int T, int F, hipStream_t s) {
+    silu_mul<<<ceil_div((size_t)T * F, 256), 256, 0, s>>>(gu, (uint16_t*)act, T, F);
+    return launch_status();
+}
+
+int llm_bias_add_f16(void* Y, const void* b, int T, int N, hipStream_t s) {
+    bias_add_f16<<<ceil_div((size_t)T * N, 256), 256, 0, s>>>((uint16_t*)Y, (const uint16_t*)b, T, N);
+    return launch_status();
+}
+
+}  // namespace cdna4

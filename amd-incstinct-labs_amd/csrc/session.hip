@@ -1,0 +1,479 @@
+// Greedy batch-1 LLM session for gfx950: model loading and the layer loop of the reference's
+// runtime, on the library's own kernels.
+//
+// Reference behaviour restated (cdna3-prims/include/cdna3/runtime/): ModelLoader (model_loader.hpp:
+// 130-193, meta.json + one raw fp16 .bin per tensor), Session::run_layers (session.hpp:141-235:
+// norm, Q/K/V projections + bias, RoPE, KV append, causal prefill or strided decode, O projection
+// + residual, norm, SiLU-gated MLP + residual, final norm) and Session::generate / greedy_from_last
+// (session.hpp:262-338: prefill the prompt, then one token at a time, lm_head + argmax).
+//
+// MI355X design (host C++ over the library's kernels, one HIP stream per session):
+//   * Weights are loaded once; Q/K/V rows are concatenated into one matrix (and their biases into
+//     one vector), gate and up rows into one, so the decode step reads each as a single stream.
+//   * Prompt (T > 1): the projections are rocBLAS GEMMs (f16 in, f32 accumulate; the O and down
+//     projections accumulate into the fp32 residual with beta = 1), RoPE + KV append is one fused
+//     launch that also writes Q head-major, and the causal prefill reads K/V in place from the
+//     cache and writes O token-major for the O projection (no repacks).
+//   * Decode (T = 1): every projection is an HBM-streaming GEMV with its epilogue fused (bias,
+//     residual add, SiLU product); attention is the split-K decode over the strided cache.
+//   * The RoPE table for every position is built once on the device. The next token id never
+//     leaves the device: argmax writes it where the next step's embedding gather reads it, so a
+//     generation of N tokens is one queue of launches and one copy back at the end (unless an
+//     EOS id must be checked after each step).
+#include "common.hpp"
+#include <rocblas/rocblas.h>
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+#include <map>
+#include <string>
+#include <vector>
+
+namespace cdna4 {
+
+int llm_embed(const void* embed, const int* ids, float* out, int T, int H, int V, hipStream_t s);
+int llm_norm_cast(bool layer, const float* X, const void* W, const void* B, void* Y, int M, int H, float eps,
+                  hipStream_t s);
+int llm_gemv_residual(const void* x, const void* W, float* out, int N, int K, hipStream_t s);
+int llm_gemv_qkv(bool layer, const float* hidden, const void* gain, const void* beta, float eps, const void* W,
+                 const void* bias, int H, int D, int nH, int nKV, const float* cos_row, const float* sin_row,
+                 void* q_out, void* Kc, void* Vc, int pos, int max_seq, hipStream_t s);
+int llm_gemv_silu(bool layer, const float* hidden, const void* gain, const void* beta, float eps, const void* W,
+                  void* act, int F, int H, hipStream_t s);
+size_t llm_argmax_partials(int V);
+int llm_logits_argmax(bool layer, const float* hidden, const void* gain, const void* beta, float eps,
+                      const void* W, float* logits, int V, int H, unsigned long long* partial,
+                      unsigned long long* scratch16, int* ids, int* tokens, int step, hipStream_t s);
+int llm_silu_mul(const float* gu, void* act, int T, int F, hipStream_t s);
+int llm_bias_add_f16(void* Y, const void* b, int T, int N, hipStream_t s);
+
+namespace {
+
+#define CK(expr)                                   \
+    do {                                           \
+        const int e_ = (int)(expr);                \
+        if (e_ != 0) return e_;                    \
+    } while (0)
+
+// meta.json of the reference's exporter: one flat object of "key": value pairs.
+bool parse_meta(const std::string& path, std::map<std::string, std::string>& out) {
+    FILE* f = fopen(path.c_str(), "rb");
+    if (!f) return false;
+    std::string s;
+    char buf[4096];
+    size_t n;
+    while ((n = fread(buf, 1, sizeof buf, f)) > 0) s.append(buf, n);
+    fclose(f);
+    size_t i = 0;
+    auto skip = [&] { while (i < s.size() && strchr(" \t\r\n,{}", s[i])) ++i; };
+    while (true) {
+        skip();
+        if (i >= s.size() || s[i] != '"') break;
+        const size_t k0 = ++i;
+        while (i < s.size() && s[i] != '"') ++i;
+        const std::string key = s.substr(k0, i - k0);
+        ++i;
+        while (i < s.size() && (s[i] == ' ' || s[i] == ':')) ++i;
+        std::string val;
+        if (i < s.size() && s[i] == '"') {
+            const size_t v0 = ++i;
+            while (i < s.size() && s[i] != '"') ++i;
+            val = s.substr(v0, i - v0);
+            ++i;
+        } else {
+            const size_t v0 = i;
+            while (i < s.size() && !strchr(",}\r\n", s[i])) ++i;
+            val = s.substr(v0, i - v0);
+            while (!val.empty() && val.back() == ' ') val.pop_back();
+        }
+        out[key] = val;
+    }
+    return true;
+}
+
+// Appends the raw fp16 tensor at path (exactly `count` elements) to host.
+bool read_f16(const std::string& path, size_t count, std::vector<uint16_t>& host) {
+    FILE* f = fopen(path.c_str(), "rb");
+    if (!f) return false;
+    const size_t at = host.size();
+    host.resize(at + count);
+    const size_t got = fread(host.data() + at, 2, count, f);
+    char extra;
+    const bool more = fread(&extra, 1, 1, f) == 1;
+    fclose(f);
+    return got == count && !more;
+}
+
+struct Layer {
+    uint16_t *wqkv = nullptr, *bqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wdown = nullptr;
+    uint16_t *n_attn = nullptr, *n_attn_b = nullptr, *n_mlp = nullptr, *n_mlp_b = nullptr;
+};
+
+}  // namespace
+
+struct Session {
+    cdna3_model_cfg c{};
+    int max_seq = 0;
+    std::vector<Layer> L;
+    uint16_t *embed = nullptr, *lm_head = nullptr, *fnorm = nullptr, *fnorm_b = nullptr;
+    uint16_t *Kc = nullptr, *Vc = nullptr;            // [layers][nKVH][max_seq][D]
+    float *cos_tab = nullptr, *sin_tab = nullptr;     // [max_seq][D]
+    void* dec_ws = nullptr;
+    size_t dec_ws_bytes = 0;
+    rocblas_handle blas = nullptr;
+    hipStream_t stream = nullptr;
+    std::vector<void*> allocs;
+    // scratch, sized for `cap` tokens
+    int cap = 0;
+    float *hidden = nullptr, *gu = nullptr, *logits = nullptr;
+    unsigned long long *partial = nullptr, *scratch16 = nullptr;
+    uint16_t *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qh = nullptr, *attn = nullptr, *act = nullptr;
+    int *ids = nullptr, *tokens = nullptr;
+    std::vector<void*> scratch;
+
+    int dmalloc(void** p, size_t bytes, bool is_scratch = false) {
+        CK(hipMalloc(p, bytes ? bytes : 16));
+        (is_scratch ? scratch : allocs).push_back(*p);
+        return 0;
+    }
+    int upload(uint16_t** dst, const std::vector<uint16_t>& host) {
+        CK(dmalloc((void**)dst, host.size() * 2));
+        CK(hipMemcpy(*dst, host.data(), host.size() * 2, hipMemcpyHostToDevice));
+        return 0;
+    }
+    int qd() const { return c.n_heads * c.head_dim; }
+    int kvd() const { return c.n_kv_heads * c.head_dim; }
+    size_t layer_kv() const { return (size_t)c.n_kv_heads * max_seq * c.head_dim; }
+
+    int read_config(const std::string& dir);
+    int load(const std::string& dir);
+    int reserve(int T);
+    int gemm(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, float beta, int M, int N, int K, int ldy);
+    int run_layers(int T, int pos0);
+    int prefill(const int* host_ids, int T);
+    int check_ids(const int* host_ids, int T) const {
+        if (T < 1 || T > max_seq) return CDNA4_ERR_INVALID_VALUE;
+        for (int i = 0; i < T; ++i)
+            if (host_ids[i] < 0 || host_ids[i] >= c.vocab_size) return CDNA4_ERR_INVALID_VALUE;
+        return 0;
+    }
+    int last_token_logits(int T, int step);
+    void release();
+};
+
+// meta.json -> c, validated; host only (runs before any device call).
+int Session::read_config(const std::string& dir) {
+    std::map<std::string, std::string> meta;
+    if (!parse_meta(dir + "/meta.json", meta)) return CDNA4_ERR_INVALID_VALUE;
+    auto geti = [&](const char* k, int def) { return meta.count(k) ? atoi(meta[k].c_str()) : def; };
+    c.n_layers = geti("n_layers", 0);
+    c.hidden = geti("hidden", 0);
+    c.n_heads = geti("n_heads", 0);
+    c.n_kv_heads = geti("n_kv_heads", c.n_heads);
+    c.head_dim = geti("head_dim", c.n_heads ? c.hidden / c.n_heads : 0);
+    c.ffn_dim = geti("ffn_dim", 0);
+    c.vocab_size = geti("vocab_size", 0);
+    c.rope_theta = meta.count("rope_theta") ? (float)atof(meta["rope_theta"].c_str()) : 10000.f;
+    c.qkv_bias = meta.count("qkv_bias") && (meta["qkv_bias"] == "1" || meta["qkv_bias"] == "true");
+    c.layernorm = meta.count("norm") && meta["norm"] == "layernorm";
+    c.norm_eps = meta.count("norm_eps") ? (float)atof(meta["norm_eps"].c_str()) : (c.layernorm ? 1e-5f : 1e-6f);
+    const int H = c.hidden, F = c.ffn_dim, V = c.vocab_size, D = c.head_dim;
+    if (c.n_layers < 1 || H < 8 || H % 8 || H > 4096 || c.n_heads < 1 || c.n_kv_heads < 1 ||
+        c.n_heads % c.n_kv_heads || (D != 64 && D != 128) || F < 8 || F % 8 || F > 8192 || V < 1 || !(c.rope_theta > 0.f) ||
+        !(c.norm_eps >= 0.f))
+        return CDNA4_ERR_INVALID_VALUE;
+    return 0;
+}
+
+// Weights (Q|K|V and gate|up concatenated), KV cache, RoPE table, workspaces, rocBLAS handle.
+int Session::load(const std::string& dir) {
+    const int H = c.hidden, F = c.ffn_dim, V = c.vocab_size, D = c.head_dim;
+    auto p = [&](const std::string& name) { return dir + "/" + name + ".bin"; };
+    std::vector<uint16_t> h;
+    auto one = [&](const std::string& name, size_t count, uint16_t** dst) -> int {
+        h.clear();
+        if (!read_f16(p(name), count, h)) return CDNA4_ERR_INVALID_VALUE;
+        return upload(dst, h);
+    };
+    auto optional = [&](const std::string& name, size_t count, uint16_t** dst) -> int {
+        FILE* f = fopen(p(name).c_str(), "rb");
+        if (!f) return 0;
+        fclose(f);
+        return one(name, count, dst);
+    };
+    CK(one("embed_tokens", (size_t)V * H, &embed));
+    CK(one("lm_head", (size_t)V * H, &lm_head));
+    CK(one("final_norm", H, &fnorm));
+    CK(optional("final_norm_bias", H, &fnorm_b));
+    L.resize(c.n_layers);
+    for (int i = 0; i < c.n_layers; ++i) {
+        const std::string lp = "layer_" + std::to_string(i) + "_";
+        Layer& l = L[i];
+        h.clear();
+        if (!read_f16(p(lp + "q_proj"), (size_t)qd() * H, h) || !read_f16(p(lp + "k_proj"), (size_t)kvd() * H, h) ||
+            !read_f16(p(lp + "v_proj"), (size_t)kvd() * H, h))
+            return CDNA4_ERR_INVALID_VALUE;
+        CK(upload(&l.wqkv, h));
+        if (c.qkv_bias) {
+            h.clear();
+            if (!read_f16(p(lp + "q_bias"), qd(), h) || !read_f16(p(lp + "k_bias"), kvd(), h) ||
+                !read_f16(p(lp + "v_bias"), kvd(), h))
+                return CDNA4_ERR_INVALID_VALUE;
+            CK(upload(&l.bqkv, h));
+        }
+        CK(one(lp + "o_proj", (size_t)H * qd(), &l.wo));
+        h.clear();
+        if (!read_f16(p(lp + "gate_proj"), (size_t)F * H, h) || !read_f16(p(lp + "up_proj"), (size_t)F * H, h))
+            return CDNA4_ERR_INVALID_VALUE;
+        CK(upload(&l.wgu, h));
+        CK(one(lp + "down_proj", (size_t)H * F, &l.wdown));
+        CK(one(lp + "norm_attn", H, &l.n_attn));
+        CK(one(lp + "norm_mlp", H, &l.n_mlp));
+        CK(optional(lp + "norm_attn_bias", H, &l.n_attn_b));
+        CK(optional(lp + "norm_mlp_bias", H, &l.n_mlp_b));
+    }
+    // KV cache, RoPE table for every position, decode workspace for any length up to max_seq.
+    CK(dmalloc((void**)&Kc, layer_kv() * c.n_layers * 2));
+    CK(dmalloc((void**)&Vc, layer_kv() * c.n_layers * 2));
+    CK(dmalloc((void**)&cos_tab, (size_t)max_seq * D * 4));
+    CK(dmalloc((void**)&sin_tab, (size_t)max_seq * D * 4));
+    CK(cdna3_rope_table_f32(cos_tab, sin_tab, 0, max_seq, D, c.rope_theta, (cdna4_stream_t)stream));
+    for (int n = 1; n <= max_seq; ++n) {   // the split count is not monotonic in n: take the max
+        cdna3_decode_cfg dc{D, n, c.n_heads, c.n_kv_heads, 1, max_seq};
+        const size_t b = cdna3_attn_decode_workspace_size(&dc);
+        if (b > dec_ws_bytes) dec_ws_bytes = b;
+    }
+    CK(dmalloc(&dec_ws, dec_ws_bytes));
+    CK(dmalloc((void**)&logits, (size_t)V * 4));
+    CK(dmalloc((void**)&partial, llm_argmax_partials(V) * 8));
+    CK(dmalloc((void**)&scratch16, 16 * 8));
+    if (rocblas_create_handle(&blas) != rocblas_status_success) return CDNA4_ERR_INVALID_VALUE;
+    if (rocblas_set_stream(blas, stream) != rocblas_status_success) return CDNA4_ERR_INVALID_VALUE;
+    return (int)hipStreamSynchronize(stream);
+}
+
+int Session::reserve(int T) {
+    if (T <= cap) return 0;
+    for (void* ptr : scratch) (void)hipFree(ptr);
+    scratch.clear();
+    const size_t H = c.hidden, F = c.ffn_dim;
+    CK(dmalloc((void**)&hidden, T * H * 4, true));
+    CK(dmalloc((void**)&gu, T * 2 * F * 4, true));
+    CK(dmalloc((void**)&xn, T * (H > F ? H : F) * 2, true));
+    CK(dmalloc((void**)&q, (size_t)T * (qd() + 2 * kvd()) * 2, true));
+    k = q + (size_t)T * qd();
+    v = k + (size_t)T * kvd();
+    CK(dmalloc((void**)&qh, (size_t)T * qd() * 2, true));
+    CK(dmalloc((void**)&attn, (size_t)T * qd() * 2, true));
+    CK(dmalloc((void**)&act, T * F * 2, true));
+    CK(dmalloc((void**)&ids, (size_t)T * 4, true));
+    CK(dmalloc((void**)&tokens, (size_t)(max_seq + 1) * 4, true));
+    cap = T;
+    return 0;
+}
+
+// Row-major Y[M][N] (leading dimension ldy) = X[M][K] W[N][K]^T + beta Y, fp16 X and W, fp32
+// accumulation, fp32 or fp16 Y. rocBLAS is column-major: row-major Y is column-major Y^T [N][M],
+// and Y^T = W X^T, where the row-major W [N][K] read column-major is W^T (so op(A) = transpose,
+// lda = K) and the row-major X [M][K] read column-major is X^T (op(B) = none, ldb = K). The
+// reference derives the same call (rocblas_gemm.hpp:8-20).
+int Session::gemm(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, float beta, int M, int N, int K,
+                  int ldy) {
+    const float alpha = 1.f;
+    const rocblas_datatype yt = y_f32 ? rocblas_datatype_f32_r : rocblas_datatype_f16_r;
+    const rocblas_status st = rocblas_gemm_ex(blas, rocblas_operation_transpose, rocblas_operation_none, N, M, K,
+                                              &alpha, W, rocblas_datatype_f16_r, K, X, rocblas_datatype_f16_r, K,
+                                              &beta, Y, yt, ldy, Y, yt, ldy, rocblas_datatype_f32_r,
+                                              rocblas_gemm_algo_standard, 0, 0);
+    return st == rocblas_status_success ? 0 : CDNA4_ERR_INVALID_VALUE;
+}
+
+int Session::run_layers(int T, int pos0) {
+    const int H = c.hidden, F = c.ffn_dim, D = c.head_dim, nH = c.n_heads, nKV = c.n_kv_heads;
+    const int QD = qd(), KVD = kvd();
+    const bool lnorm = c.layernorm != 0;
+    const float eps = c.norm_eps;
+    const cdna4_stream_t s = (cdna4_stream_t)stream;
+    for (int li = 0; li < c.n_layers; ++li) {
+        const Layer& l = L[li];
+        uint16_t* Kl = Kc + layer_kv() * li;
+        uint16_t* Vl = Vc + layer_kv() * li;
+        if (T == 1) {
+            // decode step: five launches and the attention; every GEMV streams its weights once
+            CK(llm_gemv_qkv(lnorm, hidden, l.n_attn, l.n_attn_b, eps, l.wqkv, l.bqkv, H, D, nH, nKV,
+                            cos_tab + (size_t)pos0 * D, sin_tab + (size_t)pos0 * D, qh, Kl, Vl, pos0, max_seq,
+                            stream));
+            cdna3_decode_cfg dc{D, pos0 + 1, nH, nKV, 1, max_seq};
+            CK(cdna3_attn_decode(qh, Kl, Vl, attn, &dc, CDNA4_F16, dec_ws, dec_ws_bytes, s));
+            CK(llm_gemv_residual(attn, l.wo, hidden, H, QD, stream));
+            CK(llm_gemv_silu(lnorm, hidden, l.n_mlp, l.n_mlp_b, eps, l.wgu, act, F, H, stream));
+            CK(llm_gemv_residual(act, l.wdown, hidden, H, F, stream));
+            continue;
+        }
+        CK(llm_norm_cast(lnorm, hidden, l.n_attn, l.n_attn_b, xn, T, H, eps, stream));
+        CK(gemm(xn, l.wqkv, q, false, 0.f, T, QD, H, QD));
+        CK(gemm(xn, l.wqkv + (size_t)QD * H, k, false, 0.f, T, KVD, H, KVD));
+        CK(gemm(xn, l.wqkv + (size_t)(QD + KVD) * H, v, false, 0.f, T, KVD, H, KVD));
+        if (l.bqkv) {
+            CK(llm_bias_add_f16(q, l.bqkv, T, QD, stream));
+            CK(llm_bias_add_f16(k, l.bqkv + QD, T, KVD, stream));
+            CK(llm_bias_add_f16(v, l.bqkv + QD + KVD, T, KVD, stream));
+        }
+        CK(cdna3_rope_append_kv_f16(q, k, v, qh, Kl, Vl, cos_tab + (size_t)pos0 * D, sin_tab + (size_t)pos0 * D, T,
+                                    nH, nKV, D, pos0, max_seq, s));
+        // Prompt from an empty cache (pos0 == 0): causal over the T cached keys, read in place;
+        // O written token-major for the O projection.
+        cdna3_prefill_cfg pc{D, T, T, nH, nKV, 1, 1};
+        cdna3_prefill_strides ps;
+        ps.q_row = D; ps.q_head = (long long)T * D; ps.q_batch = ps.q_head * nH;
+        ps.kv_row = D; ps.kv_head = (long long)max_seq * D; ps.kv_batch = ps.kv_head * nKV;
+        ps.o_row = QD; ps.o_head = D; ps.o_batch = (long long)T * QD;
+        CK(cdna3_attn_prefill_strided(qh, Kl, Vl, attn, &pc, &ps, CDNA4_F16, s));
+        CK(gemm(attn, l.wo, hidden, true, 1.f, T, H, QD, H));
+        CK(llm_norm_cast(lnorm, hidden, l.n_mlp, l.n_mlp_b, xn, T, H, eps, stream));
+        CK(gemm(xn, l.wgu, gu, true, 0.f, T, 2 * F, H, 2 * F));
+        CK(llm_silu_mul(gu, act, T, F, stream));
+        CK(gemm(act, l.wdown, hidden, true, 1.f, T, H, F, H));
+    }
+    return 0;
+}
+
+// Prompt of T tokens from an empty cache: embedding, every layer, final norm + lm_head + argmax of
+// the last token (ids[0] then holds the first generated token).
+int Session::prefill(const int* host_ids, int T) {
+    CK(reserve(T));
+    CK(hipMemcpyAsync(ids, host_ids, (size_t)T * 4, hipMemcpyHostToDevice, stream));
+    CK(llm_embed(embed, ids, hidden, T, c.hidden, c.vocab_size, stream));
+    CK(run_layers(T, 0));
+    return last_token_logits(T, 0);
+}
+
+// Final norm of the last of T rows, lm_head and argmax: the token goes to ids[0] (the next step's
+// input) and tokens[step].
+int Session::last_token_logits(int T, int step) {
+    return llm_logits_argmax(c.layernorm != 0, hidden + (size_t)(T - 1) * c.hidden, fnorm, fnorm_b, c.norm_eps,
+                             lm_head, logits, c.vocab_size, c.hidden, partial, scratch16, ids, tokens, step, stream);
+}
+
+void Session::release() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (void* ptr : scratch) (void)hipFree(ptr);
+    for (void* ptr : allocs) (void)hipFree(ptr);
+    scratch.clear();
+    allocs.clear();
+    if (blas) rocblas_destroy_handle(blas);
+    if (stream) (void)hipStreamDestroy(stream);
+    blas = nullptr;
+    stream = nullptr;
+}
+
+}  // namespace cdna4
+
+using namespace cdna4;
+
+struct cdna3_session {
+    Session impl;
+};
+
+extern "C" int cdna3_session_create(const char* model_dir, int max_seq, cdna3_session** out) {
+    if (!model_dir || !out || max_seq < 1) return CDNA4_ERR_INVALID_VALUE;
+    *out = nullptr;
+    cdna3_session* s = new cdna3_session();
+    s->impl.max_seq = max_seq;
+    if (int e = s->impl.read_config(model_dir)) {
+        delete s;
+        return e;
+    }
+    if (int e = check_device()) {
+        delete s;
+        return e;
+    }
+    int e = (int)hipStreamCreateWithFlags(&s->impl.stream, hipStreamNonBlocking);
+    if (e == 0) e = s->impl.load(model_dir);
+    if (e != 0) {
+        s->impl.release();
+        delete s;
+        return e;
+    }
+    *out = s;
+    return 0;
+}
+
+extern "C" void cdna3_session_destroy(cdna3_session* s) {
+    if (!s) return;
+    s->impl.release();
+    delete s;
+}
+
+extern "C" int cdna3_session_config(const cdna3_session* s, cdna3_model_cfg* out) {
+    if (!s || !out) return CDNA4_ERR_INVALID_VALUE;
+    *out = s->impl.c;
+    return 0;
+}
+
+extern "C" int cdna3_session_generate(cdna3_session* s, const int* ids, int n_ids, int max_new_tokens,
+                                      int eos_token_id, int* out_tokens, int* n_out, float* step_logits,
+                                      float* ttft_ms, float* decode_ms) {
+    if (!s || !ids || n_ids < 1 || max_new_tokens < 1 || !out_tokens || !n_out) return CDNA4_ERR_INVALID_VALUE;
+    Session& S = s->impl;
+    if (int e = S.check_ids(ids, n_ids)) return e;
+    if (int e = check_device()) return e;
+    *n_out = 0;
+    // Decode step `step` writes cache row n_ids + step - 1; the reference stops once the cache
+    // is full (session.hpp:283-284).
+    if (max_new_tokens > S.max_seq - n_ids + 1) max_new_tokens = S.max_seq - n_ids + 1;
+    CK(S.reserve(n_ids));   // before e0: a first call's allocations are not part of the timings
+    hipEvent_t e0, e1, e2;
+    CK(hipEventCreate(&e0));
+    CK(hipEventCreate(&e1));
+    CK(hipEventCreate(&e2));
+    int rc = 0;
+    const size_t V = S.c.vocab_size;
+    auto body = [&]() -> int {
+        CK(hipEventRecord(e0, S.stream));
+        CK(S.prefill(ids, n_ids));
+        if (step_logits) CK(hipMemcpyAsync(step_logits, S.logits, V * 4, hipMemcpyDeviceToHost, S.stream));
+        CK(hipEventRecord(e1, S.stream));
+        int produced = 1;
+        for (int step = 1; step < max_new_tokens; ++step) {
+            if (eos_token_id >= 0) {
+                int last = -1;
+                CK(hipMemcpyAsync(&last, S.ids, 4, hipMemcpyDeviceToHost, S.stream));
+                CK(hipStreamSynchronize(S.stream));
+                if (last == eos_token_id) break;
+            }
+            const int pos = n_ids + step - 1;
+            CK(llm_embed(S.embed, S.ids, S.hidden, 1, S.c.hidden, S.c.vocab_size, S.stream));
+            CK(S.run_layers(1, pos));
+            CK(S.last_token_logits(1, step));
+            if (step_logits)
+                CK(hipMemcpyAsync(step_logits + (size_t)step * V, S.logits, V * 4, hipMemcpyDeviceToHost, S.stream));
+            ++produced;
+        }
+        CK(hipEventRecord(e2, S.stream));
+        CK(hipMemcpyAsync(out_tokens, S.tokens, (size_t)produced * 4, hipMemcpyDeviceToHost, S.stream));
+        CK(hipStreamSynchronize(S.stream));
+        *n_out = produced;
+        float t = 0.f;
+        CK(hipEventElapsedTime(&t, e0, e1));
+        if (ttft_ms) *ttft_ms = t;
+        CK(hipEventElapsedTime(&t, e1, e2));
+        if (decode_ms) *decode_ms = t;
+        return 0;
+    };
+    rc = body();
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipEventDestroy(e2);
+    return rc;
+}
+
+extern "C" int cdna3_session_prefill_logits(cdna3_session* s, const int* ids, int n_ids, float* logits) {
+    if (!s || !ids || !logits) return CDNA4_ERR_INVALID_VALUE;
+    Session& S = s->impl;
+    if (int e = S.check_ids(ids, n_ids)) return e;
+    if (int e = check_device()) return e;
+    CK(S.prefill(ids, n_ids));
+    CK(hipMemcpyAsync(logits, S.logits, (size_t)S.c.vocab_size * 4, hipMemcpyDeviceToHost, S.stream));
+    return (int)hipStreamSynchronize(S.stream);
+}

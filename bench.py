@@ -12,7 +12,12 @@ Also reported in the same line:
           Infinity Cache cannot serve repeats) in GB/s of algorithmic bytes;
   cfg1:   BASELINE config 1, the reference's FA2 configuration, fp32 and fp16 arms;
   copy_1GiB: a plain device copy, the achievable-bandwidth reference and the known-size kernel
-          that calibrates the HBM traffic counters.
+          that calibrates the HBM traffic counters;
+  llm:    BASELINE config 5, the small-LLM runtime (12 layers, d 768, 12 heads of 64, MLP 3072,
+          vocab 32000, random-init fp16 weights N(0, 0.02), LayerNorm gains 1 and betas 0): greedy
+          decode of 128 tokens after a 512-token prompt of seeded random ids, in tokens/s over the
+          decode phase, with the time to the first token separately, and the CPU oracle's decode
+          step beside it.
 Kernel durations come from HIP events recorded on the stream the kernels run on (torch's current
 stream). The CPU baseline times the reference's own fp32 cpu_prefill (built from the reference
 sources into oracle/_ref) on one (batch, head) of config 3, one thread; the oracle's restatement
@@ -40,7 +45,7 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["all", "prefill", "decode", "dpp", "cfg1", "copy"], default="all")
+    p.add_argument("--only", choices=["all", "prefill", "decode", "dpp", "cfg1", "copy", "llm"], default="all")
     return p.parse_args()
 
 
@@ -199,11 +204,66 @@ def bench_copy(torch, steps, warmup):
             "bytes_read": 4 * n, "bytes_written": 4 * n}
 
 
+def bench_llm(steps):
+    """BASELINE config 5 through cdna4.Session (the C ABI session): `steps` generations of 128
+    tokens after the same 512-token prompt, after one untimed warm-up generation. Decode tokens/s
+    = 127 decode steps / the device time between the first token and the last (median run)."""
+    import tempfile
+    import numpy as np
+    import cdna4
+    from cdna4 import model_format as mf
+    L, H, nH, F, V, prompt, new = 12, 768, 12, 3072, 32000, 512, 128
+    with tempfile.TemporaryDirectory(prefix="cfg5_") as d:
+        meta = mf.random_model(d, n_layers=L, hidden=H, n_heads=nH, ffn_dim=F, vocab_size=V, norm="layernorm", seed=5)
+        ids = np.random.default_rng(5).integers(0, V, prompt).astype(np.int32)
+        with cdna4.Session(d, max_seq=prompt + new) as s:
+            s.generate_ex(ids, cdna4.GenerateCfg(new))
+            runs = [s.generate_ex(ids, cdna4.GenerateCfg(new)) for _ in range(max(1, steps))]
+        cpu = None if os.environ.get("CDNA4_NO_CPU_BASELINE") else cpu_baseline_llm(d, prompt)
+    runs.sort(key=lambda r: r["decode_ms"])
+    r = runs[len(runs) // 2]
+    n_dec = len(r["tokens"]) - 1
+    ms_tok = r["decode_ms"] / n_dec
+    params = L * (4 * H * H + 3 * H * F) + V * H                # lm_head; the embedding is a row gather
+    kv_bytes = 2 * L * H * 2 * (prompt + new / 2)                 # mean cache read per decode step
+    gbs = (2 * params + kv_bytes) / (ms_tok * 1e-3) / 1e9
+    out = {"value": 1e3 / ms_tok, "unit": "tokens/s", "ms_per_token": ms_tok, "ttft_ms": r["ttft_ms"],
+           "tokens": len(r["tokens"]), "runs": len(runs),
+           "config": {"workload": "small-LLM greedy decode, BASELINE config 5", "layers": L, "d_model": H,
+                      "heads": nH, "head_dim": H // nH, "mlp": F, "vocab": V, "prompt": prompt, "new_tokens": new,
+                      "norm": meta.get("norm"), "dtype": "fp16"},
+           "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                        "frac": gbs / PEAK_HBM_GBS, "traffic": None,
+                        "bytes_per_token": 2 * params + kv_bytes}}
+    if cpu:
+        out["cpu_baseline"] = cpu
+    return out
+
+
+def cpu_baseline_llm(model_dir, pos):
+    """The oracle's decode step (oracle/llm.c, one thread) for config 5: four tokens at positions
+    pos .. pos+3 over a zero-filled cache (attention cost at these positions is <1% of a step)."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    import oracle
+    from cdna4 import model_format as mf
+    meta, t = mf.read_model(model_dir)
+    m = oracle.LLM(meta, t, pos + 8)
+    m.pos = pos
+    n = 4
+    t0 = time.perf_counter()
+    for i in range(n):
+        m.forward([i])
+    dt = (time.perf_counter() - t0) / n
+    return {"value": 1.0 / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"4 decode steps at positions {pos}..{pos + 3}, {dt * 1e3:.0f} ms per token"}
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build runs on one GPU only; multi-GPU runs are not part of it "
-              "(see DESIGN.md, 'More than one GPU').", file=sys.stderr)
+        print("bench.py: this build runs on one GPU only; how the hot path would shard across GPUs is a "
+              "design note, not part of the build.", file=sys.stderr)
         sys.exit(2)
     import torch
     import cdna4
@@ -229,6 +289,14 @@ def main():
         result["cfg1"] = bench_cfg1(torch, cdna4, args.steps, args.warmup)
     if args.only in ("all", "copy"):
         result["copy_1GiB"] = bench_copy(torch, args.steps, args.warmup)
+    if args.only in ("all", "llm"):
+        if args.no_cpu_baseline:
+            os.environ["CDNA4_NO_CPU_BASELINE"] = "1"
+        result["llm"] = bench_llm(min(args.steps, 5))
+        if "value" not in result:
+            l = result["llm"]
+            result.update({"value": l["value"], "unit": l["unit"], "ms_per_step": l["ms_per_token"],
+                           "config": l["config"], "roofline": l["roofline"], "dtype": "fp16"})
     if args.only in ("all", "prefill") and not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_prefill()
     print(json.dumps(result), flush=True)

@@ -194,6 +194,56 @@ int cdna3_rope_append_kv_f16(const void* q, const void* k, const void* v, void* 
                              const float* sin_tab, int T, int nQH, int nKVH, int D, int pos0,
                              int max_seq, cdna4_stream_t stream);
 
+/* ---- small-LLM runtime session ------------------------------------------------
+ * Replaces cdna3::runtime::Session (cdna3-prims/include/cdna3/runtime/session.hpp:47-331) with
+ * its ModelLoader (model_loader.hpp:130-193) and KVCache (kv_cache.hpp:19-52): greedy batch-1
+ * generation over a decoder read from the reference's export format, a directory holding
+ * meta.json (flat keys n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn_dim, vocab_size,
+ * rope_theta, qkv_bias) and one raw little-endian fp16 .bin per tensor: embed_tokens,
+ * lm_head [vocab][hidden], final_norm [hidden], layer_<i>_{q,k,v,o,gate,up,down}_proj
+ * (row-major [out][in]), layer_<i>_{q,k,v}_bias when qkv_bias, layer_<i>_norm_{attn,mlp}.
+ * Extensions (absent keys keep the reference's behaviour): "norm": "layernorm" selects two-pass
+ * LayerNorm (eps 1e-5) instead of RMSNorm (eps 1e-6), with optional *_norm_*_bias /
+ * final_norm_bias tensors as beta; "norm_eps" overrides eps.
+ * Numerics follow the reference: fp32 residual stream, fp16 activations into each projection
+ * with fp32 accumulation, fp16 Q/K/V and KV cache, fp32 SiLU product; logits are kept in fp32
+ * and argmax takes the first index of the maximum.
+ * The session owns one HIP stream, a rocBLAS handle, the weights and the KV cache
+ * [layers][n_kv_heads][max_seq][head_dim]. Calls on one session must not overlap.
+ */
+typedef struct cdna3_session cdna3_session;
+
+typedef struct {
+    int n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn_dim, vocab_size;
+    float rope_theta;
+    int qkv_bias;    /* 1: per-layer q/k/v biases */
+    int layernorm;   /* 1: LayerNorm, 0: RMSNorm */
+    float norm_eps;
+} cdna3_model_cfg;
+
+/* Session(model_dir, max_seq) (session.hpp:254-260): loads the model onto the current device.
+ * Invalid: unreadable or short files, head_dim not 64/128, n_heads % n_kv_heads != 0, hidden or
+ * ffn_dim not a multiple of 8, hidden > 4096. */
+int cdna3_session_create(const char* model_dir, int max_seq, cdna3_session** out);
+void cdna3_session_destroy(cdna3_session* session);
+int cdna3_session_config(const cdna3_session* session, cdna3_model_cfg* out);
+
+/* Session::generate (session.hpp:262-296): prefill ids[0..n_ids), then greedy decode. Writes
+ * the generated tokens only (the reference returns the prompt followed by them) to out_tokens
+ * (room for max_new_tokens) and their count to *n_out. Stops after an eos_token_id (>= 0) has
+ * been produced, or when the cache is full (n_ids + steps == max_seq), as the reference does.
+ * Optional outputs (NULL to skip): step_logits, host [max_new_tokens][vocab] fp32 logits of each
+ * step; ttft_ms, device time from the prompt upload to the first token; decode_ms, device time
+ * of the remaining steps. Invalid: n_ids < 1 or > max_seq, ids out of [0, vocab). */
+int cdna3_session_generate(cdna3_session* session, const int* ids, int n_ids, int max_new_tokens,
+                           int eos_token_id, int* out_tokens, int* n_out, float* step_logits,
+                           float* ttft_ms, float* decode_ms);
+
+/* Session::prefill_logits (session.hpp:298-317): prefill only; host fp32 logits [vocab] of the
+ * last prompt token. */
+int cdna3_session_prefill_logits(cdna3_session* session, const int* ids, int n_ids,
+                                 float* logits);
+
 #ifdef __cplusplus
 }
 #endif

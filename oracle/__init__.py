@@ -275,3 +275,87 @@ def ref_attn_cpu_ref(Q, K, V, seq_q, seq_k, d) -> np.ndarray:
     O = np.empty(seq_q * d, np.float32)
     l.ref_attn_cpu_ref(Q, K, V, O, seq_q, seq_k, d)
     return O.reshape(seq_q, d)
+
+
+# ---- small-LLM runtime (llm.c) ----------------------------------------------------------------
+
+_PP = ctypes.POINTER(ctypes.c_void_p)
+
+
+class _OrcLLM(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "ffn_dim",
+                                            "vocab", "layernorm")] + \
+               [("rope_theta", ctypes.c_float), ("eps", ctypes.c_float)] + \
+               [(n, ctypes.c_void_p) for n in ("embed", "lm_head", "fnorm", "fnorm_b")] + \
+               [(n, _PP) for n in ("wq", "wk", "wv", "wo", "bq", "bk", "bv", "wg", "wu", "wd", "n1", "n1b", "n2",
+                                  "n2b")]
+
+
+class LLM:
+    """CPU forward of the runtime's decoder (llm.c: Session::run_layers with the reference's
+    rounding points). `meta` and `tensors` are a model directory's meta.json dict and its fp16
+    arrays by file name. Holds the KV cache; `forward` appends to it like the runtime does."""
+
+    _KIND = {"wq": "q_proj", "wk": "k_proj", "wv": "v_proj", "wo": "o_proj", "bq": "q_bias", "bk": "k_bias",
+             "bv": "v_bias", "wg": "gate_proj", "wu": "up_proj", "wd": "down_proj", "n1": "norm_attn",
+             "n1b": "norm_attn_bias", "n2": "norm_mlp", "n2b": "norm_mlp_bias"}
+
+    def __init__(self, meta: dict, tensors: dict, max_seq: int):
+        L, H, nH = int(meta["n_layers"]), int(meta["hidden"]), int(meta["n_heads"])
+        nKV = int(meta.get("n_kv_heads", nH))
+        D = int(meta.get("head_dim", H // nH))
+        layer = meta.get("norm", "rms") == "layernorm"
+        eps = float(meta.get("norm_eps", 1e-5 if layer else 1e-6))
+        self.meta, self.max_seq, self.vocab = meta, max_seq, int(meta["vocab_size"])
+        self._keep = []
+
+        def f32(a):
+            a = np.ascontiguousarray(np.asarray(a, np.float16).astype(np.float32))
+            self._keep.append(a)
+            return a.ctypes.data
+
+        m = _OrcLLM(L, H, nH, nKV, D, int(meta["ffn_dim"]), self.vocab, int(layer),
+                    float(meta.get("rope_theta", 10000.0)), eps)
+        m.embed, m.lm_head, m.fnorm = f32(tensors["embed_tokens"]), f32(tensors["lm_head"]), f32(tensors["final_norm"])
+        m.fnorm_b = f32(tensors["final_norm_bias"]) if "final_norm_bias" in tensors else None
+        for field, suffix in self._KIND.items():
+            names = [f"layer_{i}_{suffix}" for i in range(L)]
+            if not all(n in tensors for n in names):
+                setattr(m, field, None)
+                continue
+            arr = (ctypes.c_void_p * L)(*[f32(tensors[n]) for n in names])
+            self._keep.append(arr)
+            setattr(m, field, ctypes.cast(arr, _PP))
+        self._m = m
+        self.Kc = np.zeros(L * nKV * max_seq * D, np.uint16)
+        self.Vc = np.zeros_like(self.Kc)
+        self.pos = 0
+        l = lib()
+        l.orc_llm_forward.restype = ctypes.c_int
+        l.orc_llm_forward.argtypes = [ctypes.POINTER(_OrcLLM), _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_int, _f32p, ctypes.c_int]
+
+    def reset(self) -> None:
+        self.Kc[:] = 0
+        self.Vc[:] = 0
+        self.pos = 0
+
+    def forward(self, ids, all_logits: bool = False) -> np.ndarray:
+        """Runs ids at the next cache positions; fp32 logits [T][vocab] (all_logits) or [vocab]."""
+        ids = np.ascontiguousarray(np.asarray(ids, np.int32).reshape(-1))
+        T = ids.size
+        out = np.empty((T if all_logits else 1) * self.vocab, np.float32)
+        rc = lib().orc_llm_forward(ctypes.byref(self._m), ids, T, self.pos, self.Kc.ctypes.data, self.Vc.ctypes.data,
+                                   self.max_seq, out, int(all_logits))
+        if rc:
+            raise ValueError("orc_llm_forward: bad arguments")
+        self.pos += T
+        return out.reshape(T, self.vocab) if all_logits else out
+
+    def greedy(self, ids, max_new_tokens: int) -> list:
+        """Session::generate's loop on the CPU (first index of the maximum on ties)."""
+        self.reset()
+        toks = [int(np.argmax(self.forward(ids)))]
+        while len(toks) < max_new_tokens and self.pos < self.max_seq:
+            toks.append(int(np.argmax(self.forward([toks[-1]]))))
+        return toks

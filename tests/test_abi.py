@@ -124,9 +124,9 @@ def test_wave_primitives_use_no_lds_and_no_readlane(tmp_path):
 
 
 def test_library_kernels_avoid_lds_where_designed_to(tmp_path):
-    # Reductions, scans, norms, KV-cache kernels and the decode merge are LDS-free by design; prefill and the
+    # Reductions, scans, norms, KV-cache and runtime kernels and the decode merge are LDS-free by design; prefill and the
     # decode partial kernel stage K/V in LDS.
-    for src in ("reduce_scan.hip", "norms.hip", "decode.hip", "kv_cache.hip"):
+    for src in ("reduce_scan.hip", "norms.hip", "decode.hip", "kv_cache.hip", "llm.hip"):
         asm = _device_asm(os.path.join(ROOT, "amd-incstinct-labs_amd", "csrc", src), tmp_path)
         for name, body in _functions(asm).items():
             assert not re.search(r"v_pk_(add|mul|fma)_f32", body), (src, name)
@@ -151,3 +151,29 @@ def test_prefill_kernel_uses_async_lds_loads_and_transpose_reads(tmp_path):
     assert "ds_read_b64_tr_b16" in body
     assert "v_mfma_f32_16x16x32_bf16" in body and "v_mfma_f32_16x16x32_f16" in body
     assert not re.search(r"v_pk_(add|mul|fma)_f32", body)
+
+
+def test_session_rejects_bad_models_before_touching_a_gpu(tmp_path):
+    from cdna4 import model_format as mf
+    l = cdna4.lib()
+    h = ctypes.c_void_p()
+    assert l.cdna3_session_create(None, 16, ctypes.byref(h)) == 1
+    assert l.cdna3_session_create(str(tmp_path / "absent").encode(), 16, ctypes.byref(h)) == 1
+    good = str(tmp_path / "ok")
+    mf.random_model(good, n_layers=1, hidden=64, n_heads=1, ffn_dim=64, vocab_size=8)
+    assert l.cdna3_session_create(good.encode(), 0, ctypes.byref(h)) == 1          # max_seq
+    for key, val in (("head_dim", 96), ("n_kv_heads", 3), ("hidden", 4100), ("ffn_dim", 60), ("rope_theta", -1.0)):
+        d = tmp_path / f"bad_{key}"
+        meta = dict(n_layers=1, hidden=128, n_heads=2, n_kv_heads=2, head_dim=64, ffn_dim=64, vocab_size=8,
+                    rope_theta=10000.0, qkv_bias=0)
+        meta[key] = val
+        d.mkdir()
+        (d / "meta.json").write_text(__import__("json").dumps(meta))
+        assert l.cdna3_session_create(str(d).encode(), 16, ctypes.byref(h)) == 1, key
+    assert not h.value
+    cfg = cdna4.ModelCfg()
+    assert l.cdna3_session_config(None, ctypes.byref(cfg)) == 1
+    n = ctypes.c_int(0)
+    assert l.cdna3_session_generate(None, None, 0, 1, -1, None, ctypes.byref(n), None, None, None) == 1
+    assert l.cdna3_session_prefill_logits(None, None, 0, None) == 1
+    l.cdna3_session_destroy(None)   # no-op

@@ -1,0 +1,149 @@
+"""The small-LLM runtime session (csrc/session.hip through the C ABI) against the CPU oracle.
+
+Logits of every step are compared with the oracle's forward over the same token sequence
+(teacher forcing: the oracle runs the prompt followed by the tokens the GPU chose), so one
+near-tie cannot derail the rest of the comparison. A chosen token must be the oracle's argmax,
+or within LOGIT_TOL of its maximum (a near-tie the fp16 rounding points can flip).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import cdna4
+import oracle
+from cdna4 import model_format as mf
+
+pytestmark = pytest.mark.gpu
+
+# |GPU - oracle| on fp32 logits, relative to the step's largest logit (at least 1): the fp16/bf16
+# bound 2e-3. The oracle rounds to fp16 where the reference does; the GPU accumulates its
+# projections in another order, which moves an fp16 rounding by one ulp now and then, and these
+# flips propagate through the layers.
+LOGIT_TOL = 2e-3
+
+
+def _row_err(got, ref):
+    """max over rows of max|got - ref| / max(1, max|ref|) (one row per step)."""
+    got, ref = np.atleast_2d(got), np.atleast_2d(ref)
+    scale = np.maximum(1.0, np.abs(ref).max(axis=1))
+    return float((np.abs(got - ref).max(axis=1) / scale).max())
+
+MODELS = {
+    "gqa_bias_d64": dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab_size=1000,
+                         qkv_bias=True),
+    "mha_d128_layernorm": dict(n_layers=2, hidden=256, n_heads=2, n_kv_heads=2, head_dim=128, ffn_dim=384,
+                               vocab_size=777, norm="layernorm", rope_theta=1e6),
+    "gqa3_d64": dict(n_layers=3, hidden=192, n_heads=3, n_kv_heads=1, head_dim=64, ffn_dim=256, vocab_size=500),
+}
+
+
+@pytest.fixture(scope="module", params=sorted(MODELS))
+def model(request, tmp_path_factory):
+    d = str(tmp_path_factory.mktemp(request.param))
+    mf.random_model(d, seed=11, norm_jitter=0.2, **MODELS[request.param])
+    meta, t = mf.read_model(d)
+    print(f"model {request.param}", flush=True)
+    return d, meta, t
+
+
+def _prompt(meta, n, seed):
+    return np.random.default_rng(seed).integers(0, int(meta["vocab_size"]), n).astype(np.int32)
+
+
+def _check_generation(meta, t, ids, out, max_seq):
+    toks, logits = out["tokens"], out["logits"]
+    ref = oracle.LLM(meta, t, max_seq).forward(np.concatenate([ids, toks[:-1]]).astype(np.int32),
+                                               all_logits=True)[len(ids) - 1:]
+    assert ref.shape == logits.shape
+    err = _row_err(logits, ref)
+    print(f"  steps {len(toks)}: max |logit - oracle| / scale = {err:.2e}, "
+          f"abs {float(np.abs(logits - ref).max()):.2e}", flush=True)
+    assert err < LOGIT_TOL, err
+    for i, tok in enumerate(toks):
+        best = int(np.argmax(ref[i]))
+        near = 2 * LOGIT_TOL * max(1.0, float(np.abs(ref[i]).max()))
+        assert tok == best or ref[i][best] - ref[i][tok] <= near, (i, tok, best)
+        assert tok == int(np.argmax(logits[i]))   # the device argmax picks the max of its own logits
+
+
+def test_config_read_from_meta(model):
+    d, meta, _ = model
+    with cdna4.Session(d, max_seq=64) as s:
+        c = s.cfg.as_dict()
+    for k in ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "ffn_dim", "vocab_size"):
+        assert c[k] == int(meta[k]), k
+    assert c["layernorm"] == int(meta.get("norm") == "layernorm")
+    assert c["qkv_bias"] == int(meta["qkv_bias"])
+    assert abs(c["norm_eps"] - (1e-5 if c["layernorm"] else 1e-6)) < 1e-9
+
+
+@pytest.mark.parametrize("n", [1, 5, 64, 100])
+def test_prefill_logits_match_oracle(model, n):
+    d, meta, t = model
+    ids = _prompt(meta, n, n)
+    with cdna4.Session(d, max_seq=128) as s:
+        got = s.prefill_logits(ids)
+    ref = oracle.LLM(meta, t, 128).forward(ids)
+    err = _row_err(got, ref)
+    print(f"  prompt {n}: max |logit - oracle| / scale = {err:.2e}", flush=True)
+    assert err < LOGIT_TOL, err
+
+
+@pytest.mark.parametrize("n,new", [(21, 16), (1, 8), (64, 12)])
+def test_generate_matches_oracle(model, n, new):
+    d, meta, t = model
+    ids = _prompt(meta, n, 100 + n)
+    with cdna4.Session(d, max_seq=96) as s:
+        out = s.generate_ex(ids, cdna4.GenerateCfg(new), with_logits=True)
+    assert len(out["tokens"]) == new
+    assert out["ttft_ms"] > 0 and out["decode_ms"] > 0
+    _check_generation(meta, t, ids, out, 96)
+
+
+def test_session_reuse_and_plain_generate(model):
+    # a second, shorter prompt on the same session sees none of the first one's cache rows
+    d, meta, t = model
+    a, b = _prompt(meta, 40, 1), _prompt(meta, 9, 2)
+    with cdna4.Session(d, max_seq=64) as s:
+        s.generate_ex(a, cdna4.GenerateCfg(10))
+        second = s.generate(b, cdna4.GenerateCfg(6))
+    with cdna4.Session(d, max_seq=64) as s:
+        fresh = s.generate_ex(b, cdna4.GenerateCfg(6), with_logits=True)
+    assert second == list(b) + fresh["tokens"]
+    _check_generation(meta, t, b, fresh, 64)
+
+
+def test_eos_and_full_cache_stop_generation(model):
+    d, meta, _ = model
+    ids = _prompt(meta, 12, 3)
+    with cdna4.Session(d, max_seq=64) as s:
+        base = s.generate_ex(ids, cdna4.GenerateCfg(10))["tokens"]
+        eos = base[4]
+        stop = base.index(eos) + 1
+        assert s.generate_ex(ids, cdna4.GenerateCfg(10, eos_token_id=eos))["tokens"] == base[:stop]
+    with cdna4.Session(d, max_seq=len(ids) + 3) as s:
+        assert s.generate_ex(ids, cdna4.GenerateCfg(10))["tokens"] == base[:4]
+
+
+def test_invalid_requests_raise(model):
+    d, meta, _ = model
+    V = int(meta["vocab_size"])
+    with cdna4.Session(d, max_seq=16) as s:
+        for bad in ([V], [-1], list(range(17)), []):
+            with pytest.raises((cdna4.CDNA4Error, ValueError)):
+                s.generate_ex(bad, cdna4.GenerateCfg(2))
+        with pytest.raises(cdna4.CDNA4Error):
+            s.prefill_logits([0, V + 5])
+
+
+def test_cfg5_shape_matches_oracle(tmp_path):
+    # the benchmark's model shape (12 layers, d 768, 12 heads of 64, MLP 3072, vocab 32000,
+    # LayerNorm with gains 1 and betas 0, weights N(0, 0.02)), on a prompt the oracle runs quickly
+    d = str(tmp_path / "cfg5")
+    mf.random_model(d, n_layers=12, hidden=768, n_heads=12, ffn_dim=3072, vocab_size=32000, norm="layernorm", seed=5)
+    meta, t = mf.read_model(d)
+    ids = _prompt(meta, 48, 9)
+    with cdna4.Session(d, max_seq=128) as s:
+        out = s.generate_ex(ids, cdna4.GenerateCfg(6), with_logits=True)
+    _check_generation(meta, t, ids, out, 128)
