@@ -95,6 +95,74 @@ __device__ __forceinline__ void load_stage(const uint16_t* __restrict__ head, in
     }
 }
 
+// Query heads of the group as B operands: lane holds q[head qh0 + li][32c + 8g .. +8], zero
+// past the group.
+template <int D>
+__device__ __forceinline__ void load_q(const DecodeArgs& a, int b, int qh0, int nrows, int li, int g,
+                                       u32x4 (&qb)[1][D / 32]) {
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+        qb[0][c] = u32x4{0u, 0u, 0u, 0u};
+        if (li < nrows)
+            qb[0][c] = *(const u32x4*)((const uint16_t*)a.q + ((size_t)b * a.nQH + qh0 + li) * D + c * 32 + g * 8);
+        asm volatile("" : : "v"(qb[0][c]));   // the loads complete before the first copy is issued
+    }
+}
+
+// The loop of decode_mfma below as a function, for the short-cache kernel (decode_mfma keeps its
+// own copy, whose code generation the long-cache tuning was measured on).
+// One wave streams keys [kbeg, kend) of one kv head through its NS-stage LDS ring and leaves the
+// unnormalised (m, l, O) of its query heads in registers: lane (li, g) holds
+// O^T[16 dt + 4 g + e][head li] in o[0][dt][e], the running base-2 max of head li in m[0] and its
+// denominator in lacc[0][0]. An empty range leaves m = kInitM, l = 0, O = 0.
+template <int D, bool kBf16, int NS>
+__device__ __forceinline__ void stream_keys(const DecodeArgs& a, const uint16_t* Kh, const uint16_t* Vh, int kbeg,
+                                            int kend, const u32x4 (&qb)[1][D / 32], f32x4 (&o)[1][D / 16],
+                                            f32x4 (&lacc)[1], float (&m)[1], uint16_t* k_lds, uint16_t* v_lds,
+                                            int lane) {
+    constexpr int NDT = D / 16;
+    constexpr int kStage = kDecT * D;                 // elements per K (or V) stage
+    constexpr int kCopies = 2 * kDecT * (D / 8) / 64;  // copies per stage (K and V)
+    const int li = lane & 15, g = lane >> 4;
+    const int nch = (kend - kbeg + kDecT - 1) / kDecT;   // <= 0 for an empty range
+    m[0] = tile::kInitM;
+    lacc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < NDT; ++d) o[0][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const tile::LdsOffsets off = tile::lds_offsets<D>(li, g);
+
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i)
+        if (i < nch) {
+            load_stage<D>(Kh, kbeg + i * kDecT, a.N, k_lds + i * kStage, lane);
+            load_stage<D>(Vh, kbeg + i * kDecT, a.N, v_lds + i * kStage, lane);
+        }
+    int st = 0;   // stage of chunk ch
+    for (int ch = 0; ch < nch; ++ch) {
+        const int ahead = ch + NS - 1;
+        if (ahead < nch) {
+            const int sa = (st == 0) ? NS - 1 : st - 1;   // stage of chunk ch - 1, already consumed
+            load_stage<D>(Kh, kbeg + ahead * kDecT, a.N, k_lds + sa * kStage, lane);
+            load_stage<D>(Vh, kbeg + ahead * kDecT, a.N, v_lds + sa * kStage, lane);
+        }
+        wait_copies_younger<kCopies>(min(NS - 1, nch - 1 - ch));
+        const char* Kt = (const char*)(k_lds + st * kStage);
+        const char* Vt = (const char*)(v_lds + st * kStage);
+        const int kb = kbeg + ch * kDecT;
+        f32x4 s[1][2];
+        tile::qk_chunk<D, 1, kBf16>(Kt, off, qb, s, 0);
+        float lm[1];
+        const bool need = (kb + kDecT > kend)
+            ? tile::check_chunk<1, true>(s, m, lm, kb, 0, kend, 0, a.sc, li, g)
+            : tile::check_chunk<1, false>(s, m, lm, kb, 0, kend, 0, a.sc, li, g);
+        if (__builtin_amdgcn_ballot_w64(need)) tile::rescale_rows<D, 1>(lm, m, o, lacc, a.sc);
+        u32x4 pb[1];
+        tile::softmax_chunk<1, kBf16>(s, m, pb, a.sc);
+        tile::pv_chunk<D, 1, kBf16>(Vt, off, pb, o, lacc, 0);
+        st = (st == NS - 1) ? 0 : st + 1;
+    }
+}
+
 template <int D, bool kBf16, int NS>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void decode_mfma(DecodeArgs a) {
     static_assert(NS >= 2 && NS <= 4, "ring depth");
@@ -178,6 +246,74 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void de
     }
 }
 
+// ---- short caches: one launch, split-K inside the workgroup --------------------------------
+//
+// For short caches the split-K grid above is small and its second (merge) launch costs as much
+// as the attention itself. Here one workgroup of W waves serves a (batch, kv head, head group):
+// wave w streams the w-th of W contiguous key ranges through its own LDS ring, then the waves
+// leave their (m, l, O) partials in LDS (over their rings, after a barrier) and all W*64 lanes
+// merge them, o = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w, writing the output directly.
+template <int D, int W>
+constexpr int wg_ring_elems() { return W * kDecStages * kDecT * D; }
+
+template <int D, bool kBf16, int W>
+__global__ __launch_bounds__(64 * W) void decode_wg(DecodeArgs a, void* __restrict__ out) {
+    constexpr int ND = D / 32, NDT = D / 16;
+    constexpr int kStage = kDecT * D;
+    constexpr int kRing = kDecStages * kStage;
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[wg_ring_elems<D, W>()];
+    __shared__ __attribute__((aligned(16))) uint16_t v_lds[wg_ring_elems<D, W>()];
+    static_assert((size_t)W * 16 * D * sizeof(float) <= sizeof(k_lds), "O partials fit over the K rings");
+    static_assert((size_t)W * 16 * 2 * sizeof(float) <= sizeof(v_lds), "(m, l) partials fit over the V rings");
+
+    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+    const int li = lane & 15, g = lane >> 4;
+    const int kvh = blockIdx.y / a.HB;
+    const int sub = blockIdx.y % a.HB;
+    const int b = blockIdx.z;
+    const int qh0 = kvh * a.G + sub * 16;
+    const int nrows = min(16, a.G - sub * 16);
+    const int kbeg = min(a.N, wave * a.KPW);
+    const int kend = min(a.N, kbeg + a.KPW);
+    const size_t head_off = ((size_t)b * a.nKVH + kvh) * (size_t)a.stride * D;
+
+    u32x4 qb[1][ND];
+    load_q<D>(a, b, qh0, nrows, li, g, qb);
+    f32x4 o[1][NDT], lacc[1];
+    float m[1];
+    stream_keys<D, kBf16, kDecStages>(a, (const uint16_t*)a.K + head_off, (const uint16_t*)a.V + head_off, kbeg,
+                                      kend, qb, o, lacc, m, k_lds + wave * kRing, v_lds + wave * kRing, lane);
+    __syncthreads();   // every wave is done with its ring: reuse the LDS for the partials
+    float* po = (float*)k_lds;   // [W][16 heads][D]
+    float* pml = (float*)v_lds;  // [W][16 heads][2]
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+        *(f32x4*)(po + ((size_t)wave * 16 + li) * D + dt * 16 + g * 4) = o[0][dt];
+    if (g == 0) {
+        pml[(wave * 16 + li) * 2] = m[0];
+        pml[(wave * 16 + li) * 2 + 1] = lacc[0][0];
+    }
+    __syncthreads();
+    // each lane merges pairs of adjacent outputs (head, d .. d + 1)
+    for (int p = (int)threadIdx.x; p < nrows * (D / 2); p += 64 * W) {
+        const int h = p / (D / 2), d = 2 * (p % (D / 2));
+        float M = tile::kInitM;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, pml[(w * 16 + h) * 2]);
+        float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float wt = exp2f(pml[(w * 16 + h) * 2] - M);
+            L = fmaf(wt, pml[(w * 16 + h) * 2 + 1], L);
+            const float2 v = *(const float2*)(po + ((size_t)w * 16 + h) * D + d);
+            o0 = fmaf(wt, v.x, o0);
+            o1 = fmaf(wt, v.y, o1);
+        }
+        const float inv = L > 0.f ? 1.f / L : 1.f;
+        *(uint32_t*)((uint16_t*)out + ((size_t)b * a.nQH + qh0 + h) * D + d) = pack2<kBf16>(o0 * inv, o1 * inv);
+    }
+}
+
 // One wave per (batch, query head): o = sum_i 2^(m_i - M) O_i / sum_i 2^(m_i - M) l_i.
 template <int D, bool kBf16>
 __global__ __launch_bounds__(64) void decode_merge(const float* __restrict__ part_ml, const float* __restrict__ part_o,
@@ -211,7 +347,12 @@ __global__ __launch_bounds__(64) void decode_merge(const float* __restrict__ par
     }
 }
 
-struct Plan { int G, HB, KPW, P; size_t ws_bytes; };
+struct Plan { int G, HB, KPW, P; size_t ws_bytes; bool wg; };
+
+// Waves per workgroup of the short-cache variant (its LDS holds W rings of two K and V stages)
+// and the longest cache it takes: at most kWgChunks 32-key chunks per wave.
+template <int D> constexpr int wg_waves() { return D == 64 ? 8 : 4; }
+constexpr int kWgChunks = 8;
 
 // HB: groups of up to 16 query heads per kv head (one MFMA column block each); KPW: keys per
 // split, a multiple of the 32-key chunk, sized so that the whole grid is one round of resident
@@ -225,6 +366,14 @@ bool plan_decode(const cdna3_decode_cfg& c, Plan& p) {
     if (stride < c.N) return false;
     p.G = c.nQHeads / c.nKVHeads;
     p.HB = (p.G + 15) / 16;
+    const int W = c.D == 64 ? wg_waves<64>() : wg_waves<128>();
+    p.wg = c.N <= W * kWgChunks * kDecT;
+    if (p.wg) {   // one workgroup per (batch, kv head, head group); W contiguous key ranges
+        p.KPW = ((c.N + W - 1) / W + kDecT - 1) / kDecT * kDecT;
+        p.P = 1;
+        p.ws_bytes = 0;
+        return true;
+    }
     const double rows = (double)c.batch * c.nKVHeads * p.HB;
     const double slots = (double)device_cus() * kDecPerCU;
     long long kpw = (long long)ceil((double)c.N * rows / slots);
@@ -252,6 +401,10 @@ int launch_decode(const cdna3_decode_cfg& c, const Plan& p, const void* q, const
     const long long gy = (long long)c.nKVHeads * p.HB;
     if (gy > 65535 || c.batch > 65535) return CDNA4_ERR_INVALID_VALUE;
     dim3 grid((unsigned)p.P, (unsigned)gy, (unsigned)c.batch);
+    if (p.wg) {
+        decode_wg<D, kBf16, wg_waves<D>()><<<grid, 64 * wg_waves<D>(), 0, s>>>(a, o);
+        return launch_status();
+    }
     decode_mfma<D, kBf16, kDecStages><<<grid, 64, 0, s>>>(a);
     decode_merge<D, kBf16><<<(unsigned)((size_t)c.batch * c.nQHeads), 64, 0, s>>>(a.part_ml, a.part_o, o, p.P);
     return launch_status();

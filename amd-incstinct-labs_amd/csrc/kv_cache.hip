@@ -77,7 +77,8 @@ __global__ __launch_bounds__(256) void rope_append(const uint16_t* __restrict__ 
                                                    const uint16_t* __restrict__ v, uint16_t* __restrict__ q_out,
                                                    uint16_t* __restrict__ Kc, uint16_t* __restrict__ Vc,
                                                    const float* __restrict__ cosv, const float* __restrict__ sinv,
-                                                   int T, int nQH, int nKVH, int D, int pos0, int max_seq) {
+                                                   int T, int nQH, int nKVH, int D, int pos0, int max_seq,
+                                                   long long ldq, long long ldk, long long ldv) {
     const int half = D >> 1;
     const int slots = nQH + 2 * nKVH;
     const size_t total = (size_t)T * slots * half;
@@ -91,15 +92,15 @@ __global__ __launch_bounds__(256) void rope_append(const uint16_t* __restrict__ 
     uint16_t* dst;
     bool rotate = true;
     if (r < nQH) {
-        src = q + ((size_t)s * nQH + r) * D;
+        src = q + s * ldq + (size_t)r * D;
         dst = q_out + ((size_t)r * T + s) * D;
     } else if (r < nQH + nKVH) {
         const int h = r - nQH;
-        src = k + ((size_t)s * nKVH + h) * D;
+        src = k + s * ldk + (size_t)h * D;
         dst = Kc + ((size_t)h * max_seq + pos0 + s) * D;
     } else {
         const int h = r - nQH - nKVH;
-        src = v + ((size_t)s * nKVH + h) * D;
+        src = v + s * ldv + (size_t)h * D;
         dst = Vc + ((size_t)h * max_seq + pos0 + s) * D;
         rotate = false;
     }
@@ -118,6 +119,18 @@ __global__ __launch_bounds__(256) void rope_append(const uint16_t* __restrict__ 
 }
 
 }  // namespace
+
+// rope_append with explicit token strides (elements) of q, k and v, so the three can be column
+// blocks of one [T][QD + 2 KVD] projection output. Arguments are validated by the caller.
+int kv_rope_append(const void* q, const void* k, const void* v, long long ldq, long long ldk, long long ldv,
+                   void* q_out, void* K_cache, void* V_cache, const float* cos_tab, const float* sin_tab, int T,
+                   int nQH, int nKVH, int D, int pos0, int max_seq, hipStream_t stream) {
+    const size_t total = (size_t)T * (nQH + 2 * nKVH) * (D / 2);
+    rope_append<<<ceil_div(total, 256), 256, 0, stream>>>(
+        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)q_out, (uint16_t*)K_cache,
+        (uint16_t*)V_cache, cos_tab, sin_tab, T, nQH, nKVH, D, pos0, max_seq, ldq, ldk, ldv);
+    return launch_status();
+}
 }  // namespace cdna4
 
 using namespace cdna4;
@@ -165,9 +178,6 @@ extern "C" int cdna3_rope_append_kv_f16(const void* q, const void* k, const void
     if (T == 0) return 0;
     if (!q || !k || !v || !q_out || !K_cache || !V_cache || !cos_tab || !sin_tab) return CDNA4_ERR_INVALID_VALUE;
     if (int e = check_device()) return e;
-    const size_t total = (size_t)T * (nQH + 2 * nKVH) * (D / 2);
-    rope_append<<<ceil_div(total, 256), 256, 0, (hipStream_t)stream>>>(
-        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)q_out, (uint16_t*)K_cache,
-        (uint16_t*)V_cache, cos_tab, sin_tab, T, nQH, nKVH, D, pos0, max_seq);
-    return launch_status();
+    return kv_rope_append(q, k, v, (long long)nQH * D, (long long)nKVH * D, (long long)nKVH * D, q_out, K_cache,
+                          V_cache, cos_tab, sin_tab, T, nQH, nKVH, D, pos0, max_seq, (hipStream_t)stream);
 }

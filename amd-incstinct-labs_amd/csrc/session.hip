@@ -46,6 +46,9 @@ int llm_logits_argmax(bool layer, const float* hidden, const void* gain, const v
                       unsigned long long* scratch16, int* ids, int* tokens, int step, hipStream_t s);
 int llm_silu_mul(const float* gu, void* act, int T, int F, hipStream_t s);
 int llm_bias_add_f16(void* Y, const void* b, int T, int N, hipStream_t s);
+int kv_rope_append(const void* q, const void* k, const void* v, long long ldq, long long ldk, long long ldv,
+                   void* q_out, void* K_cache, void* V_cache, const float* cos_tab, const float* sin_tab, int T,
+                   int nQH, int nKVH, int D, int pos0, int max_seq, hipStream_t stream);
 
 namespace {
 
@@ -127,7 +130,7 @@ struct Session {
     int cap = 0;
     float *hidden = nullptr, *gu = nullptr, *logits = nullptr;
     unsigned long long *partial = nullptr, *scratch16 = nullptr;
-    uint16_t *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qh = nullptr, *attn = nullptr, *act = nullptr;
+    uint16_t *xn = nullptr, *q = nullptr, *qh = nullptr, *attn = nullptr, *act = nullptr;   // q: [T][QD + 2 KVD]
     int *ids = nullptr, *tokens = nullptr;
     std::vector<void*> scratch;
 
@@ -261,8 +264,6 @@ int Session::reserve(int T) {
     CK(dmalloc((void**)&gu, T * 2 * F * 4, true));
     CK(dmalloc((void**)&xn, T * (H > F ? H : F) * 2, true));
     CK(dmalloc((void**)&q, (size_t)T * (qd() + 2 * kvd()) * 2, true));
-    k = q + (size_t)T * qd();
-    v = k + (size_t)T * kvd();
     CK(dmalloc((void**)&qh, (size_t)T * qd() * 2, true));
     CK(dmalloc((void**)&attn, (size_t)T * qd() * 2, true));
     CK(dmalloc((void**)&act, T * F * 2, true));
@@ -311,16 +312,12 @@ int Session::run_layers(int T, int pos0) {
             continue;
         }
         CK(llm_norm_cast(lnorm, hidden, l.n_attn, l.n_attn_b, xn, T, H, eps, stream));
-        CK(gemm(xn, l.wqkv, q, false, 0.f, T, QD, H, QD));
-        CK(gemm(xn, l.wqkv + (size_t)QD * H, k, false, 0.f, T, KVD, H, KVD));
-        CK(gemm(xn, l.wqkv + (size_t)(QD + KVD) * H, v, false, 0.f, T, KVD, H, KVD));
-        if (l.bqkv) {
-            CK(llm_bias_add_f16(q, l.bqkv, T, QD, stream));
-            CK(llm_bias_add_f16(k, l.bqkv + QD, T, KVD, stream));
-            CK(llm_bias_add_f16(v, l.bqkv + QD + KVD, T, KVD, stream));
-        }
-        CK(cdna3_rope_append_kv_f16(q, k, v, qh, Kl, Vl, cos_tab + (size_t)pos0 * D, sin_tab + (size_t)pos0 * D, T,
-                                    nH, nKV, D, pos0, max_seq, s));
+        // one GEMM for Q|K|V: row t of q is [q_t | k_t | v_t], QKVD = QD + 2 KVD wide
+        const int QKVD = QD + 2 * KVD;
+        CK(gemm(xn, l.wqkv, q, false, 0.f, T, QKVD, H, QKVD));
+        if (l.bqkv) CK(llm_bias_add_f16(q, l.bqkv, T, QKVD, stream));
+        CK(kv_rope_append(q, q + QD, q + QD + KVD, QKVD, QKVD, QKVD, qh, Kl, Vl, cos_tab + (size_t)pos0 * D,
+                          sin_tab + (size_t)pos0 * D, T, nH, nKV, D, pos0, max_seq, stream));
         // Prompt from an empty cache (pos0 == 0): causal over the T cached keys, read in place;
         // O written token-major for the O projection.
         cdna3_prefill_cfg pc{D, T, T, nH, nKV, 1, 1};

@@ -84,7 +84,8 @@ def test_invalid_arguments_rejected_without_gpu():
 def test_cpp_headers_compile_host_only(tmp_path):
     src = tmp_path / "use.cpp"
     src.write_text(
-        "#include <cdna3/attention.hpp>\n#include <cdna3/runtime/forward.hpp>\n"
+        "#include <cdna3/attention.hpp>\n#include <cdna3/runtime/forward.hpp>\n#include <cdna3/runtime/session.hpp>\n"
+        "std::vector<int> g(cdna3::runtime::Session& s) { return s.generate({1, 2, 3}, {16, -1}); }\n"
         "int f(const __half* q, const __half* k, const __half* v, __half* o) {\n"
         "  cdna3::attn::PrefillCfg p{128, 256, 256, 4, 2, 1, 1};\n"
         "  cdna3::attn::DecodeCfg d{128, 512, 32, 8};\n"
@@ -125,23 +126,24 @@ def test_wave_primitives_use_no_lds_and_no_readlane(tmp_path):
 
 def test_library_kernels_avoid_lds_where_designed_to(tmp_path):
     # Reductions, scans, norms, KV-cache and runtime kernels and the decode merge are LDS-free by design; prefill and the
-    # decode partial kernel stage K/V in LDS.
+    # decode kernels (split partials and the short-cache workgroup variant) stage K/V in LDS.
     for src in ("reduce_scan.hip", "norms.hip", "decode.hip", "kv_cache.hip", "llm.hip"):
         asm = _device_asm(os.path.join(ROOT, "amd-incstinct-labs_amd", "csrc", src), tmp_path)
         for name, body in _functions(asm).items():
             assert not re.search(r"v_pk_(add|mul|fma)_f32", body), (src, name)
-            if "decode_mfma" in name:
+            if "decode_mfma" in name or "decode_wg" in name:
                 continue
             assert not re.search(r"^\s+ds_", body, re.M), (src, name)
 
 
 def test_decode_kernel_streams_kv_through_lds_onto_matrix_cores(tmp_path):
     asm = _device_asm(os.path.join(ROOT, "amd-incstinct-labs_amd", "csrc", "decode.hip"), tmp_path)
-    body = "\n".join(v for k, v in _functions(asm).items() if "decode_mfma" in k)
+    body = "\n".join(v for k, v in _functions(asm).items() if "decode_mfma" in k or "decode_wg" in k)
     assert "global_load_lds_dwordx4" in body
     assert "ds_read_b64_tr_b16" in body and "ds_read_b128" in body
     assert "v_mfma_f32_16x16x32_bf16" in body and "v_mfma_f32_16x16x32_f16" in body
-    assert "s_barrier" not in body   # single-wave workgroups: the wave waits for its own copies
+    split = "\n".join(v for k, v in _functions(asm).items() if "decode_mfma" in k)
+    assert "s_barrier" not in split   # single-wave workgroups: the wave waits for its own copies
 
 
 def test_prefill_kernel_uses_async_lds_loads_and_transpose_reads(tmp_path):
