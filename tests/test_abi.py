@@ -179,3 +179,16 @@ def test_session_rejects_bad_models_before_touching_a_gpu(tmp_path):
     assert l.cdna3_session_generate(None, None, 0, 1, -1, None, ctypes.byref(n), None, None, None) == 1
     assert l.cdna3_session_prefill_logits(None, None, 0, None) == 1
     l.cdna3_session_destroy(None)   # no-op
+
+
+def test_torch_ops_register_on_cpu():
+    import torch
+    from cdna4 import torch_ops
+    torch_ops.register()
+    torch_ops.register()   # idempotent
+    q = torch.empty(4, 16, 64, device="meta", dtype=torch.float16)
+    k = torch.empty(2, 16, 64, device="meta", dtype=torch.float16)
+    assert torch.ops.amdinstinct.flash_attn(q, k, k).shape == q.shape
+    assert torch.ops.amdinstinct.flash_attn_decode(q[:, 0], k, k).shape == (4, 64)
+    with pytest.raises(Exception):   # no CPU kernel: the ops run on the GPU only
+        torch.ops.amdinstinct.flash_attn(q.to("cpu"), k.to("cpu"), k.to("cpu"))

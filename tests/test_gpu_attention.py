@@ -195,6 +195,31 @@ def test_torch_op_mirrors():
     assert max_rel_err(host(od), ref[:, -1]) <= tolerance(torch.float16)
 
 
+@pytest.mark.parametrize("D,S,HQ,HK,dtype", [(128, 192, 8, 2, torch.float16), (64, 333, 6, 6, torch.bfloat16)])
+def test_registered_torch_ops_against_sdpa(D, S, HQ, HK, dtype):
+    # torch.ops.amdinstinct.* as the reference's models call them, against PyTorch's own SDPA
+    # in fp32 on the same rounded inputs (the reference's compare_vs_production_fa.py check).
+    from cdna4 import torch_ops
+    torch_ops.register()
+    g = torch.Generator(device=DEV).manual_seed(D + S)
+    q = torch.randn(HQ, S, D, device=DEV, generator=g).to(dtype)
+    k = torch.randn(HK, S, D, device=DEV, generator=g).to(dtype)
+    v = torch.randn(HK, S, D, device=DEV, generator=g).to(dtype)
+    o = torch.ops.amdinstinct.flash_attn(q, k, v)
+    rep = HQ // HK
+    kf = k.float().repeat_interleave(rep, 0).contiguous()
+    vf = v.float().repeat_interleave(rep, 0).contiguous()
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float()[None], kf[None], vf[None], is_causal=True)[0]
+    assert max_rel_err(host(o), host(ref).astype(np.float64)) <= tolerance(dtype)
+    od = torch.ops.amdinstinct.flash_attn_decode(q[:, -1].contiguous(), k, v)
+    assert max_rel_err(host(od), host(ref[:, -1]).astype(np.float64)) <= tolerance(dtype)
+    for bad in ((q.float(), k, v), (q[:, :, :32].contiguous(), k, v), (q, k[:, :-1].contiguous(), v)):
+        with pytest.raises(RuntimeError):
+            torch.ops.amdinstinct.flash_attn(*bad)
+    with pytest.raises(RuntimeError):
+        torch.ops.amdinstinct.flash_attn_decode(q[:, -1].contiguous(), k.transpose(1, 2), v)
+
+
 def test_cpp_dropin_validation_program():
     exe = os.path.join(ROOT, "tests", "native", "validate_attention_api")
     assert os.path.exists(exe), "tests/native not built"
