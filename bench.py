@@ -42,11 +42,17 @@ PEAK_FP32_TFLOPS = 157.3      # MI355X fp32
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=30)
+    p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["all", "prefill", "decode", "dpp", "cfg1", "copy", "llm"], default="all")
-    return p.parse_args()
+    p.add_argument("--only", default="all",
+                   help="all, or a comma-separated subset of prefill,decode,dpp,cfg1,copy,llm")
+    args = p.parse_args()
+    legs = {"prefill", "decode", "dpp", "cfg1", "copy", "llm"}
+    args.legs = legs if args.only == "all" else set(args.only.split(","))
+    if not args.legs <= legs:
+        p.error(f"--only: unknown legs {sorted(args.legs - legs)}")
+    return args
 
 
 def time_launches(torch, fn, steps, warmup):
@@ -270,26 +276,26 @@ def main():
     torch.cuda.set_device(0)
     result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
               "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1))"}
-    if args.only in ("all", "prefill"):
+    if "prefill" in args.legs:
         p = bench_prefill(torch, cdna4, args.steps, args.warmup)
         result.update({"value": p["tflops"], "unit": "TFLOPS", "ms_per_step": p["total_ms"] / args.steps,
                        "config": p["config"],
                        "roofline": {"bound": "mfma", "achieved": p["tflops"], "peak": PEAK_BF16_TFLOPS,
                                     "unit": "TFLOP/s", "frac": p["tflops"] / PEAK_BF16_TFLOPS,
                                     "traffic": load_traffic("prefill"), "kernel_avg_ms": p["avg_ms"]}})
-    if args.only in ("all", "decode"):
+    if "decode" in args.legs:
         result["decode"] = bench_decode(torch, cdna4, args.steps, args.warmup)
         if "value" not in result:
             d = result["decode"]
             result.update({"value": d["value"], "unit": "GB/s", "ms_per_step": d["avg_us"] / 1e3,
                            "config": d["config"], "roofline": d["roofline"], "dtype": "fp16"})
-    if args.only in ("all", "dpp"):
+    if "dpp" in args.legs:
         result["dpp"] = bench_dpp(torch, cdna4, args.steps, args.warmup)
-    if args.only in ("all", "cfg1"):
+    if "cfg1" in args.legs:
         result["cfg1"] = bench_cfg1(torch, cdna4, args.steps, args.warmup)
-    if args.only in ("all", "copy"):
+    if "copy" in args.legs:
         result["copy_1GiB"] = bench_copy(torch, args.steps, args.warmup)
-    if args.only in ("all", "llm"):
+    if "llm" in args.legs:
         if args.no_cpu_baseline:
             os.environ["CDNA4_NO_CPU_BASELINE"] = "1"
         result["llm"] = bench_llm(min(args.steps, 5))
@@ -297,7 +303,7 @@ def main():
             l = result["llm"]
             result.update({"value": l["value"], "unit": l["unit"], "ms_per_step": l["ms_per_token"],
                            "config": l["config"], "roofline": l["roofline"], "dtype": "fp16"})
-    if args.only in ("all", "prefill") and not args.no_cpu_baseline:
+    if "prefill" in args.legs and not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_prefill()
     print(json.dumps(result), flush=True)
 
