@@ -24,8 +24,8 @@
 //   * Q stays in VGPRs as B operands for the whole kernel; softmax is base-2 with a
 //     log2(e)-prescaled scale; causal blocks are issued heaviest first, with all q blocks
 //     of a (batch, head) on the same XCD so its K/V stay in that XCD's L2.
-// The fp32 kernel (fa_f32) is a plain VALU kernel for the fp32 arm of the reference
-// configuration (fp32 in and out, accuracy 1e-4).
+// The fp32 kernel (fa_f32) serves the fp32 arm of the reference configuration (fp32 in and
+// out, accuracy 1e-4) on the fp32 matrix-core instruction (v_mfma_f32_16x16x4_f32).
 #include "attn_tile.hpp"
 
 namespace cdna4 {
@@ -295,16 +295,49 @@ __global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
 }
 
 // ---- fp32 kernel: one wave per 16 query rows, one key per lane ------------------------
-constexpr int kF32Br = 16;
+// ---- fp32 arm on the matrix cores -------------------------------------------------------
+// v_mfma_f32_16x16x4_f32 multiplies and accumulates in fp32. Lane L holds A[L % 16][L / 16],
+// B[L / 16][L % 16] and C[4 (L / 16) + i][L % 16], i < 4 (cdna4::mfma::*_16x16x4f32 and its exact
+// small-integer GEMM test). The reduction index of a product may be permuted freely as long as A
+// and B agree, which gives every lane contiguous operands:
+//   S^T = K Q^T, step s: lane (r = L % 16, g = L / 16) supplies K[key r][g D/4 + s] and
+//                        Q[query r][g D/4 + s]; C: lane (r, g) holds keys 4g + i of query r.
+//   O^T = V^T P^T, step s (keys 4g + s): B is the lane's own P of key 4g + s; A for row block b is
+//                        V[key 4g + s][16 b + r]; C: lane (r, g) holds O[query r][16 b + 4 g + i].
+// A workgroup of kF32Waves waves serves 16 queries of one (batch, head); wave w takes the 16-key
+// chunks w, w + W, ... (the causal diagonal spreads over the waves), keeps a running base-2
+// (m, l, O), and the waves merge through LDS at the end. The next chunk's K and V are loaded
+// into registers while the current one is computed.
+constexpr int kF32Br = 16;      // queries per workgroup
+constexpr int kF32Waves = 4;
 
 template <int D>
-__global__ __launch_bounds__(64) void fa_f32(const float* __restrict__ Q, const float* __restrict__ K,
-                                              const float* __restrict__ V, float* __restrict__ O, int seqQ,
-                                              int seqK, int nQH, int nKVH, int causal, int nqb) {
-    __shared__ float q_s[kF32Br][D];
-    __shared__ float v_s[64][D + 1];
-    __shared__ float p_s[kF32Br][64];
-    const int lane = threadIdx.x;
+__device__ __forceinline__ void f32_chunk_load(const float* __restrict__ Kh, const float* __restrict__ Vh, int kb,
+                                               int seqK, int r, int g, float (&kf)[D / 4], float (&vf)[4][D / 16]) {
+    constexpr int DS = D / 4;
+    const float* kp = Kh + (size_t)min(kb + r, seqK - 1) * D + g * DS;
+#pragma unroll
+    for (int s = 0; s < DS; s += 4) {
+        const float4 v = *(const float4*)(kp + s);
+        kf[s] = v.x; kf[s + 1] = v.y; kf[s + 2] = v.z; kf[s + 3] = v.w;
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const float* vp = Vh + (size_t)min(kb + 4 * g + s, seqK - 1) * D + r;
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b) vf[s][b] = vp[16 * b];
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * kF32Waves) void fa_f32(const float* __restrict__ Q, const float* __restrict__ K,
+                                                         const float* __restrict__ V, float* __restrict__ O, int seqQ,
+                                                         int seqK, int nQH, int nKVH, int causal, int nqb, float sc) {
+    constexpr int DS = D / 4, NB = D / 16;
+    __shared__ __attribute__((aligned(16))) float o_s[kF32Waves][kF32Br][D];
+    __shared__ float m_s[kF32Waves][kF32Br], l_s[kF32Waves][kF32Br];
+    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+    const int r = lane & 15, g = lane >> 4;
     const int qb = blockIdx.x % nqb;
     const int bh = blockIdx.x / nqb;
     const int b = bh / nQH, h = bh % nQH;
@@ -313,70 +346,86 @@ __global__ __launch_bounds__(64) void fa_f32(const float* __restrict__ Q, const 
     const float* Qh = Q + ((size_t)b * nQH + h) * (size_t)seqQ * D;
     const float* Kh = K + ((size_t)b * nKVH + kvh) * (size_t)seqK * D;
     const float* Vh = V + ((size_t)b * nKVH + kvh) * (size_t)seqK * D;
-    for (int i = lane; i < kF32Br * D; i += 64) {
-        const int r = i / D, c = i % D;
-        q_s[r][c] = (q0 + r < seqQ) ? Qh[(size_t)(q0 + r) * D + c] : 0.f;
-    }
-    constexpr int EPL = D / 64;   // output columns per lane
-    float m[kF32Br], l[kF32Br], acc[kF32Br][EPL];
+
+    float qf[DS];
+    {
+        const float* qp = Qh + (size_t)min(q0 + r, seqQ - 1) * D + g * DS;
 #pragma unroll
-    for (int r = 0; r < kF32Br; ++r) {
-        m[r] = -INFINITY; l[r] = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[r][e] = 0.f;
+        for (int s = 0; s < DS; s += 4) {
+            const float4 v = *(const float4*)(qp + s);
+            qf[s] = v.x; qf[s + 1] = v.y; qf[s + 2] = v.z; qf[s + 3] = v.w;
+        }
     }
-    const float scale = 1.f / sqrtf((float)D);
-    int kend = seqK;
-    if (causal) kend = min(seqK, min(q0 + kF32Br, seqQ));
+    const int kend = causal ? min(seqK, q0 + kF32Br) : seqK;
+    const int qrow = q0 + r;
+    float m = kInitM, lpart = 0.f;
+    f32x4 o[NB];
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) o[bb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    float kf[DS], vf[4][NB];
+    int kb = wave * 16;
+    if (kb < kend) f32_chunk_load<D>(Kh, Vh, kb, seqK, r, g, kf, vf);
+    for (; kb < kend; kb += 16 * kF32Waves) {
+        f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < DS; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], qf[s], st, 0, 0, 0);
+        float vc[4][NB];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int bb = 0; bb < NB; ++bb) vc[s][bb] = vf[s][bb];
+        const int kn = kb + 16 * kF32Waves;
+        if (kn < kend) f32_chunk_load<D>(Kh, Vh, kn, seqK, r, g, kf, vf);   // next chunk, in flight
+        float p[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = kb + 4 * g + i;
+            p[i] = (key < kend && !(causal && key > qrow)) ? st[i] * sc : -INFINITY;
+            mx = fmaxf(mx, p[i]);
+        }
+        mx = cross_row_allreduce(mx, Max{});
+        const float mnew = fmaxf(m, mx);
+        const float alpha = exp2f(m - mnew);
+        float ps = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            p[i] = exp2f(p[i] - mnew);
+            ps += p[i];
+        }
+        lpart = lpart * alpha + ps;
+        m = mnew;
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) o[bb] *= alpha;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int bb = 0; bb < NB; ++bb) o[bb] = __builtin_amdgcn_mfma_f32_16x16x4f32(vc[s][bb], p[s], o[bb], 0, 0, 0);
+    }
+    const float l = cross_row_allreduce(lpart, Sum{});
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) *(f32x4*)&o_s[wave][r][16 * bb + 4 * g] = o[bb];
+    if (g == 0) {
+        m_s[wave][r] = m;
+        l_s[wave][r] = l;
+    }
     __syncthreads();
-    for (int k0 = 0; k0 < kend; k0 += 64) {
-        const int key = k0 + lane;
-        const bool valid = key < kend;
-        for (int i = lane; i < 64 * D; i += 64) {
-            const int r = i / D, c = i % D;
-            v_s[r][c] = (k0 + r < seqK) ? Vh[(size_t)(k0 + r) * D + c] : 0.f;
-        }
-        float kr[D];
-#pragma unroll
-        for (int c = 0; c < D; ++c) kr[c] = valid ? Kh[(size_t)key * D + c] : 0.f;
-        __syncthreads();
-#pragma unroll
-        for (int r = 0; r < kF32Br; ++r) {
-            float dot = 0.f;
-#pragma unroll
-            for (int c = 0; c < D; ++c) dot += q_s[r][c] * kr[c];
-            float s = dot * scale;
-            if (!valid || (causal && key > q0 + r)) s = -INFINITY;
-            const float mx = allreduce(s, Max{});
-            const float mnew = fmaxf(m[r], mx);
-            const float mref = (mnew == -INFINITY) ? 0.f : mnew;
-            const float p = expf(s - mref);
-            const float alpha = expf(m[r] - mref);
-            l[r] = l[r] * alpha + allreduce(p, Sum{});
-            m[r] = mnew;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) acc[r][e] *= alpha;
-            p_s[r][lane] = p;
-        }
-        __syncthreads();
-        const int nk = min(64, kend - k0);
-        for (int k = 0; k < nk; ++k) {
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const float v = v_s[k][lane + 64 * e];
-#pragma unroll
-                for (int r = 0; r < kF32Br; ++r) acc[r][e] += p_s[r][k] * v;
-            }
-        }
-        __syncthreads();
-    }
     float* Oh = O + ((size_t)b * nQH + h) * (size_t)seqQ * D;
+    for (int idx = (int)threadIdx.x; idx < kF32Br * D; idx += 64 * kF32Waves) {
+        const int q = idx / D, d = idx % D;
+        if (q0 + q >= seqQ) break;
+        float M = kInitM;
 #pragma unroll
-    for (int r = 0; r < kF32Br; ++r) {
-        if (q0 + r >= seqQ) break;
-        const float inv = (l[r] > 0.f) ? 1.f / l[r] : 1.f;
+        for (int w = 0; w < kF32Waves; ++w) M = fmaxf(M, m_s[w][q]);
+        float L = 0.f, acc = 0.f;
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) Oh[(size_t)(q0 + r) * D + lane + 64 * e] = acc[r][e] * inv;
+        for (int w = 0; w < kF32Waves; ++w) {
+            const float wt = exp2f(m_s[w][q] - M);
+            L = fmaf(wt, l_s[w][q], L);
+            acc = fmaf(wt, o_s[w][q][d], acc);
+        }
+        Oh[(size_t)(q0 + q) * D + d] = L > 0.f ? acc / L : 0.f;
     }
 }
 
@@ -448,7 +497,8 @@ extern "C" int cdna3_attn_prefill(const void* Q, const void* K, const void* V, v
     if (int e = check_cfg(cfg, Q, K, V, O)) return e;
     const cdna3_prefill_cfg& c = *cfg;
     if (dtype != CDNA4_F16 && dtype != CDNA4_BF16 && dtype != CDNA4_F32) return CDNA4_ERR_INVALID_VALUE;
-    if (dtype != CDNA4_F32 && ((((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V) & 15u) || ((uintptr_t)O & 7u)))
+    // 16-byte loads of Q, K, V rows (both kernels); O rows are stored 8 (16-bit) or 4 bytes at a time.
+    if ((((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V) & 15u) || ((uintptr_t)O & (dtype == CDNA4_F32 ? 3u : 7u)))
         return CDNA4_ERR_INVALID_VALUE;
     if (int e = check_device()) return e;
     hipStream_t s = (hipStream_t)stream;
@@ -456,12 +506,15 @@ extern "C" int cdna3_attn_prefill(const void* Q, const void* K, const void* V, v
         const int nqb = (c.seqQ + kF32Br - 1) / kF32Br;
         const long long blocks = (long long)c.batch * c.nQHeads * nqb;
         if (blocks > 0x7fffffffLL) return CDNA4_ERR_INVALID_VALUE;
+        const float sc = kLog2e / sqrtf((float)c.D);
         if (c.D == 128)
-            fa_f32<128><<<(unsigned)blocks, 64, 0, s>>>((const float*)Q, (const float*)K, (const float*)V, (float*)O,
-                                                       c.seqQ, c.seqK, c.nQHeads, c.nKVHeads, c.causal ? 1 : 0, nqb);
+            fa_f32<128><<<(unsigned)blocks, 64 * kF32Waves, 0, s>>>((const float*)Q, (const float*)K, (const float*)V,
+                                                                    (float*)O, c.seqQ, c.seqK, c.nQHeads, c.nKVHeads,
+                                                                    c.causal ? 1 : 0, nqb, sc);
         else
-            fa_f32<64><<<(unsigned)blocks, 64, 0, s>>>((const float*)Q, (const float*)K, (const float*)V, (float*)O,
-                                                      c.seqQ, c.seqK, c.nQHeads, c.nKVHeads, c.causal ? 1 : 0, nqb);
+            fa_f32<64><<<(unsigned)blocks, 64 * kF32Waves, 0, s>>>((const float*)Q, (const float*)K, (const float*)V,
+                                                                   (float*)O, c.seqQ, c.seqK, c.nQHeads, c.nKVHeads,
+                                                                   c.causal ? 1 : 0, nqb, sc);
         return launch_status();
     }
     const cdna3_prefill_strides st = contiguous_strides(c);

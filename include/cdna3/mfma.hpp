@@ -138,5 +138,21 @@ __device__ __forceinline__ void store_C_32x32x16(float* C, f32x16 c, int lane, i
     for (int e = 0; e < 16; ++e) C[((e / 4) * 8 + r0 + e % 4) * ldC + col] = c[e];
 }
 
+// ---- 16x16x4 fp32 ------------------------------------------------------------------------
+// fp32 products and accumulation; lane L holds A[L % 16][L / 16], B[L / 16][L % 16] and
+// C[4 (L / 16) + i][L % 16] (the 16x16x32 C layout).
+__device__ __forceinline__ f32x4 mma_16x16x4f32(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float load_A_16x16x4f32(const float* A, int lane, int ldA = 4) {
+    return A[(lane % 16) * ldA + lane / 16];
+}
+__device__ __forceinline__ float load_B_16x16x4f32(const float* B, int lane, int ldB = 16) {
+    return B[(lane / 16) * ldB + lane % 16];
+}
+__device__ __forceinline__ void store_C_16x16x4f32(float* C, f32x4 c, int lane, int ldC = 16) {
+    store_C_16x16x32(C, c, lane, ldC);
+}
+
 }  // namespace mfma
 }  // namespace cdna4

@@ -90,7 +90,8 @@ const char* cdna3_error_string(int code);
  * Unlike the reference, any seqQ, seqK >= 1 is accepted (ragged tails are masked);
  * shapes the reference would silently truncate therefore compute the full result.
  * Invalid: D not in {64,128}, non-positive sizes, nQHeads % nKVHeads != 0,
- * causal with seqQ != seqK, an unknown dtype.
+ * causal with seqQ != seqK, an unknown dtype, Q/K/V not 16-byte aligned, O not 8-byte
+ * (16-bit) or 4-byte (fp32) aligned.
  */
 int cdna3_attn_prefill(const void* Q, const void* K, const void* V, void* O,
                        const cdna3_prefill_cfg* cfg, int dtype, cdna4_stream_t stream);

@@ -151,7 +151,14 @@ extern "C" int hook_ballot(const int32_t* in, uint64_t* out, int nwaves, void* s
     return (int)hipGetLastError();
 }
 
-// which: 0 = cdna3::mfma 16x16x16 f16; 1/2 = 16x16x32 f16/bf16; 3/4 = 32x32x16 f16/bf16.
+__global__ void mfma16x4f32_kernel(const float* A, const float* B, float* C) {
+    const int lane = threadIdx.x;
+    cdna4::mfma::f32x4 c = {0.f, 0.f, 0.f, 0.f};
+    c = cdna4::mfma::mma_16x16x4f32(cdna4::mfma::load_A_16x16x4f32(A, lane), cdna4::mfma::load_B_16x16x4f32(B, lane), c);
+    cdna4::mfma::store_C_16x16x4f32(C, c, lane);
+}
+
+// which: 0 = cdna3::mfma 16x16x16 f16; 1/2 = 16x16x32 f16/bf16; 3/4 = 32x32x16 f16/bf16; 5 = 16x16x4 f32.
 extern "C" int hook_mfma(int which, const void* A, const void* B, float* C, void* stream) {
     hipStream_t s = (hipStream_t)stream;
     switch (which) {
@@ -160,6 +167,7 @@ extern "C" int hook_mfma(int which, const void* A, const void* B, float* C, void
         case 2: mfma16x32_kernel<cdna4::mfma::bf16x8, __bf16><<<1, 64, 0, s>>>((const __bf16*)A, (const __bf16*)B, C); break;
         case 3: mfma32x16_kernel<cdna4::mfma::f16x8, _Float16><<<1, 64, 0, s>>>((const _Float16*)A, (const _Float16*)B, C); break;
         case 4: mfma32x16_kernel<cdna4::mfma::bf16x8, __bf16><<<1, 64, 0, s>>>((const __bf16*)A, (const __bf16*)B, C); break;
+        case 5: mfma16x4f32_kernel<<<1, 64, 0, s>>>((const float*)A, (const float*)B, C); break;
         default: return 1;
     }
     return (int)hipGetLastError();

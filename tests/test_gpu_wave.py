@@ -151,13 +151,17 @@ def test_row_softmax_lane():
 
 
 def _mm(which, A, B):
-    half = which in (0, 1, 3)
-    dt = torch.float16 if half else torch.bfloat16
-    kind = oracle.F16 if half else oracle.BF16
-    _, ab = oracle.round16(A.astype(np.float32), kind)
-    _, bb = oracle.round16(B.astype(np.float32), kind)
-    ta = torch.from_numpy(ab.view(np.int16)).view(dt).to(DEV)
-    tb = torch.from_numpy(bb.view(np.int16)).view(dt).to(DEV)
+    if which == 5:   # fp32 operands
+        ta = torch.from_numpy(np.ascontiguousarray(A, np.float32)).to(DEV)
+        tb = torch.from_numpy(np.ascontiguousarray(B, np.float32)).to(DEV)
+    else:
+        half = which in (0, 1, 3)
+        dt = torch.float16 if half else torch.bfloat16
+        kind = oracle.F16 if half else oracle.BF16
+        _, ab = oracle.round16(A.astype(np.float32), kind)
+        _, bb = oracle.round16(B.astype(np.float32), kind)
+        ta = torch.from_numpy(ab.view(np.int16)).view(dt).to(DEV)
+        tb = torch.from_numpy(bb.view(np.int16)).view(dt).to(DEV)
     c = torch.zeros(A.shape[0] * B.shape[1], dtype=torch.float32, device=DEV)
     assert hooks().hook_mfma(which, ptr(ta), ptr(tb), ptr(c), stream()) == 0
     torch.cuda.synchronize()
@@ -165,7 +169,7 @@ def _mm(which, A, B):
 
 
 @pytest.mark.parametrize("which,shape", [(0, (16, 16, 16)), (1, (16, 32, 16)), (2, (16, 32, 16)),
-                                         (3, (32, 16, 32)), (4, (32, 16, 32))])
+                                         (3, (32, 16, 32)), (4, (32, 16, 32)), (5, (16, 4, 16))])
 def test_mfma_lane_mapping_exact_gemm(which, shape):
     M, K, N = shape
     # Small integers: every product and sum is exact in fp32 (probe_mfma_mapping.hip style).
