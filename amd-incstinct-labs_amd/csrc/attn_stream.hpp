@@ -1,0 +1,110 @@
+// Streaming K/V through a per-wave LDS ring for the gfx950 attention kernels: asynchronous
+// 16-byte global->LDS copies issued as inline assembly and waited for explicitly, the swizzled
+// stage layout the tile reads expect, and the per-wave loop that folds a key range into a
+// running base-2 (m, l, O) for 16 query columns on the matrix cores.
+#pragma once
+#include "attn_tile.hpp"
+
+namespace cdna4 {
+namespace stream {
+
+using tile::f32x4;
+
+constexpr int kDecT = 32;       // keys per chunk / ring stage
+constexpr int kDecStages = 2;   // ring depth: one chunk in flight while the wave computes one
+
+// One asynchronous copy, 16 bytes per lane: lane i's bytes at gsrc land at LDS lds_dst + 16 i
+// (lds_dst wave-uniform, in M0). Issued as inline assembly so that the compiler does not track
+// it (it would otherwise wait for every copy before any LDS read); the kernel waits itself.
+__device__ __forceinline__ void dma16(const void* gsrc, const void* lds_dst) {
+    const uint32_t base = (uint32_t)(uintptr_t)(const tile::LDS_AS_T*)lds_dst;
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "{m0}"(base) : "memory");
+}
+
+// Wait until at most Y of this wave's newest copy groups (kCopies copies each) are in flight.
+template <int kCopies>
+__device__ __forceinline__ void wait_copies_younger(int y) {
+    switch (y) {
+        case 0: asm volatile("s_waitcnt vmcnt(0)" : : : "memory"); break;
+        case 1: asm volatile("s_waitcnt vmcnt(%0)" : : "n"(kCopies) : "memory"); break;
+        case 2: asm volatile("s_waitcnt vmcnt(%0)" : : "n"(2 * kCopies) : "memory"); break;
+        default: asm volatile("s_waitcnt vmcnt(%0)" : : "n"(3 * kCopies) : "memory"); break;
+    }
+}
+
+// Copy keys [k0, k0 + kDecT) of one head (row stride rs elements; rows past N re-read key N-1,
+// they are masked) into a ring stage, 16-byte chunks of a row XOR-swizzled as the tile reads expect.
+template <int D>
+__device__ __forceinline__ void load_stage(const uint16_t* __restrict__ head, long long rs, int k0, int N,
+                                           uint16_t* stage, int lane) {
+    constexpr int CPR = D / 8;
+    constexpr int NI = kDecT * CPR / 64;
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        const int p = j * 64 + lane;
+        const int r = p / CPR;
+        const int lc = (p % CPR) ^ tile::swz<D>(r);
+        const int key = min(k0 + r, N - 1);
+        dma16(head + key * rs + lc * 8, stage + j * 64 * 8);
+    }
+}
+
+// The per-wave loop of the split-K decode kernel as a function (decode_mfma keeps its own copy,
+// whose code generation the long-cache tuning was measured on), for the kernels that split a key
+// range over the waves of a workgroup.
+// One wave streams keys [kbeg, kend) of one kv head through its NS-stage LDS ring and leaves the
+// unnormalised (m, l, O) of its query heads in registers: lane (li, g) holds
+// O^T[16 dt + 4 g + e][head li] in o[0][dt][e], the running base-2 max of head li in m[0] and its
+// denominator in lacc[0][0]. An empty range leaves m = kInitM, l = 0, O = 0.
+// Keys are rows of K and V (row stride rs elements, N rows); the 16 B-operand columns of qb are
+// 16 query heads (decode) or 16 query rows qw0 .. qw0 + 15 (prefill; causal masks key > query).
+template <int D, bool kBf16, int NS>
+__device__ __forceinline__ void stream_keys(const uint16_t* Kh, const uint16_t* Vh, long long rs, int N, int kbeg,
+                                            int kend, int qw0, int causal, float sc, const u32x4 (&qb)[1][D / 32],
+                                            f32x4 (&o)[1][D / 16], f32x4 (&lacc)[1], float (&m)[1], uint16_t* k_lds,
+                                            uint16_t* v_lds, int lane) {
+    constexpr int NDT = D / 16;
+    constexpr int kStage = kDecT * D;                 // elements per K (or V) stage
+    constexpr int kCopies = 2 * kDecT * (D / 8) / 64;  // copies per stage (K and V)
+    const int li = lane & 15, g = lane >> 4;
+    const int nch = (kend - kbeg + kDecT - 1) / kDecT;   // <= 0 for an empty range
+    m[0] = tile::kInitM;
+    lacc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < NDT; ++d) o[0][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const tile::LdsOffsets off = tile::lds_offsets<D>(li, g);
+
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i)
+        if (i < nch) {
+            load_stage<D>(Kh, rs, kbeg + i * kDecT, N, k_lds + i * kStage, lane);
+            load_stage<D>(Vh, rs, kbeg + i * kDecT, N, v_lds + i * kStage, lane);
+        }
+    int st = 0;   // stage of chunk ch
+    for (int ch = 0; ch < nch; ++ch) {
+        const int ahead = ch + NS - 1;
+        if (ahead < nch) {
+            const int sa = (st == 0) ? NS - 1 : st - 1;   // stage of chunk ch - 1, already consumed
+            load_stage<D>(Kh, rs, kbeg + ahead * kDecT, N, k_lds + sa * kStage, lane);
+            load_stage<D>(Vh, rs, kbeg + ahead * kDecT, N, v_lds + sa * kStage, lane);
+        }
+        wait_copies_younger<kCopies>(min(NS - 1, nch - 1 - ch));
+        const char* Kt = (const char*)(k_lds + st * kStage);
+        const char* Vt = (const char*)(v_lds + st * kStage);
+        const int kb = kbeg + ch * kDecT;
+        f32x4 s[1][2];
+        tile::qk_chunk<D, 1, kBf16>(Kt, off, qb, s, 0);
+        float lm[1];
+        const bool need = (kb + kDecT > kend || (causal && kb + kDecT - 1 > qw0))
+            ? tile::check_chunk<1, true>(s, m, lm, kb, qw0, kend, causal, sc, li, g)
+            : tile::check_chunk<1, false>(s, m, lm, kb, qw0, kend, causal, sc, li, g);
+        if (__builtin_amdgcn_ballot_w64(need)) tile::rescale_rows<D, 1>(lm, m, o, lacc, sc);
+        u32x4 pb[1];
+        tile::softmax_chunk<1, kBf16>(s, m, pb, sc);
+        tile::pv_chunk<D, 1, kBf16>(Vt, off, pb, o, lacc, 0);
+        st = (st == NS - 1) ? 0 : st + 1;
+    }
+}
+
+}  // namespace stream
+}  // namespace cdna4

@@ -17,11 +17,14 @@
 //   * A second kernel merges the (m, l, O) partials of each query head, with the max and the
 //     denominator formed by the wave butterfly.
 #include "attn_tile.hpp"
+#include "attn_stream.hpp"
 #include <mutex>
 #include <math.h>
 
 namespace cdna4 {
 namespace {
+
+using namespace stream;
 
 using wave::xlane::allreduce;
 using wave::xlane::Sum;
@@ -55,45 +58,7 @@ struct DecodeArgs {
 // copy of chunk c + NS - 1 is issued before chunk c is computed, so NS - 1 chunks per wave are
 // in flight while the matrix cores work. A single wave needs no barrier: it waits (vmcnt) for
 // its own copies, and a stage is refilled only after the wave's reads of it have completed.
-constexpr int kDecT = 32;       // keys per chunk / ring stage
-constexpr int kDecStages = 2;   // ring depth: one chunk in flight while the wave computes one
 constexpr int kDecPerCU = 4;    // resident single-wave workgroups per CU the grid is sized for
-
-// One asynchronous copy, 16 bytes per lane: lane i's bytes at gsrc land at LDS lds_dst + 16 i
-// (lds_dst wave-uniform, in M0). Issued as inline assembly so that the compiler does not track
-// it (it would otherwise wait for every copy before any LDS read); the kernel waits itself.
-__device__ __forceinline__ void dma16(const void* gsrc, const void* lds_dst) {
-    const uint32_t base = (uint32_t)(uintptr_t)(const tile::LDS_AS_T*)lds_dst;
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "{m0}"(base) : "memory");
-}
-
-// Wait until at most Y of this wave's newest copy groups (kCopies copies each) are in flight.
-template <int kCopies>
-__device__ __forceinline__ void wait_copies_younger(int y) {
-    switch (y) {
-        case 0: asm volatile("s_waitcnt vmcnt(0)" : : : "memory"); break;
-        case 1: asm volatile("s_waitcnt vmcnt(%0)" : : "n"(kCopies) : "memory"); break;
-        case 2: asm volatile("s_waitcnt vmcnt(%0)" : : "n"(2 * kCopies) : "memory"); break;
-        default: asm volatile("s_waitcnt vmcnt(%0)" : : "n"(3 * kCopies) : "memory"); break;
-    }
-}
-
-// Copy keys [k0, k0 + kDecT) of one head (rows past N re-read key N-1; they are masked) into a
-// ring stage, 16-byte chunks of a row XOR-swizzled as the tile reads expect.
-template <int D>
-__device__ __forceinline__ void load_stage(const uint16_t* __restrict__ head, int k0, int N, uint16_t* stage,
-                                           int lane) {
-    constexpr int CPR = D / 8;
-    constexpr int NI = kDecT * CPR / 64;
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-        const int p = j * 64 + lane;
-        const int r = p / CPR;
-        const int lc = (p % CPR) ^ tile::swz<D>(r);
-        const int key = min(k0 + r, N - 1);
-        dma16(head + (size_t)key * D + lc * 8, stage + j * 64 * 8);
-    }
-}
 
 // Query heads of the group as B operands: lane holds q[head qh0 + li][32c + 8g .. +8], zero
 // past the group.
@@ -106,60 +71,6 @@ __device__ __forceinline__ void load_q(const DecodeArgs& a, int b, int qh0, int 
         if (li < nrows)
             qb[0][c] = *(const u32x4*)((const uint16_t*)a.q + ((size_t)b * a.nQH + qh0 + li) * D + c * 32 + g * 8);
         asm volatile("" : : "v"(qb[0][c]));   // the loads complete before the first copy is issued
-    }
-}
-
-// The loop of decode_mfma below as a function, for the short-cache kernel (decode_mfma keeps its
-// own copy, whose code generation the long-cache tuning was measured on).
-// One wave streams keys [kbeg, kend) of one kv head through its NS-stage LDS ring and leaves the
-// unnormalised (m, l, O) of its query heads in registers: lane (li, g) holds
-// O^T[16 dt + 4 g + e][head li] in o[0][dt][e], the running base-2 max of head li in m[0] and its
-// denominator in lacc[0][0]. An empty range leaves m = kInitM, l = 0, O = 0.
-template <int D, bool kBf16, int NS>
-__device__ __forceinline__ void stream_keys(const DecodeArgs& a, const uint16_t* Kh, const uint16_t* Vh, int kbeg,
-                                            int kend, const u32x4 (&qb)[1][D / 32], f32x4 (&o)[1][D / 16],
-                                            f32x4 (&lacc)[1], float (&m)[1], uint16_t* k_lds, uint16_t* v_lds,
-                                            int lane) {
-    constexpr int NDT = D / 16;
-    constexpr int kStage = kDecT * D;                 // elements per K (or V) stage
-    constexpr int kCopies = 2 * kDecT * (D / 8) / 64;  // copies per stage (K and V)
-    const int li = lane & 15, g = lane >> 4;
-    const int nch = (kend - kbeg + kDecT - 1) / kDecT;   // <= 0 for an empty range
-    m[0] = tile::kInitM;
-    lacc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int d = 0; d < NDT; ++d) o[0][d] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const tile::LdsOffsets off = tile::lds_offsets<D>(li, g);
-
-#pragma unroll
-    for (int i = 0; i < NS - 1; ++i)
-        if (i < nch) {
-            load_stage<D>(Kh, kbeg + i * kDecT, a.N, k_lds + i * kStage, lane);
-            load_stage<D>(Vh, kbeg + i * kDecT, a.N, v_lds + i * kStage, lane);
-        }
-    int st = 0;   // stage of chunk ch
-    for (int ch = 0; ch < nch; ++ch) {
-        const int ahead = ch + NS - 1;
-        if (ahead < nch) {
-            const int sa = (st == 0) ? NS - 1 : st - 1;   // stage of chunk ch - 1, already consumed
-            load_stage<D>(Kh, kbeg + ahead * kDecT, a.N, k_lds + sa * kStage, lane);
-            load_stage<D>(Vh, kbeg + ahead * kDecT, a.N, v_lds + sa * kStage, lane);
-        }
-        wait_copies_younger<kCopies>(min(NS - 1, nch - 1 - ch));
-        const char* Kt = (const char*)(k_lds + st * kStage);
-        const char* Vt = (const char*)(v_lds + st * kStage);
-        const int kb = kbeg + ch * kDecT;
-        f32x4 s[1][2];
-        tile::qk_chunk<D, 1, kBf16>(Kt, off, qb, s, 0);
-        float lm[1];
-        const bool need = (kb + kDecT > kend)
-            ? tile::check_chunk<1, true>(s, m, lm, kb, 0, kend, 0, a.sc, li, g)
-            : tile::check_chunk<1, false>(s, m, lm, kb, 0, kend, 0, a.sc, li, g);
-        if (__builtin_amdgcn_ballot_w64(need)) tile::rescale_rows<D, 1>(lm, m, o, lacc, a.sc);
-        u32x4 pb[1];
-        tile::softmax_chunk<1, kBf16>(s, m, pb, a.sc);
-        tile::pv_chunk<D, 1, kBf16>(Vt, off, pb, o, lacc, 0);
-        st = (st == NS - 1) ? 0 : st + 1;
     }
 }
 
@@ -207,16 +118,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void de
 #pragma unroll
     for (int i = 0; i < NS - 1; ++i)
         if (i < nch) {
-            load_stage<D>(Kh, kbeg + i * kDecT, a.N, k_lds + i * kStage, lane);
-            load_stage<D>(Vh, kbeg + i * kDecT, a.N, v_lds + i * kStage, lane);
+            load_stage<D>(Kh, D, kbeg + i * kDecT, a.N, k_lds + i * kStage, lane);
+            load_stage<D>(Vh, D, kbeg + i * kDecT, a.N, v_lds + i * kStage, lane);
         }
     int st = 0;   // stage of chunk ch
     for (int ch = 0; ch < nch; ++ch) {
         const int ahead = ch + NS - 1;
         if (ahead < nch) {
             const int sa = (st == 0) ? NS - 1 : st - 1;   // stage of chunk ch - 1, already consumed
-            load_stage<D>(Kh, kbeg + ahead * kDecT, a.N, k_lds + sa * kStage, lane);
-            load_stage<D>(Vh, kbeg + ahead * kDecT, a.N, v_lds + sa * kStage, lane);
+            load_stage<D>(Kh, D, kbeg + ahead * kDecT, a.N, k_lds + sa * kStage, lane);
+            load_stage<D>(Vh, D, kbeg + ahead * kDecT, a.N, v_lds + sa * kStage, lane);
         }
         wait_copies_younger<kCopies>(min(NS - 1, nch - 1 - ch));
         const char* Kt = (const char*)(k_lds + st * kStage);
@@ -281,8 +192,9 @@ __global__ __launch_bounds__(64 * W) void decode_wg(DecodeArgs a, void* __restri
     load_q<D>(a, b, qh0, nrows, li, g, qb);
     f32x4 o[1][NDT], lacc[1];
     float m[1];
-    stream_keys<D, kBf16, kDecStages>(a, (const uint16_t*)a.K + head_off, (const uint16_t*)a.V + head_off, kbeg,
-                                      kend, qb, o, lacc, m, k_lds + wave * kRing, v_lds + wave * kRing, lane);
+    stream_keys<D, kBf16, kDecStages>((const uint16_t*)a.K + head_off, (const uint16_t*)a.V + head_off, D, a.N, kbeg,
+                                      kend, 0, 0, a.sc, qb, o, lacc, m, k_lds + wave * kRing, v_lds + wave * kRing,
+                                      lane);
     __syncthreads();   // every wave is done with its ring: reuse the LDS for the partials
     float* po = (float*)k_lds;   // [W][16 heads][D]
     float* pml = (float*)v_lds;  // [W][16 heads][2]

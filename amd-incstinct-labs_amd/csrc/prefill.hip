@@ -27,6 +27,7 @@
 // The fp32 kernel (fa_f32) serves the fp32 arm of the reference configuration (fp32 in and
 // out, accuracy 1e-4) on the fp32 matrix-core instruction (v_mfma_f32_16x16x4_f32).
 #include "attn_tile.hpp"
+#include "attn_stream.hpp"
 
 namespace cdna4 {
 namespace {
@@ -294,7 +295,6 @@ __global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
     }
 }
 
-// ---- fp32 kernel: one wave per 16 query rows, one key per lane ------------------------
 // ---- fp32 arm on the matrix cores -------------------------------------------------------
 // v_mfma_f32_16x16x4_f32 multiplies and accumulates in fp32. Lane L holds A[L % 16][L / 16],
 // B[L / 16][L % 16] and C[4 (L / 16) + i][L % 16], i < 4 (cdna4::mfma::*_16x16x4f32 and its exact
@@ -429,6 +429,83 @@ __global__ __launch_bounds__(64 * kF32Waves) void fa_f32(const float* __restrict
     }
 }
 
+// ---- small problems: the keys of 16 queries split over the waves of a workgroup -------------
+// When the regular grid has too few workgroups to fill the chip (e.g. the FA2 reference
+// configuration: 8 heads x 512 queries), one workgroup of W waves serves 16 queries of one
+// (batch, head): wave w streams the w-th contiguous part of the visible keys through its own LDS
+// ring (the per-wave loop of the short-cache decode kernel, with the 16 queries as its columns and
+// the causal mask), then the waves merge their (m, l, O) through LDS over their rings.
+template <int D> constexpr int small_waves() { return D == 64 ? 8 : 4; }
+
+template <int D, bool kBf16, int W>
+__global__ __launch_bounds__(64 * W) void fa_small(PrefillArgs a) {
+    constexpr int ND = D / 32, NDT = D / 16;
+    constexpr int kStage = stream::kDecT * D;
+    constexpr int kRing = stream::kDecStages * kStage;
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[W * kRing];
+    __shared__ __attribute__((aligned(16))) uint16_t v_lds[W * kRing];
+    static_assert((size_t)W * 16 * D * sizeof(float) <= sizeof(k_lds), "O partials fit over the K rings");
+    static_assert((size_t)W * 16 * 2 * sizeof(float) <= sizeof(v_lds), "(m, l) partials fit over the V rings");
+
+    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+    const int li = lane & 15, g = lane >> 4;
+    const int nqb = (a.seqQ + 15) / 16;
+    const int qblk = blockIdx.x % nqb;
+    const int bh = blockIdx.x / nqb;
+    const int b = bh / a.nQH, h = bh % a.nQH;
+    const int kvh = h / (a.nQH / a.nKVH);
+    const int q0 = qblk * 16;
+    const int nrows = min(16, a.seqQ - q0);
+    const uint16_t* Qh = a.Q + b * a.q_bs + h * a.q_hs;
+    const uint16_t* Kh = a.K + b * a.k_bs + kvh * a.k_hs;
+    const uint16_t* Vh = a.V + b * a.k_bs + kvh * a.k_hs;
+
+    u32x4 qb[1][ND];
+#pragma unroll
+    for (int c = 0; c < ND; ++c) {
+        qb[0][c] = u32x4{0u, 0u, 0u, 0u};
+        if (li < nrows) qb[0][c] = *(const u32x4*)(Qh + (q0 + li) * a.q_rs + c * 32 + g * 8);
+        asm volatile("" : : "v"(qb[0][c]));   // the loads complete before the first copy is issued
+    }
+    const int kend = a.causal ? min(a.seqK, q0 + 16) : a.seqK;
+    const int kpw = ((kend + W - 1) / W + stream::kDecT - 1) / stream::kDecT * stream::kDecT;
+    const int kbeg = min(kend, wave * kpw);
+    const int kstop = min(kend, kbeg + kpw);
+    f32x4 o[1][NDT], lacc[1];
+    float m[1];
+    stream::stream_keys<D, kBf16, stream::kDecStages>(Kh, Vh, a.k_rs, a.seqK, kbeg, kstop, q0, a.causal, a.sc, qb, o,
+                                                      lacc, m, k_lds + wave * kRing, v_lds + wave * kRing, lane);
+    __syncthreads();   // every wave is done with its ring: reuse the LDS for the partials
+    float* po = (float*)k_lds;   // [W][16 queries][D]
+    float* pml = (float*)v_lds;  // [W][16 queries][2]
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+        *(f32x4*)(po + ((size_t)wave * 16 + li) * D + dt * 16 + g * 4) = o[0][dt];
+    if (g == 0) {
+        pml[(wave * 16 + li) * 2] = m[0];
+        pml[(wave * 16 + li) * 2 + 1] = lacc[0][0];
+    }
+    __syncthreads();
+    uint16_t* Oh = a.O + b * a.o_bs + h * a.o_hs;
+    for (int p = (int)threadIdx.x; p < nrows * (D / 2); p += 64 * W) {
+        const int r = p / (D / 2), d = 2 * (p % (D / 2));
+        float M = kInitM;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, pml[(w * 16 + r) * 2]);
+        float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float wt = exp2f(pml[(w * 16 + r) * 2] - M);
+            L = fmaf(wt, pml[(w * 16 + r) * 2 + 1], L);
+            const float2 v = *(const float2*)(po + ((size_t)w * 16 + r) * D + d);
+            o0 = fmaf(wt, v.x, o0);
+            o1 = fmaf(wt, v.y, o1);
+        }
+        const float inv = L > 0.f ? 1.f / L : 1.f;
+        *(uint32_t*)(Oh + (q0 + r) * a.o_rs + d) = pack2<kBf16>(o0 * inv, o1 * inv);
+    }
+}
+
 template <int D, int W, int QT, bool kBf16>
 int launch_mfma(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& st, const void* Q, const void* K,
                 const void* V, void* O, hipStream_t s) {
@@ -459,11 +536,27 @@ int launch_mfma(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& st, con
 template <int D, bool kBf16>
 int dispatch_mfma(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& st, const void* Q, const void* K,
                   const void* V, void* O, hipStream_t s) {
-    // 8 waves x 32 queries (two waves per SIMD) when that gives >= 2 workgroups per CU, else
-    // 4 waves x 16 queries for small problems.
-    const long long big_blocks = (long long)c.batch * c.nQHeads * ((c.seqQ + 255) / 256);
+    // 8 waves x 32 queries (two waves per SIMD) when that gives >= 2 workgroups per CU; 4 waves x
+    // 16 queries for mid-size problems; for problems whose 64-query blocks would not fill the CUs
+    // twice over, 16 queries per workgroup with the keys split over its waves.
+    const long long heads = (long long)c.batch * c.nQHeads;
+    const long long big_blocks = heads * ((c.seqQ + 255) / 256);
     if (big_blocks >= 512) return launch_mfma<D, 8, 2, kBf16>(c, st, Q, K, V, O, s);
-    return launch_mfma<D, 4, 1, kBf16>(c, st, Q, K, V, O, s);
+    if (heads * ((c.seqQ + 63) / 64) >= 2LL * device_cus()) return launch_mfma<D, 4, 1, kBf16>(c, st, Q, K, V, O, s);
+    PrefillArgs a;
+    a.Q = (const uint16_t*)Q; a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.O = (uint16_t*)O;
+    a.q_bs = st.q_batch; a.q_hs = st.q_head; a.q_rs = st.q_row;
+    a.k_bs = st.kv_batch; a.k_hs = st.kv_head; a.k_rs = st.kv_row;
+    a.o_bs = st.o_batch; a.o_hs = st.o_head; a.o_rs = st.o_row;
+    a.seqQ = c.seqQ; a.seqK = c.seqK; a.nQH = c.nQHeads; a.nKVH = c.nKVHeads; a.batch = c.batch;
+    a.causal = c.causal ? 1 : 0;
+    a.nqb = (c.seqQ + 15) / 16;
+    a.xcd_map = 0;
+    a.sc = kLog2e / sqrtf((float)D);
+    const long long blocks = heads * a.nqb;
+    if (blocks > 0x7fffffffLL) return CDNA4_ERR_INVALID_VALUE;
+    fa_small<D, kBf16, small_waves<D>()><<<(unsigned)blocks, 64 * small_waves<D>(), 0, s>>>(a);
+    return launch_status();
 }
 
 int check_cfg(const cdna3_prefill_cfg* cfg, const void* Q, const void* K, const void* V, const void* O) {
