@@ -29,6 +29,7 @@ def _row_err(got, ref):
     scale = np.maximum(1.0, np.abs(ref).max(axis=1))
     return float((np.abs(got - ref).max(axis=1) / scale).max())
 
+
 MODELS = {
     "gqa_bias_d64": dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab_size=1000,
                          qkv_bias=True),
@@ -147,3 +148,27 @@ def test_cfg5_shape_matches_oracle(tmp_path):
     with cdna4.Session(d, max_seq=128) as s:
         out = s.generate_ex(ids, cdna4.GenerateCfg(6), with_logits=True)
     _check_generation(meta, t, ids, out, 128)
+
+
+def test_cpp_session_program(model):
+    # The reference's C++ usage (Session(model_dir, max_seq).generate(ids, GenerateCfg)) through
+    # include/cdna3/runtime/session.hpp, built host-only (tests/native/generate_demo.cpp): same
+    # tokens and logits as the Python mirror of the same library.
+    import subprocess
+    d, meta, t = model
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "native", "generate_demo")
+    assert os.path.exists(exe), "tests/native not built"
+    ids = _prompt(meta, 17, 4)
+    r = subprocess.run([exe, d, "64", "9"] + [str(i) for i in ids], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    lines = dict(l.split(":", 1) for l in r.stdout.strip().splitlines())
+    got = [int(x) for x in lines["tokens"].split()]
+    assert "rejected" in lines["invalid id"]
+    with cdna4.Session(d, max_seq=64) as s:
+        ref = s.generate(ids, cdna4.GenerateCfg(9))
+        lg = s.prefill_logits(ids)
+    assert got == ref
+    # The C++ process may bind another rocBLAS build than torch's (its prompt GEMMs then sum in
+    # another order), so the logits agree to the parity bound, not bit for bit.
+    assert np.allclose([float(x) for x in lines["logits0"].split()], lg[:4], atol=LOGIT_TOL)
