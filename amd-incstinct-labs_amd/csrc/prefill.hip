@@ -435,7 +435,10 @@ __global__ __launch_bounds__(64 * kF32Waves) void fa_f32(const float* __restrict
 // (batch, head): wave w streams the w-th contiguous part of the visible keys through its own LDS
 // ring (the per-wave loop of the short-cache decode kernel, with the 16 queries as its columns and
 // the causal mask), then the waves merge their (m, l, O) through LDS over their rings.
-template <int D> constexpr int small_waves() { return D == 64 ? 8 : 4; }
+// Waves per workgroup: the LDS holds one two-stage K/V ring per wave (16 KiB per wave at D = 64,
+// 32 KiB at D = 128), so the large form (128 KiB) allows one workgroup per CU and the small form
+// two; the launcher takes the large form when one round of workgroups covers the grid.
+template <int D> constexpr int small_waves(bool large) { return (D == 64 ? 8 : 4) / (large ? 1 : 2); }
 
 template <int D, bool kBf16, int W>
 __global__ __launch_bounds__(64 * W) void fa_small(PrefillArgs a) {
@@ -555,7 +558,10 @@ int dispatch_mfma(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& st, c
     a.sc = kLog2e / sqrtf((float)D);
     const long long blocks = heads * a.nqb;
     if (blocks > 0x7fffffffLL) return CDNA4_ERR_INVALID_VALUE;
-    fa_small<D, kBf16, small_waves<D>()><<<(unsigned)blocks, 64 * small_waves<D>(), 0, s>>>(a);
+    if (blocks <= device_cus())
+        fa_small<D, kBf16, small_waves<D>(true)><<<(unsigned)blocks, 64 * small_waves<D>(true), 0, s>>>(a);
+    else
+        fa_small<D, kBf16, small_waves<D>(false)><<<(unsigned)blocks, 64 * small_waves<D>(false), 0, s>>>(a);
     return launch_status();
 }
 
