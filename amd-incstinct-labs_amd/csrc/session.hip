@@ -25,6 +25,7 @@
 #include <math.h>
 #include <stdio.h>
 #include <string.h>
+#include <exception>
 #include <map>
 #include <string>
 #include <vector>
@@ -375,21 +376,23 @@ struct cdna3_session {
 extern "C" int cdna3_session_create(const char* model_dir, int max_seq, cdna3_session** out) {
     if (!model_dir || !out || max_seq < 1) return CDNA4_ERR_INVALID_VALUE;
     *out = nullptr;
-    cdna3_session* s = new cdna3_session();
-    s->impl.max_seq = max_seq;
-    if (int e = s->impl.read_config(model_dir)) {
-        delete s;
-        return e;
+    cdna3_session* s = nullptr;
+    int e = 0;
+    try {   // host allocations of the loader (file buffers, names) must not unwind through the C ABI
+        s = new cdna3_session();
+        s->impl.max_seq = max_seq;
+        e = s->impl.read_config(model_dir);
+        if (e == 0) e = check_device();
+        if (e == 0) e = (int)hipStreamCreateWithFlags(&s->impl.stream, hipStreamNonBlocking);
+        if (e == 0) e = s->impl.load(model_dir);
+    } catch (const std::exception&) {
+        e = (int)hipErrorOutOfMemory;
     }
-    if (int e = check_device()) {
-        delete s;
-        return e;
-    }
-    int e = (int)hipStreamCreateWithFlags(&s->impl.stream, hipStreamNonBlocking);
-    if (e == 0) e = s->impl.load(model_dir);
     if (e != 0) {
-        s->impl.release();
-        delete s;
+        if (s) {
+            s->impl.release();
+            delete s;
+        }
         return e;
     }
     *out = s;
