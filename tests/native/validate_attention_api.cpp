@@ -4,6 +4,7 @@
 // oracle (liboracle.so, loaded with dlopen). Prints one PASS/FAIL line per configuration and
 // exits 0 only when all pass.
 #include <cdna3/attention.hpp>
+#include <cdna3/llm_integration.hpp>
 #include <hip/hip_runtime.h>
 #include <dlfcn.h>
 #include <cmath>
@@ -33,7 +34,8 @@ static bool close_enough(const std::vector<float>& got, const std::vector<float>
     return w <= 2e-3f;
 }
 
-static bool test_prefill(int D, int seqQ, int seqK, int nQH, int nKVH, int batch, int causal, const char* label) {
+static bool test_prefill(int D, int seqQ, int seqK, int nQH, int nKVH, int batch, int causal, const char* label,
+                         bool torch_op_launcher = false) {
     const size_t qn = (size_t)batch * nQH * seqQ * D, kn = (size_t)batch * nKVH * seqK * D;
     std::vector<float> Q(qn), K(kn), V(kn), Qr(qn), Kr(kn), Vr(kn), O(qn), Og(qn);
     std::vector<uint16_t> hQ(qn), hK(kn), hV(kn), hO(qn);
@@ -49,7 +51,9 @@ static bool test_prefill(int D, int seqQ, int seqK, int nQH, int nKVH, int batch
     CK(hipMemcpy(dK, hK.data(), kn * 2, hipMemcpyHostToDevice));
     CK(hipMemcpy(dV, hV.data(), kn * 2, hipMemcpyHostToDevice));
     cdna3::attn::PrefillCfg cfg{D, seqQ, seqK, nQH, nKVH, batch, causal};
-    const hipError_t e = cdna3::attn::prefill(dQ, dK, dV, dO, cfg);
+    // fa_attn::launch: batch 1, causal, seqQ == seqK (the torch op's launcher)
+    const hipError_t e = torch_op_launcher ? fa_attn::launch(dQ, dK, dV, dO, seqQ, nQH, nKVH, D)
+                                           : cdna3::attn::prefill(dQ, dK, dV, dO, cfg);
     bool ok = false;
     float worst = 0.f;
     if (e != hipSuccess) {
@@ -66,7 +70,7 @@ static bool test_prefill(int D, int seqQ, int seqK, int nQH, int nKVH, int batch
     return ok;
 }
 
-static bool test_decode(int D, int N, int nQH, int nKVH, const char* label) {
+static bool test_decode(int D, int N, int nQH, int nKVH, const char* label, bool torch_op_launcher = false) {
     const size_t qn = (size_t)nQH * D, kn = (size_t)nKVH * N * D;
     std::vector<float> q(qn), K(kn), V(kn), qr(qn), Kr(kn), Vr(kn), o(qn), og(qn);
     std::vector<uint16_t> hq(qn), hK(kn), hV(kn), ho(qn);
@@ -82,7 +86,8 @@ static bool test_decode(int D, int N, int nQH, int nKVH, const char* label) {
     CK(hipMemcpy(dK, hK.data(), kn * 2, hipMemcpyHostToDevice));
     CK(hipMemcpy(dV, hV.data(), kn * 2, hipMemcpyHostToDevice));
     cdna3::attn::DecodeCfg cfg{D, N, nQH, nKVH};
-    const hipError_t e = cdna3::attn::decode(dq, dK, dV, dO, cfg);
+    const hipError_t e = torch_op_launcher ? fa_decode::launch(dq, dK, dV, dO, fa_decode::DCfg{D, N, nQH, nKVH}, 4)
+                                           : cdna3::attn::decode(dq, dK, dV, dO, cfg);
     bool ok = false;
     float worst = 0.f;
     if (e != hipSuccess) {
@@ -127,6 +132,11 @@ int main(int argc, char** argv) {
     chk(test_decode(128, 1024, 32, 8, "GQA D128 N1024 32q8kv"));
     chk(test_decode(128, 4096, 32, 8, "GQA D128 N4096 32q8kv"));
     chk(test_decode(128, 8192, 32, 8, "GQA D128 N8192 32q8kv"));
+    printf("-- torch-op launchers (fa_attn::launch, fa_decode::launch) --\n");
+    chk(test_prefill(128, 256, 256, 4, 2, 1, 1, "fa_attn GQA causal D128 seq256", true));
+    chk(test_prefill(64, 200, 200, 6, 6, 1, 1, "fa_attn MHA causal D64 seq200", true));
+    chk(test_decode(128, 1000, 8, 2, "fa_decode GQA D128 N1000", true));
+    chk(test_decode(64, 77, 4, 4, "fa_decode MHA D64 N77", true));
     printf("Result: %d/%d PASS\n", pass, total);
     return pass == total ? 0 : 1;
 }

@@ -85,6 +85,10 @@ def test_cpp_headers_compile_host_only(tmp_path):
     src = tmp_path / "use.cpp"
     src.write_text(
         "#include <cdna3/attention.hpp>\n#include <cdna3/runtime/forward.hpp>\n#include <cdna3/runtime/session.hpp>\n"
+        "#include <cdna3/llm_integration.hpp>\n"
+        "hipError_t h(const __half* q, const __half* k, const __half* v, __half* o) {\n"
+        "  return fa_attn::launch(q, k, v, o, 256, 8, 2, 128) == hipSuccess\n"
+        "       ? fa_decode::launch(q, k, v, o, fa_decode::DCfg{128, 256, 8, 2}, 4) : hipErrorInvalidValue;\n}\n"
         "std::vector<int> g(cdna3::runtime::Session& s) { return s.generate({1, 2, 3}, {16, -1}); }\n"
         "int f(const __half* q, const __half* k, const __half* v, __half* o) {\n"
         "  cdna3::attn::PrefillCfg p{128, 256, 256, 4, 2, 1, 1};\n"

@@ -227,7 +227,7 @@ def test_cpp_dropin_validation_program():
                        timeout=300)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert "Result: 13/13 PASS" in r.stdout
+    assert "Result: 17/17 PASS" in r.stdout
 
 
 @pytest.mark.parametrize("D,S,HQ,HK,dtype", [(64, 512, 12, 12, torch.float16), (128, 300, 8, 2, torch.bfloat16),
