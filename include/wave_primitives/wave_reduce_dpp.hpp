@@ -5,7 +5,7 @@
 // (research/wave-primitives/include/wave_primitives/wave_reduce_dpp.hpp:56-113):
 //   reduce_sum / reduce_max / reduce_min        result on lane 63
 //   reduce_sum_bcast / _max_bcast / _min_bcast  result on every lane
-//   id_sum / id_max / id_min, SumOp / MaxOp / MinOp, dpp_reduce, bcast_lane63
+//   id_sum / id_max / id_min, SumOp / MaxOp / MinOp, dpp_reduce, dpp_move, bcast_lane63
 //
 // Unlike the reference's lane-63 chain (row_shr 1/2/4/8 + row_bcast15/31, then
 // v_readlane for the broadcast), every reduction here is an all-lanes butterfly
@@ -29,6 +29,14 @@ template <typename T> __device__ __forceinline__ T id_min() { return std::numeri
 using SumOp = xlane::Sum;
 using MaxOp = xlane::Max;
 using MinOp = xlane::Min;
+
+// One DPP move with control code Ctrl (row/bank masks all on): lane i receives the Ctrl-selected
+// lane's v, or old_val where that lane is outside the row (e.g. row_shr:1 = 0x111 gives each row's
+// lane 0 old_val). 32- and 64-bit types (a 64-bit value moves as two 32-bit halves).
+template <int Ctrl, typename T>
+__device__ __forceinline__ T dpp_move(T v, T old_val) {
+    return xlane::dpp<Ctrl>(old_val, v);
+}
 
 // Full-wave combine with an arbitrary associative, commutative functor. The identity
 // argument is kept for signature compatibility; the butterfly never reads it.

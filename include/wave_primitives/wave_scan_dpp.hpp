@@ -4,7 +4,7 @@
 // Same names and semantics as the reference's wave::dpp scans
 // (research/wave-primitives/include/wave_primitives/wave_scan_dpp.hpp:31-87):
 //   scan_inclusive(v, op, identity), scan_inclusive_sum / _max / _min,
-//   scan_exclusive_sum, scan_id_*, ScanSum / ScanMax / ScanMin, scan_lane_id.
+//   scan_exclusive_sum, scan_id_*, ScanSum / ScanMax / ScanMin, scan_lane_id, scan_dpp_step.
 // The in-row part (row_shr 1/2/4/8) is the same Hillis-Steele step the reference
 // uses; the cross-row carry is re-derived for gfx950 from row_newbcast:15 and the
 // permlane16/32 swaps (detail/xlane.hpp) instead of three cascaded row_bcast15.
@@ -28,6 +28,15 @@ using ScanMax = xlane::Max;
 using ScanMin = xlane::Min;
 
 __device__ __forceinline__ unsigned scan_lane_id() { return xlane::lane(); }
+
+// One in-row Hillis-Steele step: op(v, the value Shift lanes below within the 16-lane row), lanes
+// with no such neighbour combining with `identity` (row_shr:Shift, Shift in 1, 2, 4, 8).
+template <int Shift, typename T, typename Op>
+__device__ __forceinline__ T scan_dpp_step(T v, Op op, T identity) {
+    static_assert(Shift == 1 || Shift == 2 || Shift == 4 || Shift == 8, "row_shr 1/2/4/8");
+    const T moved = xlane::dpp<0x110 + Shift>(identity, v);
+    return op(v, moved);
+}
 
 // The identity argument is kept for signature compatibility; Op supplies its own.
 template <typename T, typename Op>

@@ -11,7 +11,7 @@ namespace {
 enum Kind {
     kDppSum = 0, kDppMax, kDppMin, kDppSumBcast, kDppScanSum, kDppScanMax, kDppScanMin, kDppScanExSum,
     kDppBcast63, kPortSum, kPortScanSum, kPortScanExSum, kPortAnd, kPortOr, kDppScanExMax, kSoftmaxLane,
-    kPortMax, kPortMin, kNumKinds
+    kPortMax, kPortMin, kDppMoveShr1, kDppStep1, kDppStep4, kDppStep1248, kNumKinds
 };
 
 template <typename In>
@@ -45,6 +45,17 @@ __global__ void wave_kernel(int kind, const T* in, T* out) {
         case kSoftmaxLane: if constexpr (std::is_same<T, float>::value) r = cdna3::ex::row_softmax_lane(x); break;
         case kPortMax: r = wave::reduce_max(x); break;
         case kPortMin: r = wave::reduce_min(x); break;
+        case kDppMoveShr1: r = wave::dpp::dpp_move<0x111>(x, T(-7)); break;   // row_shr:1, row starts read -7
+        case kDppStep1: r = wave::dpp::scan_dpp_step<1>(x, wave::dpp::ScanSum{}, T(0)); break;
+        case kDppStep4: r = wave::dpp::scan_dpp_step<4>(x, wave::dpp::ScanMax{}, wave::dpp::scan_id_max<T>()); break;
+        case kDppStep1248: {   // the four in-row steps: inclusive prefix within each 16-lane row
+            const wave::dpp::ScanSum op{};
+            r = wave::dpp::scan_dpp_step<1>(x, op, T(0));
+            r = wave::dpp::scan_dpp_step<2>(r, op, T(0));
+            r = wave::dpp::scan_dpp_step<4>(r, op, T(0));
+            r = wave::dpp::scan_dpp_step<8>(r, op, T(0));
+            break;
+        }
         default: break;
     }
     out[i] = r;

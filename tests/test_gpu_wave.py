@@ -14,7 +14,8 @@ from gpu_util import DEV, hooks, ptr, stream
 pytestmark = pytest.mark.gpu
 
 DPP_SUM, DPP_MAX, DPP_MIN, DPP_SUM_B, DPP_SCAN, DPP_SCAN_MAX, DPP_SCAN_MIN, DPP_SCAN_EX, BCAST63, \
-    PORT_SUM, PORT_SCAN, PORT_SCAN_EX, PORT_AND, PORT_OR, DPP_SCAN_EX_MAX, SOFTMAX, PORT_MAX, PORT_MIN = range(18)
+    PORT_SUM, PORT_SCAN, PORT_SCAN_EX, PORT_AND, PORT_OR, DPP_SCAN_EX_MAX, SOFTMAX, PORT_MAX, PORT_MIN, \
+    DPP_MOVE_SHR1, DPP_STEP1, DPP_STEP4, DPP_STEP1248 = range(22)
 TYPES = {oracle.F32: (np.float32, torch.float32), oracle.F64: (np.float64, torch.float64),
          oracle.I32: (np.int32, torch.int32), oracle.I64: (np.int64, torch.int64)}
 
@@ -60,6 +61,21 @@ def test_scan_known_answers_lane_by_lane(dtype):
     assert np.array_equal(run(DPP_SCAN_MIN, dtype, rev), rev)
     assert np.array_equal(run(DPP_SCAN_MAX, dtype, rev), np.full(128, 63))
     assert np.array_equal(run(BCAST63, dtype, lanes), np.full(128, 63))
+
+
+@pytest.mark.parametrize("dtype", list(TYPES))
+def test_dpp_building_blocks_lane_by_lane(dtype):
+    # dpp_move (wave_reduce_dpp.hpp:61-64) and scan_dpp_step (wave_scan_dpp.hpp:43-49): row_shr
+    # moves within 16-lane rows; lanes without a source in their row take old / identity.
+    lanes = np.tile(np.arange(64), 2)
+    r = lanes % 16
+    assert np.array_equal(run(DPP_MOVE_SHR1, dtype, lanes), np.where(r >= 1, lanes - 1, -7))
+    assert np.array_equal(run(DPP_STEP1, dtype, lanes), np.where(r >= 1, 2 * lanes - 1, lanes))
+    rev = np.tile(np.arange(63, -1, -1), 2)
+    rr = np.tile(np.arange(64), 2) % 16
+    assert np.array_equal(run(DPP_STEP4, dtype, rev), np.where(rr >= 4, rev + 4, rev))
+    ones = np.ones(128)
+    assert np.array_equal(run(DPP_STEP1248, dtype, ones), r + 1)   # in-row inclusive prefix
 
 
 def test_integer_scans_and_reductions_bit_exact_random():
