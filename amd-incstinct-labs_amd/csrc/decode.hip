@@ -245,6 +245,7 @@ __global__ __launch_bounds__(64) void decode_merge(const float* __restrict__ par
     float acc[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+#pragma unroll 8   // eight partials' loads in flight at once (the loop was a chain of dependent latencies)
     for (int i = 0; i < P; ++i) {
         const float w = exp2f(ml[2 * i] - Mref);
 #pragma unroll
