@@ -45,6 +45,9 @@ struct DecodeArgs {
     float* part_o;    // [batch][nQH][P][D]
     int N, nQH, nKVH, stride, G, HB, KPW, P;   // HB: groups of <= 16 query heads per kv head
     float sc;         // log2(e) / sqrt(D)
+    // Replayable launches (a captured decode step): when set, the cache length is *len_pos + 1,
+    // read on the device, and the short-cache variant sizes its per-wave key ranges from it.
+    const int* len_pos;
 };
 
 // ---- matrix-core split-K partial -----------------------------------------------------------
@@ -92,8 +95,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void de
     const int qh0 = kvh * a.G + sub * 16;
     const int nrows = min(16, a.G - sub * 16);
 
+    const int N = a.len_pos ? *a.len_pos + 1 : a.N;
     const int kbeg = split * a.KPW;
-    const int kend = min(a.N, kbeg + a.KPW);
+    const int kend = min(N, kbeg + a.KPW);
     const int nch = (kend - kbeg + kDecT - 1) / kDecT;
     const size_t head_off = ((size_t)b * a.nKVH + kvh) * (size_t)a.stride * D;
     const uint16_t* Kh = (const uint16_t*)a.K + head_off;
@@ -118,16 +122,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void de
 #pragma unroll
     for (int i = 0; i < NS - 1; ++i)
         if (i < nch) {
-            load_stage<D>(Kh, D, kbeg + i * kDecT, a.N, k_lds + i * kStage, lane);
-            load_stage<D>(Vh, D, kbeg + i * kDecT, a.N, v_lds + i * kStage, lane);
+            load_stage<D>(Kh, D, kbeg + i * kDecT, N, k_lds + i * kStage, lane);
+            load_stage<D>(Vh, D, kbeg + i * kDecT, N, v_lds + i * kStage, lane);
         }
     int st = 0;   // stage of chunk ch
     for (int ch = 0; ch < nch; ++ch) {
         const int ahead = ch + NS - 1;
         if (ahead < nch) {
             const int sa = (st == 0) ? NS - 1 : st - 1;   // stage of chunk ch - 1, already consumed
-            load_stage<D>(Kh, D, kbeg + ahead * kDecT, a.N, k_lds + sa * kStage, lane);
-            load_stage<D>(Vh, D, kbeg + ahead * kDecT, a.N, v_lds + sa * kStage, lane);
+            load_stage<D>(Kh, D, kbeg + ahead * kDecT, N, k_lds + sa * kStage, lane);
+            load_stage<D>(Vh, D, kbeg + ahead * kDecT, N, v_lds + sa * kStage, lane);
         }
         wait_copies_younger<kCopies>(min(NS - 1, nch - 1 - ch));
         const char* Kt = (const char*)(k_lds + st * kStage);
@@ -167,6 +171,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void de
 template <int D, int W>
 constexpr int wg_ring_elems() { return W * kDecStages * kDecT * D; }
 
+// Keys per wave of the short-cache variant: N split into W ranges of whole 32-key chunks.
+__host__ __device__ constexpr int wg_keys_per_wave(int N, int W) { return ((N + W - 1) / W + kDecT - 1) / kDecT * kDecT; }
+
 template <int D, bool kBf16, int W>
 __global__ __launch_bounds__(64 * W) void decode_wg(DecodeArgs a, void* __restrict__ out) {
     constexpr int ND = D / 32, NDT = D / 16;
@@ -184,15 +191,17 @@ __global__ __launch_bounds__(64 * W) void decode_wg(DecodeArgs a, void* __restri
     const int b = blockIdx.z;
     const int qh0 = kvh * a.G + sub * 16;
     const int nrows = min(16, a.G - sub * 16);
-    const int kbeg = min(a.N, wave * a.KPW);
-    const int kend = min(a.N, kbeg + a.KPW);
+    const int N = a.len_pos ? *a.len_pos + 1 : a.N;
+    const int KPW = a.len_pos ? wg_keys_per_wave(N, W) : a.KPW;
+    const int kbeg = min(N, wave * KPW);
+    const int kend = min(N, kbeg + KPW);
     const size_t head_off = ((size_t)b * a.nKVH + kvh) * (size_t)a.stride * D;
 
     u32x4 qb[1][ND];
     load_q<D>(a, b, qh0, nrows, li, g, qb);
     f32x4 o[1][NDT], lacc[1];
     float m[1];
-    stream_keys<D, kBf16, kDecStages>((const uint16_t*)a.K + head_off, (const uint16_t*)a.V + head_off, D, a.N, kbeg,
+    stream_keys<D, kBf16, kDecStages>((const uint16_t*)a.K + head_off, (const uint16_t*)a.V + head_off, D, N, kbeg,
                                       kend, 0, 0, a.sc, qb, o, lacc, m, k_lds + wave * kRing, v_lds + wave * kRing,
                                       lane);
     __syncthreads();   // every wave is done with its ring: reuse the LDS for the partials
@@ -282,7 +291,7 @@ bool plan_decode(const cdna3_decode_cfg& c, Plan& p) {
     const int W = c.D == 64 ? wg_waves<64>() : wg_waves<128>();
     p.wg = c.N <= W * kWgChunks * kDecT;
     if (p.wg) {   // one workgroup per (batch, kv head, head group); W contiguous key ranges
-        p.KPW = ((c.N + W - 1) / W + kDecT - 1) / kDecT * kDecT;
+        p.KPW = wg_keys_per_wave(c.N, W);
         p.P = 1;
         p.ws_bytes = 0;
         return true;
@@ -302,8 +311,9 @@ bool plan_decode(const cdna3_decode_cfg& c, Plan& p) {
 
 template <int D, bool kBf16>
 int launch_decode(const cdna3_decode_cfg& c, const Plan& p, const void* q, const void* K, const void* V, void* o,
-                  void* ws, hipStream_t s) {
+                  void* ws, hipStream_t s, const int* len_pos = nullptr) {
     DecodeArgs a;
+    a.len_pos = len_pos;
     a.q = q; a.K = K; a.V = V;
     const size_t nml = (size_t)c.batch * c.nQHeads * p.P * 2;
     a.part_ml = (float*)ws;
@@ -350,6 +360,29 @@ int fallback_workspace(size_t need, void** out) {
 }
 
 }  // namespace
+
+// Plan identity for replayed launches: two cache lengths with the same key launch the same grid
+// with the same arguments apart from the length itself. -1 for an invalid configuration.
+long long attn_decode_plan_key(const cdna3_decode_cfg& c) {
+    Plan p;
+    if (!plan_decode(c, p)) return -1;
+    return p.wg ? 1 : ((long long)p.P << 32) | (long long)p.KPW;
+}
+
+// The launches of cdna3_attn_decode planned for cfg->N, but with the cache length read on the
+// device (*len_pos + 1) when they run, so that a captured graph of them serves every length with
+// the same plan key. Used by the runtime's captured decode step; no validation beyond the plan.
+int attn_decode_replayable(const void* q, const void* K, const void* V, void* o, const cdna3_decode_cfg& c, int dtype,
+                           void* ws, size_t ws_bytes, const int* len_pos, hipStream_t s) {
+    Plan p;
+    if (!plan_decode(c, p) || !len_pos || ws_bytes < p.ws_bytes + 256) return CDNA4_ERR_INVALID_VALUE;
+    const bool bf = dtype == CDNA4_BF16;
+    if (c.D == 128) return bf ? launch_decode<128, true>(c, p, q, K, V, o, ws, s, len_pos)
+                              : launch_decode<128, false>(c, p, q, K, V, o, ws, s, len_pos);
+    return bf ? launch_decode<64, true>(c, p, q, K, V, o, ws, s, len_pos)
+              : launch_decode<64, false>(c, p, q, K, V, o, ws, s, len_pos);
+}
+
 }  // namespace cdna4
 
 using namespace cdna4;

@@ -184,6 +184,9 @@ struct GemvArgs {
     uint16_t *q_out, *Kc, *Vc;
     const float *cos_row, *sin_row;
     int D, QD, KVD, pos, max_seq;
+    // replayable step: when set, the position is *pos_dev (read on the device) and cos_row /
+    // sin_row are the bases of the [max_seq][D] tables
+    const int* pos_dev;
     // kLogits
     unsigned long long* partial;   // one (orderable value, ~index) key per wave
 };
@@ -287,11 +290,18 @@ __global__ __launch_bounds__(256) void gemv2(GemvArgs a) {
             h1 = f32_to_f16_bits(f16_bits_to_f32(h1) + f16_bits_to_f32(a.bias[r1]));
         }
         const int half = a.D / 2;
+        int pos = a.pos;
+        const float *cos_row = a.cos_row, *sin_row = a.sin_row;
+        if (a.pos_dev) {
+            pos = *a.pos_dev;
+            cos_row += (size_t)pos * a.D;
+            sin_row += (size_t)pos * a.D;
+        }
         if (r0 < a.QD + a.KVD) {   // Q or K: rotate the pair (d, d + D/2)
             const int d = (r0 % a.D);
             const float t0 = f16_bits_to_f32(h0), t1 = f16_bits_to_f32(h1);
-            h0 = f32_to_f16_bits(t0 * a.cos_row[d] - t1 * a.sin_row[d]);
-            h1 = f32_to_f16_bits(t1 * a.cos_row[d + half] + t0 * a.sin_row[d + half]);
+            h0 = f32_to_f16_bits(t0 * cos_row[d] - t1 * sin_row[d]);
+            h1 = f32_to_f16_bits(t1 * cos_row[d + half] + t0 * sin_row[d + half]);
         }
         if (r0 < a.QD) {
             a.q_out[r0] = (uint16_t)h0;
@@ -299,7 +309,7 @@ __global__ __launch_bounds__(256) void gemv2(GemvArgs a) {
         } else {
             const bool is_k = r0 < a.QD + a.KVD;
             const int rr = r0 - (is_k ? a.QD : a.QD + a.KVD);
-            uint16_t* cache = (is_k ? a.Kc : a.Vc) + ((size_t)(rr / a.D) * a.max_seq + a.pos) * a.D + rr % a.D;
+            uint16_t* cache = (is_k ? a.Kc : a.Vc) + ((size_t)(rr / a.D) * a.max_seq + pos) * a.D + rr % a.D;
             cache[0] = (uint16_t)h0;
             cache[half] = (uint16_t)h1;
         }
@@ -309,10 +319,11 @@ __global__ __launch_bounds__(256) void gemv2(GemvArgs a) {
 // Final argmax over the per-wave keys of the logits GEMV: one workgroup of 1024 lanes, each
 // folding a strided share (loads issued 8 at a time), then the DPP butterfly per wave and wave 0
 // over the 16 wave results. Writes the token to ids[0] (the next step's embedding input) and to
-// tokens[step].
+// tokens[step]. With a device step state {pos, step} (replayable steps), step is read from it
+// and both fields advance by one, ready for the next replay.
 __global__ __launch_bounds__(1024) void argmax_keys(const unsigned long long* __restrict__ keys, int n,
                                                     unsigned long long* __restrict__ scratch, int* __restrict__ ids,
-                                                    int* __restrict__ tokens, int step) {
+                                                    int* __restrict__ tokens, int step, int* __restrict__ state) {
     unsigned long long best = 0;
     for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 1024) {
         unsigned long long k[8];
@@ -337,7 +348,12 @@ __global__ __launch_bounds__(1024) void argmax_keys(const unsigned long long* __
         if (threadIdx.x == 0) {
             const int tok = (int)(0xffffffffu - l2);
             ids[0] = tok;
+            if (state) step = state[1];
             if (tokens) tokens[step] = tok;
+            if (state) {
+                state[0] += 1;
+                state[1] = step + 1;
+            }
         }
     }
 }
@@ -443,14 +459,14 @@ int llm_gemv_residual(const void* x, const void* W, float* out, int N, int K, hi
 
 int llm_gemv_qkv(bool layer, const float* hidden, const void* gain, const void* beta, float eps, const void* W,
                  const void* bias, int H, int D, int nH, int nKV, const float* cos_row, const float* sin_row,
-                 void* q_out, void* Kc, void* Vc, int pos, int max_seq, hipStream_t s) {
+                 void* q_out, void* Kc, void* Vc, int pos, int max_seq, hipStream_t s, const int* pos_dev) {
     if (!gemv_shape_ok(H) || D % 2) return CDNA4_ERR_INVALID_VALUE;
     GemvArgs a{};
     a.x = hidden; a.W = (const uint16_t*)W; a.bias = (const uint16_t*)bias; a.gain = (const uint16_t*)gain;
     a.beta = (const uint16_t*)beta; a.eps = eps; a.K = H;
     a.D = D; a.QD = nH * D; a.KVD = nKV * D; a.rows = a.QD + 2 * a.KVD; a.units = a.rows / 2;
     a.cos_row = cos_row; a.sin_row = sin_row; a.q_out = (uint16_t*)q_out; a.Kc = (uint16_t*)Kc;
-    a.Vc = (uint16_t*)Vc; a.pos = pos; a.max_seq = max_seq;
+    a.Vc = (uint16_t*)Vc; a.pos = pos; a.max_seq = max_seq; a.pos_dev = pos_dev;
     return gemv_dispatch<kQKV>(layer, a, s);
 }
 
@@ -467,13 +483,28 @@ size_t llm_argmax_partials(int V) { return (size_t)(V + 1) / 2; }
 
 int llm_logits_argmax(bool layer, const float* hidden, const void* gain, const void* beta, float eps,
                       const void* W, float* logits, int V, int H, unsigned long long* partial,
-                      unsigned long long* scratch16, int* ids, int* tokens, int step, hipStream_t s) {
+                      unsigned long long* scratch16, int* ids, int* tokens, int step, hipStream_t s, int* state) {
     if (!gemv_shape_ok(H) || V < 1) return CDNA4_ERR_INVALID_VALUE;
     GemvArgs a{};
     a.x = hidden; a.W = (const uint16_t*)W; a.gain = (const uint16_t*)gain; a.beta = (const uint16_t*)beta;
     a.eps = eps; a.out = logits; a.K = H; a.rows = V; a.units = (V + 1) / 2; a.partial = partial;
     if (int e = gemv_dispatch<kLogits>(layer, a, s)) return e;
-    argmax_keys<<<1, 1024, 0, s>>>(partial, a.units, scratch16, ids, tokens, step);
+    argmax_keys<<<1, 1024, 0, s>>>(partial, a.units, scratch16, ids, tokens, step, state);
+    return launch_status();
+}
+
+namespace {
+__global__ void step_state(int* state, int pos, int step) {
+    if (threadIdx.x == 0) {
+        state[0] = pos;
+        state[1] = step;
+    }
+}
+}  // namespace
+
+// Device step state {pos, step} of replayed decode steps.
+int llm_step_state(int* state, int pos, int step, hipStream_t s) {
+    step_state<<<1, 64, 0, s>>>(state, pos, step);
     return launch_status();
 }
 

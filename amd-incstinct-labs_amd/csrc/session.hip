@@ -20,10 +20,15 @@
 //     leaves the device: argmax writes it where the next step's embedding gather reads it, so a
 //     generation of N tokens is one queue of launches and one copy back at the end (unless an
 //     EOS id must be checked after each step).
+//   * The decode step is captured once as a HIP graph and replayed: the position and the token
+//     index live in a device step state that the kernels read and the argmax advances, so one
+//     graph serves every step with the same attention plan (re-captured when the plan changes
+//     with the cache length). CDNA4_SESSION_GRAPH=0 launches the same kernels one by one.
 #include "common.hpp"
 #include <rocblas/rocblas.h>
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 #include <exception>
 #include <map>
@@ -38,13 +43,19 @@ int llm_norm_cast(bool layer, const float* X, const void* W, const void* B, void
 int llm_gemv_residual(const void* x, const void* W, float* out, int N, int K, hipStream_t s);
 int llm_gemv_qkv(bool layer, const float* hidden, const void* gain, const void* beta, float eps, const void* W,
                  const void* bias, int H, int D, int nH, int nKV, const float* cos_row, const float* sin_row,
-                 void* q_out, void* Kc, void* Vc, int pos, int max_seq, hipStream_t s);
+                 void* q_out, void* Kc, void* Vc, int pos, int max_seq, hipStream_t s,
+                 const int* pos_dev = nullptr);
 int llm_gemv_silu(bool layer, const float* hidden, const void* gain, const void* beta, float eps, const void* W,
                   void* act, int F, int H, hipStream_t s);
 size_t llm_argmax_partials(int V);
 int llm_logits_argmax(bool layer, const float* hidden, const void* gain, const void* beta, float eps,
                       const void* W, float* logits, int V, int H, unsigned long long* partial,
-                      unsigned long long* scratch16, int* ids, int* tokens, int step, hipStream_t s);
+                      unsigned long long* scratch16, int* ids, int* tokens, int step, hipStream_t s,
+                      int* state = nullptr);
+int llm_step_state(int* state, int pos, int step, hipStream_t s);
+long long attn_decode_plan_key(const cdna3_decode_cfg& c);
+int attn_decode_replayable(const void* q, const void* K, const void* V, void* o, const cdna3_decode_cfg& c, int dtype,
+                           void* ws, size_t ws_bytes, const int* len_pos, hipStream_t s);
 int llm_silu_mul(const float* gu, void* act, int T, int F, hipStream_t s);
 int llm_bias_add_f16(void* Y, const void* b, int T, int N, hipStream_t s);
 int kv_rope_append(const void* q, const void* k, const void* v, long long ldq, long long ldk, long long ldv,
@@ -134,6 +145,13 @@ struct Session {
     uint16_t *xn = nullptr, *q = nullptr, *qh = nullptr, *attn = nullptr, *act = nullptr;   // q: [T][QD + 2 KVD]
     int *ids = nullptr, *tokens = nullptr;
     std::vector<void*> scratch;
+    // Captured decode step: one graph replayed for every step whose attention plan matches gkey;
+    // positions and the token index live in the device step state dstate = {pos, step}.
+    int* dstate = nullptr;
+    bool use_graph = true;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    long long gkey = -1;
 
     int dmalloc(void** p, size_t bytes, bool is_scratch = false) {
         CK(hipMalloc(p, bytes ? bytes : 16));
@@ -153,15 +171,24 @@ struct Session {
     int load(const std::string& dir);
     int reserve(int T);
     int gemm(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, float beta, int M, int N, int K, int ldy);
-    int run_layers(int T, int pos0);
+    int run_layers(int T, int pos0, const int* pos_dev = nullptr);
     int prefill(const int* host_ids, int T);
+    int decode_step(int pos, int step, bool dev);
+    int replay_step(int pos);
+    void drop_graph() {
+        if (gexec) (void)hipGraphExecDestroy(gexec);
+        if (graph) (void)hipGraphDestroy(graph);
+        gexec = nullptr;
+        graph = nullptr;
+        gkey = -1;
+    }
     int check_ids(const int* host_ids, int T) const {
         if (T < 1 || T > max_seq) return CDNA4_ERR_INVALID_VALUE;
         for (int i = 0; i < T; ++i)
             if (host_ids[i] < 0 || host_ids[i] >= c.vocab_size) return CDNA4_ERR_INVALID_VALUE;
         return 0;
     }
-    int last_token_logits(int T, int step);
+    int last_token_logits(int T, int step, int* state = nullptr);
     void release();
 };
 
@@ -251,6 +278,7 @@ int Session::load(const std::string& dir) {
     CK(dmalloc((void**)&logits, (size_t)V * 4));
     CK(dmalloc((void**)&partial, llm_argmax_partials(V) * 8));
     CK(dmalloc((void**)&scratch16, 16 * 8));
+    CK(dmalloc((void**)&dstate, 2 * sizeof(int)));
     if (rocblas_create_handle(&blas) != rocblas_status_success) return CDNA4_ERR_INVALID_VALUE;
     if (rocblas_set_stream(blas, stream) != rocblas_status_success) return CDNA4_ERR_INVALID_VALUE;
     return (int)hipStreamSynchronize(stream);
@@ -258,6 +286,7 @@ int Session::load(const std::string& dir) {
 
 int Session::reserve(int T) {
     if (T <= cap) return 0;
+    drop_graph();   // it holds the old scratch addresses
     for (void* ptr : scratch) (void)hipFree(ptr);
     scratch.clear();
     const size_t H = c.hidden, F = c.ffn_dim;
@@ -290,7 +319,7 @@ int Session::gemm(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, flo
     return st == rocblas_status_success ? 0 : CDNA4_ERR_INVALID_VALUE;
 }
 
-int Session::run_layers(int T, int pos0) {
+int Session::run_layers(int T, int pos0, const int* pos_dev) {
     const int H = c.hidden, F = c.ffn_dim, D = c.head_dim, nH = c.n_heads, nKV = c.n_kv_heads;
     const int QD = qd(), KVD = kvd();
     const bool lnorm = c.layernorm != 0;
@@ -302,11 +331,14 @@ int Session::run_layers(int T, int pos0) {
         uint16_t* Vl = Vc + layer_kv() * li;
         if (T == 1) {
             // decode step: five launches and the attention; every GEMV streams its weights once
+            const size_t rope_off = pos_dev ? 0 : (size_t)pos0 * D;   // replayed: the kernel adds pos * D
             CK(llm_gemv_qkv(lnorm, hidden, l.n_attn, l.n_attn_b, eps, l.wqkv, l.bqkv, H, D, nH, nKV,
-                            cos_tab + (size_t)pos0 * D, sin_tab + (size_t)pos0 * D, qh, Kl, Vl, pos0, max_seq,
-                            stream));
+                            cos_tab + rope_off, sin_tab + rope_off, qh, Kl, Vl, pos0, max_seq, stream, pos_dev));
             cdna3_decode_cfg dc{D, pos0 + 1, nH, nKV, 1, max_seq};
-            CK(cdna3_attn_decode(qh, Kl, Vl, attn, &dc, CDNA4_F16, dec_ws, dec_ws_bytes, s));
+            if (pos_dev)
+                CK(attn_decode_replayable(qh, Kl, Vl, attn, dc, CDNA4_F16, dec_ws, dec_ws_bytes, pos_dev, stream));
+            else
+                CK(cdna3_attn_decode(qh, Kl, Vl, attn, &dc, CDNA4_F16, dec_ws, dec_ws_bytes, s));
             CK(llm_gemv_residual(attn, l.wo, hidden, H, QD, stream));
             CK(llm_gemv_silu(lnorm, hidden, l.n_mlp, l.n_mlp_b, eps, l.wgu, act, F, H, stream));
             CK(llm_gemv_residual(act, l.wdown, hidden, H, F, stream));
@@ -348,13 +380,48 @@ int Session::prefill(const int* host_ids, int T) {
 
 // Final norm of the last of T rows, lm_head and argmax: the token goes to ids[0] (the next step's
 // input) and tokens[step].
-int Session::last_token_logits(int T, int step) {
+int Session::last_token_logits(int T, int step, int* state) {
     return llm_logits_argmax(c.layernorm != 0, hidden + (size_t)(T - 1) * c.hidden, fnorm, fnorm_b, c.norm_eps,
-                             lm_head, logits, c.vocab_size, c.hidden, partial, scratch16, ids, tokens, step, stream);
+                             lm_head, logits, c.vocab_size, c.hidden, partial, scratch16, ids, tokens, step, stream,
+                             state);
+}
+
+// One decode step at cache position pos, token `step`: embedding of ids[0], every layer, final
+// norm + lm_head + argmax. With dev, the kernels read the position and the token index from the
+// device step state (and the argmax advances it), so the launches are the same for every step.
+int Session::decode_step(int pos, int step, bool dev) {
+    CK(llm_embed(embed, ids, hidden, 1, c.hidden, c.vocab_size, stream));
+    CK(run_layers(1, pos, dev ? dstate : nullptr));
+    return last_token_logits(1, step, dev ? dstate : nullptr);
+}
+
+// The decode step as one graph launch (the ~5 launches per layer then cost ~1.9 us each instead
+// of ~2.7 us as separate launches). The graph is captured on first use and again only when the
+// attention plan changes with the cache length; dstate must hold {pos, step} for this step.
+int Session::replay_step(int pos) {
+    const cdna3_decode_cfg dc{c.head_dim, pos + 1, c.n_heads, c.n_kv_heads, 1, max_seq};
+    const long long key = attn_decode_plan_key(dc);
+    if (key < 0) return CDNA4_ERR_INVALID_VALUE;
+    if (!gexec || key != gkey) {
+        drop_graph();
+        CK(hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed));
+        const int e = decode_step(pos, 0, true);
+        hipGraph_t g = nullptr;
+        const hipError_t ee = hipStreamEndCapture(stream, &g);   // ends the capture on every path
+        if (e != 0 || ee != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            return e != 0 ? e : (int)ee;
+        }
+        graph = g;
+        CK(hipGraphInstantiate(&gexec, graph, nullptr, nullptr, 0));
+        gkey = key;
+    }
+    return (int)hipGraphLaunch(gexec, stream);
 }
 
 void Session::release() {
     if (stream) (void)hipStreamSynchronize(stream);
+    drop_graph();
     for (void* ptr : scratch) (void)hipFree(ptr);
     for (void* ptr : allocs) (void)hipFree(ptr);
     scratch.clear();
@@ -381,6 +448,8 @@ extern "C" int cdna3_session_create(const char* model_dir, int max_seq, cdna3_se
     try {   // host allocations of the loader (file buffers, names) must not unwind through the C ABI
         s = new cdna3_session();
         s->impl.max_seq = max_seq;
+        const char* g = getenv("CDNA4_SESSION_GRAPH");   // "0": separate launches per decode step
+        s->impl.use_graph = !(g && g[0] == '0' && g[1] == 0);
         e = s->impl.read_config(model_dir);
         if (e == 0) e = check_device();
         if (e == 0) e = (int)hipStreamCreateWithFlags(&s->impl.stream, hipStreamNonBlocking);
@@ -435,6 +504,7 @@ extern "C" int cdna3_session_generate(cdna3_session* s, const int* ids, int n_id
         if (step_logits) CK(hipMemcpyAsync(step_logits, S.logits, V * 4, hipMemcpyDeviceToHost, S.stream));
         CK(hipEventRecord(e1, S.stream));
         int produced = 1;
+        if (S.use_graph && max_new_tokens > 1) CK(llm_step_state(S.dstate, n_ids, 1, S.stream));
         for (int step = 1; step < max_new_tokens; ++step) {
             if (eos_token_id >= 0) {
                 int last = -1;
@@ -443,9 +513,8 @@ extern "C" int cdna3_session_generate(cdna3_session* s, const int* ids, int n_id
                 if (last == eos_token_id) break;
             }
             const int pos = n_ids + step - 1;
-            CK(llm_embed(S.embed, S.ids, S.hidden, 1, S.c.hidden, S.c.vocab_size, S.stream));
-            CK(S.run_layers(1, pos));
-            CK(S.last_token_logits(1, step));
+            if (S.use_graph) CK(S.replay_step(pos));
+            else CK(S.decode_step(pos, step, false));
             if (step_logits)
                 CK(hipMemcpyAsync(step_logits + (size_t)step * V, S.logits, V * 4, hipMemcpyDeviceToHost, S.stream));
             ++produced;

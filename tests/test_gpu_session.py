@@ -115,6 +115,26 @@ def test_session_reuse_and_plain_generate(model):
     _check_generation(meta, t, b, fresh, 64)
 
 
+@pytest.mark.parametrize("n,new,max_seq", [(7, 12, 64), (1000, 40, 1100)])
+def test_captured_step_equals_separate_launches(model, monkeypatch, n, new, max_seq):
+    # The decode step replayed as one captured graph (positions in device memory) against the
+    # same kernels launched one by one: identical tokens and bit-identical logits. 1000 + 40
+    # crosses the short-cache limit of the decode attention (1024 keys at D = 128, 2048 at
+    # D = 64), so the graph is captured again when the attention plan changes.
+    d, meta, t = model
+    ids = _prompt(meta, n, 300 + n)
+    outs = []
+    for graph in ("1", "0"):
+        monkeypatch.setenv("CDNA4_SESSION_GRAPH", graph)
+        with cdna4.Session(d, max_seq=max_seq) as s:
+            outs.append(s.generate_ex(ids, cdna4.GenerateCfg(new), with_logits=True))
+            again = s.generate_ex(ids, cdna4.GenerateCfg(new), with_logits=True)   # graph reused
+            assert again["tokens"] == outs[-1]["tokens"]
+            assert np.array_equal(again["logits"], outs[-1]["logits"])
+    assert outs[0]["tokens"] == outs[1]["tokens"]
+    assert np.array_equal(outs[0]["logits"], outs[1]["logits"])
+
+
 def test_eos_and_full_cache_stop_generation(model):
     d, meta, _ = model
     ids = _prompt(meta, 12, 3)
