@@ -102,6 +102,102 @@ def cpu_baseline_prefill():
                       f"identical, so the full config takes 128x as long"}
 
 
+def cpu_threads():
+    """Worker threads for the threaded CPU figures: the cores this process may use, at most 16
+    (one GPU's share of the box)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_baseline_prefill_threads():
+    """The same fp32 prefill on one (batch, head) of config 3 per thread, all threads at once
+    (labelled as threaded: the reference's CPU path is single-threaded; ctypes releases the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+    sys.path.insert(0, ROOT)
+    import oracle
+    S, D = 8192, 128
+    n = cpu_threads()
+    q, k, v = oracle.normal(11, S * D), oracle.normal(12, S * D), oracle.normal(13, S * D)
+    use_ref = oracle.ref_lib("ref_attention_api") is not None
+    run = oracle.ref_prefill if use_ref else oracle.prefill
+    t = time.perf_counter()
+    with ThreadPoolExecutor(n) as ex:
+        list(ex.map(lambda _: run(q, k, v, D, S, S, 1, 1, 1, 1), range(n)))
+    dt = time.perf_counter() - t
+    flop = 4.0 * D * S * (S + 1) / 2
+    return {"value": n * flop / dt / 1e12, "unit": "TFLOPS", "cores": n, "kind": "reference" if use_ref else "port",
+            "sample": f"{n} (batch, head) units of config 3 on {n} threads at once, {dt:.1f} s"}
+
+
+def cpu_baseline_decode():
+    """Reference cpu_decode (oracle/_ref; the oracle's restatement without it) on batch elements of
+    config 4, one thread: every batch element is the same work (32 q heads over 8 kv heads, N =
+    8192, D = 128), so 8 of the 32 give the full rate. GB/s counts the same algorithmic (fp16) bytes
+    as the GPU figure."""
+    sys.path.insert(0, ROOT)
+    import oracle
+    HQ, HK, D, N, nb = 32, 8, 128, 8192, 8
+    q = oracle.normal(21, HQ * D)
+    K = oracle.normal(22, HK * N * D)
+    V = oracle.normal(23, HK * N * D)
+    use_ref = oracle.ref_lib("ref_attention_api") is not None
+    t = time.perf_counter()
+    for _ in range(nb):
+        if use_ref:
+            oracle.ref_decode(q, K, V, D, N, HQ, HK)
+        else:
+            oracle.decode(q, K, V, D, N, HQ, HK)
+    dt = (time.perf_counter() - t) / nb
+    nbytes = 2.0 * HK * N * D * 2 + 2.0 * HQ * D * 2
+    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "reference" if use_ref else "port",
+            "sample": f"{nb} of the 32 batch elements of config 4, {dt * 1e3:.0f} ms each"}
+
+
+def cpu_baseline_cfg1():
+    """The reference's attn_cpu_ref (oracle/_ref fa_steps; the oracle's restatement without it) over
+    all 8 heads of config 1, one thread."""
+    sys.path.insert(0, ROOT)
+    import oracle
+    H, S, D = 8, 512, 64
+    Q, K, V = (oracle.normal(31 + i, H * S * D).reshape(H, S * D) for i in range(3))
+    use_ref = oracle.ref_lib("ref_fa_steps") is not None
+    t = time.perf_counter()
+    for h in range(H):
+        if use_ref:
+            oracle.ref_attn_cpu_ref(Q[h], K[h], V[h], S, S, D)
+        else:
+            oracle.prefill(Q[h], K[h], V[h], D, S, S, 1, 1, 1, 0)
+    dt = time.perf_counter() - t
+    flop = 4.0 * H * S * S * D
+    return {"value": flop / dt / 1e12, "unit": "TFLOPS", "us": dt * 1e6, "cores": 1,
+            "kind": "reference" if use_ref else "port", "sample": "the full config 1 (8 heads), fp32"}
+
+
+def cpu_baseline_dpp():
+    """Config 2 on the CPU, one thread: the oracle's reduce_sum and inclusive scan_sum over 2^26 f32
+    and i32 values (f32 combined in fp64, as the oracle's checker does)."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    import oracle
+    n = 1 << 26
+    rng = np.random.default_rng(2)
+    out = {"cores": 1, "kind": "port", "unit": "GB/s", "sample": "n = 2^26, f32 and i32, reduce_sum and scan_sum"}
+    for name, code, x in (("f32", oracle.F32, rng.uniform(-1, 1, n).astype(np.float32)),
+                          ("i32", oracle.I32, rng.integers(-1000, 1001, n, dtype=np.int32))):
+        t = time.perf_counter()
+        oracle.reduce(oracle.SUM, code, x)
+        dr = time.perf_counter() - t
+        t = time.perf_counter()
+        y = oracle.scan_inclusive(oracle.SUM, code, x)
+        ds = time.perf_counter() - t
+        out[name] = {"reduce_sum": round(n * 4 / dr / 1e9, 2), "scan_sum": round(n * 8 / ds / 1e9, 2)}
+        del y
+    return out
+
+
 def bench_prefill(torch, cdna4, steps, warmup):
     B, H, S, D = 4, 32, 8192, 128
     g = torch.Generator(device="cuda").manual_seed(0)
@@ -303,8 +399,16 @@ def main():
             l = result["llm"]
             result.update({"value": l["value"], "unit": l["unit"], "ms_per_step": l["ms_per_token"],
                            "config": l["config"], "roofline": l["roofline"], "dtype": "fp16"})
-    if "prefill" in args.legs and not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline_prefill()
+    if not args.no_cpu_baseline:   # host-side figures, after every GPU leg
+        if "prefill" in args.legs:
+            result["cpu_baseline"] = cpu_baseline_prefill()
+            result["cpu_baseline_threads"] = cpu_baseline_prefill_threads()
+        if "decode" in args.legs:
+            result["decode"]["cpu_baseline"] = cpu_baseline_decode()
+        if "cfg1" in args.legs:
+            result["cfg1"]["cpu_baseline"] = cpu_baseline_cfg1()
+        if "dpp" in args.legs:
+            result["dpp"]["cpu_baseline"] = cpu_baseline_dpp()
     print(json.dumps(result), flush=True)
 
 
