@@ -21,7 +21,9 @@ Also reported in the same line:
 Kernel durations come from HIP events recorded on the stream the kernels run on (torch's current
 stream). The CPU baseline times the reference's own fp32 cpu_prefill (built from the reference
 sources into oracle/_ref) on one (batch, head) of config 3, one thread; the oracle's restatement
-is timed instead when oracle/_ref is absent.
+is timed instead when oracle/_ref is absent. `cpu_baseline_threads` is the same work on one
+(batch, head) per thread, up to 16 threads, labelled as such; the decode, cfg1 and dpp legs carry
+their own one-thread CPU figures (reference cpu_decode, attn_cpu_ref; the oracle's reduce/scan).
 """
 import argparse
 import json
