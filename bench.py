@@ -114,6 +114,20 @@ def cpu_threads():
     return max(1, min(16, n))
 
 
+def cpu_host():
+    """The host the CPU figures ran on: CPU model, logical CPUs, and the CPUs this process may use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu": model, "nproc": os.cpu_count(), "usable": cpu_threads()}
+
+
 def cpu_baseline_prefill_threads():
     """The same fp32 prefill on one (batch, head) of config 3 per thread, all threads at once
     (labelled as threaded: the reference's CPU path is single-threaded; ctypes releases the GIL)."""
@@ -402,6 +416,7 @@ def main():
             result.update({"value": l["value"], "unit": l["unit"], "ms_per_step": l["ms_per_token"],
                            "config": l["config"], "roofline": l["roofline"], "dtype": "fp16"})
     if not args.no_cpu_baseline:   # host-side figures, after every GPU leg
+        result["cpu_host"] = cpu_host()
         if "prefill" in args.legs:
             result["cpu_baseline"] = cpu_baseline_prefill()
             result["cpu_baseline_threads"] = cpu_baseline_prefill_threads()
