@@ -106,5 +106,43 @@ __device__ __forceinline__ void stream_keys(const uint16_t* Kh, const uint16_t* 
     }
 }
 
+// Workgroup merge after W waves have each run stream_keys over their own key range: the waves
+// leave their (m, l, O) in LDS (po over the K rings, pml over the V rings, after a barrier that
+// ends every ring's use), then all W * 64 lanes merge pairs of adjacent outputs,
+// o = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w, and store them as 16-bit pairs to
+// out[h * D + d] for the nrows query heads (columns) h < nrows.
+template <int D, bool kBf16, int W>
+__device__ __forceinline__ void merge_waves(const f32x4 (&o)[1][D / 16], const f32x4 (&lacc)[1], const float (&m)[1],
+                                            float* po, float* pml, int nrows, uint16_t* out, int wave, int lane) {
+    constexpr int NDT = D / 16;
+    const int li = lane & 15, g = lane >> 4;
+    __syncthreads();   // every wave is done with its ring: reuse the LDS for the partials
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+        *(f32x4*)(po + ((size_t)wave * 16 + li) * D + dt * 16 + g * 4) = o[0][dt];
+    if (g == 0) {
+        pml[(wave * 16 + li) * 2] = m[0];
+        pml[(wave * 16 + li) * 2 + 1] = lacc[0][0];
+    }
+    __syncthreads();
+    for (int p = (int)threadIdx.x; p < nrows * (D / 2); p += 64 * W) {
+        const int h = p / (D / 2), d = 2 * (p % (D / 2));
+        float M = tile::kInitM;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, pml[(w * 16 + h) * 2]);
+        float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float wt = exp2f(pml[(w * 16 + h) * 2] - M);
+            L = fmaf(wt, pml[(w * 16 + h) * 2 + 1], L);
+            const float2 v = *(const float2*)(po + ((size_t)w * 16 + h) * D + d);
+            o0 = fmaf(wt, v.x, o0);
+            o1 = fmaf(wt, v.y, o1);
+        }
+        const float inv = L > 0.f ? 1.f / L : 1.f;
+        *(uint32_t*)(out + (size_t)h * D + d) = tile::pack2<kBf16>(o0 * inv, o1 * inv);
+    }
+}
+
 }  // namespace stream
 }  // namespace cdna4

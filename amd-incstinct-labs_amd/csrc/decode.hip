@@ -204,35 +204,8 @@ __global__ __launch_bounds__(64 * W) void decode_wg(DecodeArgs a, void* __restri
     stream_keys<D, kBf16, kDecStages>((const uint16_t*)a.K + head_off, (const uint16_t*)a.V + head_off, D, N, kbeg,
                                       kend, 0, 0, a.sc, qb, o, lacc, m, k_lds + wave * kRing, v_lds + wave * kRing,
                                       lane);
-    __syncthreads();   // every wave is done with its ring: reuse the LDS for the partials
-    float* po = (float*)k_lds;   // [W][16 heads][D]
-    float* pml = (float*)v_lds;  // [W][16 heads][2]
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-        *(f32x4*)(po + ((size_t)wave * 16 + li) * D + dt * 16 + g * 4) = o[0][dt];
-    if (g == 0) {
-        pml[(wave * 16 + li) * 2] = m[0];
-        pml[(wave * 16 + li) * 2 + 1] = lacc[0][0];
-    }
-    __syncthreads();
-    // each lane merges pairs of adjacent outputs (head, d .. d + 1)
-    for (int p = (int)threadIdx.x; p < nrows * (D / 2); p += 64 * W) {
-        const int h = p / (D / 2), d = 2 * (p % (D / 2));
-        float M = tile::kInitM;
-#pragma unroll
-        for (int w = 0; w < W; ++w) M = fmaxf(M, pml[(w * 16 + h) * 2]);
-        float L = 0.f, o0 = 0.f, o1 = 0.f;
-#pragma unroll
-        for (int w = 0; w < W; ++w) {
-            const float wt = exp2f(pml[(w * 16 + h) * 2] - M);
-            L = fmaf(wt, pml[(w * 16 + h) * 2 + 1], L);
-            const float2 v = *(const float2*)(po + ((size_t)w * 16 + h) * D + d);
-            o0 = fmaf(wt, v.x, o0);
-            o1 = fmaf(wt, v.y, o1);
-        }
-        const float inv = L > 0.f ? 1.f / L : 1.f;
-        *(uint32_t*)((uint16_t*)out + ((size_t)b * a.nQH + qh0 + h) * D + d) = pack2<kBf16>(o0 * inv, o1 * inv);
-    }
+    merge_waves<D, kBf16, W>(o, lacc, m, (float*)k_lds, (float*)v_lds, nrows,
+                             (uint16_t*)out + ((size_t)b * a.nQH + qh0) * D, wave, lane);
 }
 
 // One wave per (batch, query head): o = sum_i 2^(m_i - M) O_i / sum_i 2^(m_i - M) l_i.
