@@ -12,7 +12,8 @@
 // the reference ran as separate passes (norm + cast; GEMV + bias; GEMV + residual add; gate and
 // up GEMVs + SiLU product). The next token id stays on the device (argmax writes it, the
 // embedding gather reads it), so decode steps queue back to back without a host round trip.
-// Cross-lane sums use the wave64 DPP butterfly; nothing uses LDS.
+// Cross-lane sums use the wave64 DPP butterfly; the only LDS is the four partial sums per row of the
+// residual GEMV.
 #include "common.hpp"
 #include "wave_primitives/detail/xlane.hpp"
 #include <math.h>
@@ -156,9 +157,9 @@ __global__ __launch_bounds__(256) void norm_cast(const float* __restrict__ X, co
 }
 
 // ---- decode-step GEMVs (batch 1) ---------------------------------------------------------------
-// y = W x with W row-major [rows][K] fp16 and fp32 accumulation. Each wave computes two rows; all
-// W and x loads of the wave are issued before any arithmetic. Variants:
-//   kResidual  x fp16, rows 2u, 2u + 1:  out32[r] += y                    (O and down projections)
+// y = W x with W row-major [rows][K] fp16 and fp32 accumulation, x = a norm of the fp32 hidden row
+// (each wave forms it from the row in registers). Each wave computes two rows; all W and x loads
+// of the wave are issued before any arithmetic. Variants:
 //   kQKV       x = norm(hidden) rounded to fp16 (the fused attention-input norm); unit u of the
 //              Q block (or K, V block) takes rows d and d + D/2 of one head, so the epilogue
 //              rounds y to fp16, adds the bias (rounded again, as the reference's GEMM + bias
@@ -169,16 +170,16 @@ __global__ __launch_bounds__(256) void norm_cast(const float* __restrict__ X, co
 //   kLogits    x = final norm(hidden) in fp32 (unrounded, as the reference's lm_head reads it);
 //              rows 2u, 2u + 1: logits[r] = y, and the wave's (max, first index) pair goes to
 //              the argmax partials
-enum GemvKind { kResidual = 0, kQKV = 1, kSiluMul = 2, kLogits = 3 };
+enum GemvKind { kQKV = 0, kSiluMul = 1, kLogits = 2 };
 
 struct GemvArgs {
-    const void* x;            // fp16 input (kResidual) or fp32 hidden row (the others)
+    const float* x;           // fp32 hidden row
     const uint16_t* W;
     const uint16_t* bias;     // kQKV: [QD + 2 KVD] or null
     const uint16_t* gain;     // norm weight
     const uint16_t* beta;     // norm bias or null
     float eps;
-    void* out;                // kResidual: f32 [rows]; kSiluMul: f16 [F]; kLogits: f32 logits [V]
+    void* out;                // kSiluMul: f16 [F]; kLogits: f32 logits [V]
     int units, K, rows;       // units = waves with work; rows = rows of W (kLogits: V)
     // kQKV
     uint16_t *q_out, *Kc, *Vc;
@@ -223,20 +224,10 @@ __global__ __launch_bounds__(256) void gemv2(GemvArgs a) {
     load_f16_row<J>(a.W + (size_t)r0 * K, C, lane, w0);
     load_f16_row<J>(a.W + (size_t)r1 * K, C, lane, w1);
     float y0 = 0.f, y1 = 0.f;
-    if constexpr (kKind == kResidual) {
-        u32x4 xv[J];
-#pragma unroll
-        for (int j = 0; j < J; ++j) xv[j] = ((const u32x4*)a.x)[chunk(lane, j, C)];
-#pragma unroll
-        for (int j = 0; j < J; ++j)
-            if (lane + 64 * j < C) {
-                y0 = dot8(w0[j], xv[j], y0);
-                y1 = dot8(w1[j], xv[j], y1);
-            }
-    } else {
+    {
         f32x4 lo[J], hi[J];
         u32x4 g[J], b[J];
-        load_f32_row<J>((const float*)a.x, C, lane, lo, hi);
+        load_f32_row<J>(a.x, C, lane, lo, hi);
         load_f16_row<J>(a.gain, C, lane, g);
         if (a.beta) load_f16_row<J>(a.beta, C, lane, b);
         float mean, inv;
@@ -277,11 +268,7 @@ __global__ __launch_bounds__(256) void gemv2(GemvArgs a) {
         return;
     }
     if (lane != 0) return;
-    if constexpr (kKind == kResidual) {
-        float* o = (float*)a.out;
-        o[r0] += y0;
-        if (r1 != r0) o[r1] += y1;
-    } else if constexpr (kKind == kSiluMul) {
+    if constexpr (kKind == kSiluMul) {
         ((uint16_t*)a.out)[r0] = (uint16_t)f32_to_f16_bits(y0 / (1.f + expf(-y0)) * y1);
     } else {   // kQKV
         uint32_t h0 = f32_to_f16_bits(y0), h1 = f32_to_f16_bits(y1);
@@ -313,6 +300,45 @@ __global__ __launch_bounds__(256) void gemv2(GemvArgs a) {
             cache[0] = (uint16_t)h0;
             cache[half] = (uint16_t)h1;
         }
+    }
+}
+
+// out32[r] += W[r][:] . x for fp16 x (the O and down projections of a decode step): one workgroup
+// per row, the row's 16-byte chunks split over its four waves (wave w: chunks q0 + l + 64 j of its
+// quarter, lane l), so a 768-row GEMV still spreads over every CU instead of the 96 workgroups of
+// two rows per wave (measured +3.6 % tokens/s for the config-5 decode step over that form). The
+// four partial sums meet in LDS and are added in wave order. All loads are issued before any
+// arithmetic.
+constexpr int kSplitWaves = 4;
+
+template <int J>
+__global__ __launch_bounds__(64 * kSplitWaves) void gemv_residual_split(const uint16_t* __restrict__ x,
+                                                                        const uint16_t* __restrict__ W,
+                                                                        float* __restrict__ out, int K) {
+    __shared__ float part[kSplitWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int C = K / 8, Q = (C + kSplitWaves - 1) / kSplitWaves;   // chunks per row, per wave
+    const int q0 = wave * Q, qn = min(C, q0 + Q) - q0;              // this wave's chunks (qn may be <= 0)
+    const int row = blockIdx.x;
+    u32x4 w[J], xv[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {   // loads clamped into the row, masked below
+        const int c = min(q0 + min(lane + 64 * j, max(qn - 1, 0)), C - 1);
+        xv[j] = ((const u32x4*)x)[c];
+        w[j] = __builtin_nontemporal_load((const u32x4*)(W + (size_t)row * K) + c);
+    }
+    float y = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+        if (lane + 64 * j < qn) y = dot8(w[j], xv[j], y);
+    y = allreduce(y, Sum{});
+    if (lane == 0) part[wave] = y;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float acc = part[0];
+#pragma unroll
+        for (int i = 1; i < kSplitWaves; ++i) acc += part[i];
+        out[row] += acc;
     }
 }
 
@@ -419,12 +445,6 @@ int gemv_dispatch(bool layer, const GemvArgs& a, hipStream_t s) {
         case 4: gemv_launch<kKind, 4>(layer, a, s); break;
         case 6: gemv_launch<kKind, 6>(layer, a, s); break;
         case 8: gemv_launch<kKind, 8>(layer, a, s); break;
-        case 12:
-            if constexpr (kKind == kResidual) { gemv_launch<kKind, 12>(layer, a, s); break; }
-            return CDNA4_ERR_INVALID_VALUE;
-        case 16:
-            if constexpr (kKind == kResidual) { gemv_launch<kKind, 16>(layer, a, s); break; }
-            return CDNA4_ERR_INVALID_VALUE;
         default: return CDNA4_ERR_INVALID_VALUE;
     }
     return launch_status();
@@ -452,9 +472,16 @@ int llm_norm_cast(bool layer, const float* X, const void* W, const void* B, void
 
 int llm_gemv_residual(const void* x, const void* W, float* out, int N, int K, hipStream_t s) {
     if (!gemv_shape_ok(K, true) || N < 1) return CDNA4_ERR_INVALID_VALUE;
-    GemvArgs a{};
-    a.x = x; a.W = (const uint16_t*)W; a.out = out; a.K = K; a.rows = N; a.units = (N + 1) / 2;
-    return gemv_dispatch<kResidual>(false, a, s);
+    const int q = (K / 8 + kSplitWaves - 1) / kSplitWaves;   // chunks per wave: at most 256 (K <= 8192)
+    const uint16_t *xx = (const uint16_t*)x, *WW = (const uint16_t*)W;
+    const unsigned grid = (unsigned)N, block = 64 * kSplitWaves;
+    switch ((q + 63) / 64) {
+        case 1: gemv_residual_split<1><<<grid, block, 0, s>>>(xx, WW, out, K); break;
+        case 2: gemv_residual_split<2><<<grid, block, 0, s>>>(xx, WW, out, K); break;
+        case 3: gemv_residual_split<3><<<grid, block, 0, s>>>(xx, WW, out, K); break;
+        default: gemv_residual_split<4><<<grid, block, 0, s>>>(xx, WW, out, K); break;
+    }
+    return launch_status();
 }
 
 int llm_gemv_qkv(bool layer, const float* hidden, const void* gain, const void* beta, float eps, const void* W,

@@ -130,14 +130,19 @@ def test_wave_primitives_use_no_lds_and_no_readlane(tmp_path):
 
 def test_library_kernels_avoid_lds_where_designed_to(tmp_path):
     # Reductions, scans, norms, KV-cache and runtime kernels and the decode merge are LDS-free by design; prefill and the
-    # decode kernels (split partials and the short-cache workgroup variant) stage K/V in LDS.
+    # decode kernels (split partials and the short-cache workgroup variant) stage K/V in LDS, and the residual GEMV
+    # of the runtime meets its four waves' partial sums of a row in LDS (one write per wave, one read of four).
     for src in ("reduce_scan.hip", "norms.hip", "decode.hip", "kv_cache.hip", "llm.hip"):
         asm = _device_asm(os.path.join(ROOT, "amd-incstinct-labs_amd", "csrc", src), tmp_path)
         for name, body in _functions(asm).items():
             assert not re.search(r"v_pk_(add|mul|fma)_f32", body), (src, name)
             if "decode_mfma" in name or "decode_wg" in name:
                 continue
-            assert not re.search(r"^\s+ds_", body, re.M), (src, name)
+            ds = re.findall(r"^\s+(ds_\w+)", body, re.M)
+            if "gemv_residual_split" in name:
+                assert len(ds) <= 4, (src, name, ds)
+                continue
+            assert not ds, (src, name)
 
 
 def test_decode_kernel_streams_kv_through_lds_onto_matrix_cores(tmp_path):
