@@ -181,6 +181,7 @@ struct GemvArgs {
     float eps;
     void* out;                // kSiluMul: f16 [F]; kLogits: f32 logits [V]
     int units, K, rows;       // units = waves with work; rows = rows of W (kLogits: V)
+    int pairs;                // row pairs (NP per wave)
     // kQKV
     uint16_t *q_out, *Kc, *Vc;
     const float *cos_row, *sin_row;
@@ -199,31 +200,44 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
     return ((unsigned long long)u << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
 }
 
-template <int kKind, int J, bool kLayer>
-__global__ __launch_bounds__(256) void gemv2(GemvArgs a) {
-    const int unit = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (unit >= a.units) return;
-    const int K = a.K, C = K / 8;
-    int r0, r1;
+// Rows (r0, r1) of row pair p of a GEMV kind (see above).
+template <int kKind>
+__device__ __forceinline__ void pair_rows(const GemvArgs& a, int p, int& r0, int& r1) {
     if constexpr (kKind == kQKV) {
         const int half = a.D / 2;
-        int base = 0, u = unit;
+        int base = 0, u = p;
         if (u >= a.QD / 2 + a.KVD / 2) { base = a.QD + a.KVD; u -= a.QD / 2 + a.KVD / 2; }
         else if (u >= a.QD / 2) { base = a.QD; u -= a.QD / 2; }
         r0 = base + (u / half) * a.D + u % half;
         r1 = r0 + half;
     } else if constexpr (kKind == kSiluMul) {
-        r0 = unit;
-        r1 = unit + a.rows / 2;
+        r0 = p;
+        r1 = p + a.rows / 2;
     } else {
-        r0 = 2 * unit;
-        r1 = min(2 * unit + 1, a.rows - 1);
+        r0 = 2 * p;
+        r1 = min(2 * p + 1, a.rows - 1);
     }
-    u32x4 w0[J], w1[J];
-    load_f16_row<J>(a.W + (size_t)r0 * K, C, lane, w0);
-    load_f16_row<J>(a.W + (size_t)r1 * K, C, lane, w1);
-    float y0 = 0.f, y1 = 0.f;
+}
+
+// Each wave takes NP consecutive row pairs, so the norm of the hidden row (loaded, reduced and
+// formed in every wave) is paid once per 2 NP rows.
+template <int kKind, int J, bool kLayer, int NP>
+__global__ __launch_bounds__(256) void gemv2(GemvArgs a) {
+    const int unit = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (unit >= a.units) return;
+    const int K = a.K, C = K / 8;
+    int r0[NP], r1[NP];
+    u32x4 w0[NP][J], w1[NP][J];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        pair_rows<kKind>(a, min(unit * NP + p, a.pairs - 1), r0[p], r1[p]);
+        load_f16_row<J>(a.W + (size_t)r0[p] * K, C, lane, w0[p]);
+        load_f16_row<J>(a.W + (size_t)r1[p] * K, C, lane, w1[p]);
+    }
+    float y0[NP], y1[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) y0[p] = y1[p] = 0.f;
     {
         f32x4 lo[J], hi[J];
         u32x4 g[J], b[J];
@@ -239,8 +253,11 @@ __global__ __launch_bounds__(256) void gemv2(GemvArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float xe = normed<J>(lo, hi, g, b, a.beta != nullptr, j, e, mean, inv);
-                    y0 = fmaf(half_of(w0[j], e), xe, y0);
-                    y1 = fmaf(half_of(w1[j], e), xe, y1);
+#pragma unroll
+                    for (int p = 0; p < NP; ++p) {
+                        y0[p] = fmaf(half_of(w0[p][j], e), xe, y0[p]);
+                        y1[p] = fmaf(half_of(w1[p][j], e), xe, y1[p]);
+                    }
                 }
             } else {
                 u32x4 xn;
@@ -249,56 +266,72 @@ __global__ __launch_bounds__(256) void gemv2(GemvArgs a) {
                     xn[e >> 1] = f32_to_f16_bits(normed<J>(lo, hi, g, b, a.beta != nullptr, j, e, mean, inv)) |
                                  (f32_to_f16_bits(normed<J>(lo, hi, g, b, a.beta != nullptr, j, e + 1, mean, inv))
                                   << 16);
-                y0 = dot8(w0[j], xn, y0);
-                y1 = dot8(w1[j], xn, y1);
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    y0[p] = dot8(w0[p][j], xn, y0[p]);
+                    y1[p] = dot8(w1[p][j], xn, y1[p]);
+                }
             }
         }
     }
-    y0 = allreduce(y0, Sum{});
-    y1 = allreduce(y1, Sum{});
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        y0[p] = allreduce(y0[p], Sum{});
+        y1[p] = allreduce(y1[p], Sum{});
+    }
+    if (lane != 0) return;   // every lane holds the sums: lane 0 stores
     if constexpr (kKind == kLogits) {
-        // every lane holds the sums: lane 0 stores, the wave's partial argmax needs no shuffle
-        if (lane == 0) {
-            float* lg = (float*)a.out;
-            lg[r0] = y0;
-            if (r1 != r0) lg[r1] = y1;
-            unsigned long long k0 = argmax_key(y0, r0), k1 = argmax_key(y1, r1);
-            a.partial[unit] = k0 > k1 ? k0 : k1;
+        float* lg = (float*)a.out;
+        unsigned long long best = 0ull;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            if (unit * NP + p >= a.pairs) continue;
+            lg[r0[p]] = y0[p];
+            if (r1[p] != r0[p]) lg[r1[p]] = y1[p];
+            const unsigned long long k0 = argmax_key(y0[p], r0[p]), k1 = argmax_key(y1[p], r1[p]);
+            const unsigned long long k = k0 > k1 ? k0 : k1;
+            best = k > best ? k : best;
         }
+        a.partial[unit] = best;   // the wave's (max, first index) key for the argmax
         return;
     }
-    if (lane != 0) return;
-    if constexpr (kKind == kSiluMul) {
-        ((uint16_t*)a.out)[r0] = (uint16_t)f32_to_f16_bits(y0 / (1.f + expf(-y0)) * y1);
-    } else {   // kQKV
-        uint32_t h0 = f32_to_f16_bits(y0), h1 = f32_to_f16_bits(y1);
-        if (a.bias) {
-            h0 = f32_to_f16_bits(f16_bits_to_f32(h0) + f16_bits_to_f32(a.bias[r0]));
-            h1 = f32_to_f16_bits(f16_bits_to_f32(h1) + f16_bits_to_f32(a.bias[r1]));
-        }
-        const int half = a.D / 2;
-        int pos = a.pos;
-        const float *cos_row = a.cos_row, *sin_row = a.sin_row;
-        if (a.pos_dev) {
-            pos = *a.pos_dev;
-            cos_row += (size_t)pos * a.D;
-            sin_row += (size_t)pos * a.D;
-        }
-        if (r0 < a.QD + a.KVD) {   // Q or K: rotate the pair (d, d + D/2)
-            const int d = (r0 % a.D);
-            const float t0 = f16_bits_to_f32(h0), t1 = f16_bits_to_f32(h1);
-            h0 = f32_to_f16_bits(t0 * cos_row[d] - t1 * sin_row[d]);
-            h1 = f32_to_f16_bits(t1 * cos_row[d + half] + t0 * sin_row[d + half]);
-        }
-        if (r0 < a.QD) {
-            a.q_out[r0] = (uint16_t)h0;
-            a.q_out[r1] = (uint16_t)h1;
-        } else {
-            const bool is_k = r0 < a.QD + a.KVD;
-            const int rr = r0 - (is_k ? a.QD : a.QD + a.KVD);
-            uint16_t* cache = (is_k ? a.Kc : a.Vc) + ((size_t)(rr / a.D) * a.max_seq + pos) * a.D + rr % a.D;
-            cache[0] = (uint16_t)h0;
-            cache[half] = (uint16_t)h1;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        if (unit * NP + p >= a.pairs) continue;
+        const float ya = y0[p], yb = y1[p];
+        const int ra = r0[p], rb = r1[p];
+        if constexpr (kKind == kSiluMul) {
+            ((uint16_t*)a.out)[ra] = (uint16_t)f32_to_f16_bits(ya / (1.f + expf(-ya)) * yb);
+        } else {   // kQKV
+            uint32_t h0 = f32_to_f16_bits(ya), h1 = f32_to_f16_bits(yb);
+            if (a.bias) {
+                h0 = f32_to_f16_bits(f16_bits_to_f32(h0) + f16_bits_to_f32(a.bias[ra]));
+                h1 = f32_to_f16_bits(f16_bits_to_f32(h1) + f16_bits_to_f32(a.bias[rb]));
+            }
+            const int half = a.D / 2;
+            int pos = a.pos;
+            const float *cos_row = a.cos_row, *sin_row = a.sin_row;
+            if (a.pos_dev) {
+                pos = *a.pos_dev;
+                cos_row += (size_t)pos * a.D;
+                sin_row += (size_t)pos * a.D;
+            }
+            if (ra < a.QD + a.KVD) {   // Q or K: rotate the pair (d, d + D/2)
+                const int d = (ra % a.D);
+                const float t0 = f16_bits_to_f32(h0), t1 = f16_bits_to_f32(h1);
+                h0 = f32_to_f16_bits(t0 * cos_row[d] - t1 * sin_row[d]);
+                h1 = f32_to_f16_bits(t1 * cos_row[d + half] + t0 * sin_row[d + half]);
+            }
+            if (ra < a.QD) {
+                a.q_out[ra] = (uint16_t)h0;
+                a.q_out[rb] = (uint16_t)h1;
+            } else {
+                const bool is_k = ra < a.QD + a.KVD;
+                const int rr = ra - (is_k ? a.QD : a.QD + a.KVD);
+                uint16_t* cache = (is_k ? a.Kc : a.Vc) + ((size_t)(rr / a.D) * a.max_seq + pos) * a.D + rr % a.D;
+                cache[0] = (uint16_t)h0;
+                cache[half] = (uint16_t)h1;
+            }
         }
     }
 }
@@ -429,11 +462,21 @@ void norm_cast_launch(bool layer, const float* X, const void* W, const void* B, 
         norm_cast<J, false><<<grid, 256, 0, s>>>(X, (const uint16_t*)W, (const uint16_t*)B, (uint16_t*)Y, M, H, eps);
 }
 
+// Row pairs per wave of each kind. The lm_head GEMV (32,000 rows at config 5) has parallelism to
+// spare and gains from paying its norm once per 8 rows (+1 % tokens/s); the Q/K/V and gate/up
+// GEMVs measured slower with two pairs per wave (fewer waves in flight).
+constexpr int kPairsQKV = 1, kPairsSilu = 1, kPairsLogits = 4;
+template <int kKind> constexpr int pairs_per_wave() {
+    return kKind == kQKV ? kPairsQKV : (kKind == kSiluMul ? kPairsSilu : kPairsLogits);
+}
+
 template <int kKind, int J>
-void gemv_launch(bool layer, const GemvArgs& a, hipStream_t s) {
+void gemv_launch(bool layer, GemvArgs a, hipStream_t s) {
+    constexpr int NP = pairs_per_wave<kKind>();
+    a.units = (a.pairs + NP - 1) / NP;
     const unsigned grid = ceil_div(a.units, 4);
-    if (layer) gemv2<kKind, J, true><<<grid, 256, 0, s>>>(a);
-    else gemv2<kKind, J, false><<<grid, 256, 0, s>>>(a);
+    if (layer) gemv2<kKind, J, true, NP><<<grid, 256, 0, s>>>(a);
+    else gemv2<kKind, J, false, NP><<<grid, 256, 0, s>>>(a);
 }
 
 template <int kKind>
@@ -491,7 +534,7 @@ int llm_gemv_qkv(bool layer, const float* hidden, const void* gain, const void* 
     GemvArgs a{};
     a.x = hidden; a.W = (const uint16_t*)W; a.bias = (const uint16_t*)bias; a.gain = (const uint16_t*)gain;
     a.beta = (const uint16_t*)beta; a.eps = eps; a.K = H;
-    a.D = D; a.QD = nH * D; a.KVD = nKV * D; a.rows = a.QD + 2 * a.KVD; a.units = a.rows / 2;
+    a.D = D; a.QD = nH * D; a.KVD = nKV * D; a.rows = a.QD + 2 * a.KVD; a.pairs = a.rows / 2;
     a.cos_row = cos_row; a.sin_row = sin_row; a.q_out = (uint16_t*)q_out; a.Kc = (uint16_t*)Kc;
     a.Vc = (uint16_t*)Vc; a.pos = pos; a.max_seq = max_seq; a.pos_dev = pos_dev;
     return gemv_dispatch<kQKV>(layer, a, s);
@@ -502,10 +545,11 @@ int llm_gemv_silu(bool layer, const float* hidden, const void* gain, const void*
     if (!gemv_shape_ok(H) || F < 1) return CDNA4_ERR_INVALID_VALUE;
     GemvArgs a{};
     a.x = hidden; a.W = (const uint16_t*)W; a.gain = (const uint16_t*)gain; a.beta = (const uint16_t*)beta;
-    a.eps = eps; a.out = act; a.K = H; a.rows = 2 * F; a.units = F;
+    a.eps = eps; a.out = act; a.K = H; a.rows = 2 * F; a.pairs = F;
     return gemv_dispatch<kSiluMul>(layer, a, s);
 }
 
+// Argmax partial keys of the logits GEMV for a vocabulary of V (one per wave; an upper bound).
 size_t llm_argmax_partials(int V) { return (size_t)(V + 1) / 2; }
 
 int llm_logits_argmax(bool layer, const float* hidden, const void* gain, const void* beta, float eps,
@@ -514,9 +558,10 @@ int llm_logits_argmax(bool layer, const float* hidden, const void* gain, const v
     if (!gemv_shape_ok(H) || V < 1) return CDNA4_ERR_INVALID_VALUE;
     GemvArgs a{};
     a.x = hidden; a.W = (const uint16_t*)W; a.gain = (const uint16_t*)gain; a.beta = (const uint16_t*)beta;
-    a.eps = eps; a.out = logits; a.K = H; a.rows = V; a.units = (V + 1) / 2; a.partial = partial;
+    a.eps = eps; a.out = logits; a.K = H; a.rows = V; a.pairs = (V + 1) / 2; a.partial = partial;
     if (int e = gemv_dispatch<kLogits>(layer, a, s)) return e;
-    argmax_keys<<<1, 1024, 0, s>>>(partial, a.units, scratch16, ids, tokens, step, state);
+    constexpr int NP = pairs_per_wave<kLogits>();
+    argmax_keys<<<1, 1024, 0, s>>>(partial, (a.pairs + NP - 1) / NP, scratch16, ids, tokens, step, state);
     return launch_status();
 }
 
