@@ -377,12 +377,15 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemv_residual_split(const ui
 
 // Final argmax over the per-wave keys of the logits GEMV: one workgroup of 1024 lanes, each
 // folding a strided share (loads issued 8 at a time), then the DPP butterfly per wave and wave 0
-// over the 16 wave results. Writes the token to ids[0] (the next step's embedding input) and to
-// tokens[step]. With a device step state {pos, step} (replayable steps), step is read from it
+// over the 16 wave results. Writes the token to ids[0] and tokens[step] and, when embed is
+// given, the token's embedding row to next_row (the next decode step's input). With a device step state {pos, step} (replayable steps), step is read from it
 // and both fields advance by one, ready for the next replay.
 __global__ __launch_bounds__(1024) void argmax_keys(const unsigned long long* __restrict__ keys, int n,
                                                     unsigned long long* __restrict__ scratch, int* __restrict__ ids,
-                                                    int* __restrict__ tokens, int step, int* __restrict__ state) {
+                                                    int* __restrict__ tokens, int step, int* __restrict__ state,
+                                                    const uint16_t* __restrict__ embed, float* __restrict__ next_row,
+                                                    int H, int V) {
+    __shared__ int tok_s;
     unsigned long long best = 0;
     for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 1024) {
         unsigned long long k[8];
@@ -406,6 +409,7 @@ __global__ __launch_bounds__(1024) void argmax_keys(const unsigned long long* __
         const uint32_t l2 = (uint32_t)allreduce((int)((hi == h2 ? lo : 0u) ^ 0x80000000u), Max{}) ^ 0x80000000u;
         if (threadIdx.x == 0) {
             const int tok = (int)(0xffffffffu - l2);
+            tok_s = tok;
             ids[0] = tok;
             if (state) step = state[1];
             if (tokens) tokens[step] = tok;
@@ -414,6 +418,25 @@ __global__ __launch_bounds__(1024) void argmax_keys(const unsigned long long* __
                 state[1] = step + 1;
             }
         }
+    }
+    // The next step's input: the chosen token's embedding row as fp32 (H % 8 == 0), so the step
+    // needs no separate gather launch.
+    if (!embed) return;
+    __syncthreads();
+    const int id = min(max(tok_s, 0), V - 1);
+    const uint16_t* src = embed + (size_t)id * H;
+    for (int c = threadIdx.x; c < H / 8; c += 1024) {
+        const u32x4 v = *(const u32x4*)(src + c * 8);
+        f32x4 lo, hi;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            lo[2 * i] = f16_bits_to_f32(v[i] & 0xffffu);
+            lo[2 * i + 1] = f16_bits_to_f32(v[i] >> 16);
+            hi[2 * i] = f16_bits_to_f32(v[i + 2] & 0xffffu);
+            hi[2 * i + 1] = f16_bits_to_f32(v[i + 2] >> 16);
+        }
+        *(f32x4*)(next_row + c * 8) = lo;
+        *(f32x4*)(next_row + c * 8 + 4) = hi;
     }
 }
 
@@ -554,14 +577,16 @@ size_t llm_argmax_partials(int V) { return (size_t)(V + 1) / 2; }
 
 int llm_logits_argmax(bool layer, const float* hidden, const void* gain, const void* beta, float eps,
                       const void* W, float* logits, int V, int H, unsigned long long* partial,
-                      unsigned long long* scratch16, int* ids, int* tokens, int step, hipStream_t s, int* state) {
+                      unsigned long long* scratch16, int* ids, int* tokens, int step, hipStream_t s, int* state,
+                      const void* embed, float* next_row) {
     if (!gemv_shape_ok(H) || V < 1) return CDNA4_ERR_INVALID_VALUE;
     GemvArgs a{};
     a.x = hidden; a.W = (const uint16_t*)W; a.gain = (const uint16_t*)gain; a.beta = (const uint16_t*)beta;
     a.eps = eps; a.out = logits; a.K = H; a.rows = V; a.pairs = (V + 1) / 2; a.partial = partial;
     if (int e = gemv_dispatch<kLogits>(layer, a, s)) return e;
     constexpr int NP = pairs_per_wave<kLogits>();
-    argmax_keys<<<1, 1024, 0, s>>>(partial, (a.pairs + NP - 1) / NP, scratch16, ids, tokens, step, state);
+    argmax_keys<<<1, 1024, 0, s>>>(partial, (a.pairs + NP - 1) / NP, scratch16, ids, tokens, step, state,
+                                   (const uint16_t*)embed, next_row, H, V);
     return launch_status();
 }
 

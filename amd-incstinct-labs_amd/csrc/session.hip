@@ -17,9 +17,9 @@
 //   * Decode (T = 1): every projection is an HBM-streaming GEMV with its epilogue fused (bias,
 //     residual add, SiLU product); attention is the split-K decode over the strided cache.
 //   * The RoPE table for every position is built once on the device. The next token id never
-//     leaves the device: argmax writes it where the next step's embedding gather reads it, so a
-//     generation of N tokens is one queue of launches and one copy back at the end (unless an
-//     EOS id must be checked after each step).
+//     leaves the device: argmax writes it, and the token's embedding row as the next step's
+//     input, so a generation of N tokens is one queue of launches and one copy back at the end
+//     (unless an EOS id must be checked after each step).
 //   * The decode step is captured once as a HIP graph and replayed: the position and the token
 //     index live in a device step state that the kernels read and the argmax advances, so one
 //     graph serves every step with the same attention plan (re-captured when the plan changes
@@ -51,7 +51,7 @@ size_t llm_argmax_partials(int V);
 int llm_logits_argmax(bool layer, const float* hidden, const void* gain, const void* beta, float eps,
                       const void* W, float* logits, int V, int H, unsigned long long* partial,
                       unsigned long long* scratch16, int* ids, int* tokens, int step, hipStream_t s,
-                      int* state = nullptr);
+                      int* state = nullptr, const void* embed = nullptr, float* next_row = nullptr);
 int llm_step_state(int* state, int pos, int step, hipStream_t s);
 long long attn_decode_plan_key(const cdna3_decode_cfg& c);
 int attn_decode_replayable(const void* q, const void* K, const void* V, void* o, const cdna3_decode_cfg& c, int dtype,
@@ -378,19 +378,20 @@ int Session::prefill(const int* host_ids, int T) {
     return last_token_logits(T, 0);
 }
 
-// Final norm of the last of T rows, lm_head and argmax: the token goes to ids[0] (the next step's
-// input) and tokens[step].
+// Final norm of the last of T rows, lm_head and argmax: the token goes to ids[0] and
+// tokens[step], and its embedding row to hidden row 0, the next decode step's input (the lm_head
+// has read row T - 1 by then: same stream).
 int Session::last_token_logits(int T, int step, int* state) {
     return llm_logits_argmax(c.layernorm != 0, hidden + (size_t)(T - 1) * c.hidden, fnorm, fnorm_b, c.norm_eps,
                              lm_head, logits, c.vocab_size, c.hidden, partial, scratch16, ids, tokens, step, stream,
-                             state);
+                             state, embed, hidden);
 }
 
-// One decode step at cache position pos, token `step`: embedding of ids[0], every layer, final
-// norm + lm_head + argmax. With dev, the kernels read the position and the token index from the
-// device step state (and the argmax advances it), so the launches are the same for every step.
+// One decode step at cache position pos, token `step`: every layer over hidden row 0 (the
+// previous argmax left the token's embedding there), final norm + lm_head + argmax. With dev, the
+// kernels read the position and the token index from the device step state (and the argmax
+// advances it), so the launches are the same for every step.
 int Session::decode_step(int pos, int step, bool dev) {
-    CK(llm_embed(embed, ids, hidden, 1, c.hidden, c.vocab_size, stream));
     CK(run_layers(1, pos, dev ? dstate : nullptr));
     return last_token_logits(1, step, dev ? dstate : nullptr);
 }
