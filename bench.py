@@ -10,6 +10,9 @@ Also reported in the same line:
   dpp:    BASELINE config 2 (device-wide reduce_{sum,max,min} and inclusive scan_sum over 2^26
           elements of f32, f64, i32, i64, f16, bf16, rotating >= 1 GiB of inputs so the 256 MB
           Infinity Cache cannot serve repeats) in GB/s of algorithmic bytes;
+  prefill_fp16, prefill_vs_torch_sdpa: config 3 with fp16 inputs, and PyTorch's flash-attention
+          SDPA timed on the same bf16 inputs (the comparison the reference made against the
+          production kernel);
   cfg1:   BASELINE config 1, the reference's FA2 configuration, fp32 and fp16 arms;
   copy_1GiB: a plain device copy, the achievable-bandwidth reference and the known-size kernel
           that calibrates the HBM traffic counters;
@@ -233,6 +236,29 @@ def bench_prefill(torch, cdna4, steps, warmup, dtype=None):
                        "head_dim": D, "causal": True, "dtype": "bf16" if dtype == torch.bfloat16 else "fp16"}}
 
 
+def bench_torch_sdpa(torch, ours_tflops):
+    """The same config-3 prefill through PyTorch's scaled_dot_product_attention, restricted to its
+    flash-attention backend (the production kernel the reference compared against,
+    compare_vs_production_fa.py); None if that backend is unavailable."""
+    try:
+        from torch.nn.attention import sdpa_kernel, SDPBackend
+    except ImportError:
+        return None
+    B, H, S, D = 4, 32, 8192, 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    Q, K, V = (torch.randn(B, H, S, D, device="cuda", dtype=torch.bfloat16, generator=g) for _ in range(3))
+    flop = 4.0 * B * H * D * S * (S + 1) / 2
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            ms, _ = time_launches(torch, lambda i=0: torch.nn.functional.scaled_dot_product_attention(
+                Q, K, V, is_causal=True), 10, 3)
+    except RuntimeError:
+        return None
+    tf = flop / (ms * 1e-3) / 1e12
+    return {"torch_sdpa_tflops": tf, "backend": "flash", "torch": torch.__version__,
+            "speedup": ours_tflops / tf}
+
+
 def bench_decode(torch, cdna4, steps, warmup):
     B, HQ, HK, D, N = 32, 32, 8, 128, 8192
     g = torch.Generator(device="cuda").manual_seed(1)
@@ -402,6 +428,7 @@ def main():
         p16 = bench_prefill(torch, cdna4, max(5, args.steps // 2), max(3, args.warmup // 2), torch.float16)
         result["prefill_fp16"] = {"value": p16["tflops"], "unit": "TFLOPS", "avg_ms": p16["avg_ms"],
                                   "frac": p16["tflops"] / PEAK_BF16_TFLOPS, "config": p16["config"]}
+        result["prefill_vs_torch_sdpa"] = bench_torch_sdpa(torch, result["value"])
     if "decode" in args.legs:
         result["decode"] = bench_decode(torch, cdna4, args.steps, args.warmup)
         if "value" not in result:
