@@ -6,7 +6,8 @@ cdna3_attn_prefill launch over the whole batch, inputs resident in HBM.
 
 Also reported in the same line:
   decode: BASELINE config 4 (batch 32, 32 q heads / 8 kv heads, D 128, N 8192 fp16) in GB/s of
-          algorithmic KV + q/o bytes, with its HBM roofline fraction;
+          algorithmic KV + q/o bytes, with its HBM roofline fraction and PyTorch's flash SDPA
+          timed on the same tensors;
   dpp:    BASELINE config 2 (device-wide reduce_{sum,max,min} and inclusive scan_sum over 2^26
           elements of f32, f64, i32, i64, f16, bf16, rotating >= 1 GiB of inputs so the 256 MB
           Infinity Cache cannot serve repeats) in GB/s of algorithmic bytes;
@@ -273,7 +274,19 @@ def bench_decode(torch, cdna4, steps, warmup):
         torch, lambda i=0: cdna4.decode(q, kv[i % 2][0], kv[i % 2][1], o, cfg, workspace=ws), steps, warmup)
     nbytes = 2.0 * B * HK * N * D * 2 + 2.0 * B * HQ * D * 2
     gbs = nbytes / (avg_ms * 1e-3) / 1e9
-    return {"value": gbs, "unit": "GB/s", "avg_us": avg_ms * 1e3,
+    # PyTorch's SDPA (flash backend, GQA broadcast) on the same q / K / V, for comparison
+    sdpa = None
+    try:
+        from torch.nn.attention import sdpa_kernel, SDPBackend
+        q4 = q.unsqueeze(2)
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            tms, _ = time_launches(torch, lambda i=0: torch.nn.functional.scaled_dot_product_attention(
+                q4, kv[i % 2][0], kv[i % 2][1], enable_gqa=True), 10, 3)
+        tgbs = nbytes / (tms * 1e-3) / 1e9
+        sdpa = {"torch_sdpa_gbs": tgbs, "backend": "flash", "torch": torch.__version__, "speedup": gbs / tgbs}
+    except (ImportError, RuntimeError, TypeError):
+        pass
+    return {"value": gbs, "unit": "GB/s", "avg_us": avg_ms * 1e3, "vs_torch_sdpa": sdpa,
             "config": {"workload": "flash decode, BASELINE config 4", "batch": B, "q_heads": HQ, "kv_heads": HK,
                        "head_dim": D, "kv_len": N, "dtype": "fp16"},
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
