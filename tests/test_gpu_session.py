@@ -135,6 +135,20 @@ def test_captured_step_equals_separate_launches(model, monkeypatch, n, new, max_
     assert np.array_equal(outs[0]["logits"], outs[1]["logits"])
 
 
+def test_graph_recaptured_when_scratch_grows(model):
+    # A longer second prompt on the same session reallocates the per-token scratch buffers; the
+    # captured decode step held the old addresses, so the session must drop it and capture again.
+    d, meta, t = model
+    short, long_ = _prompt(meta, 5, 41), _prompt(meta, 50, 42)
+    with cdna4.Session(d, max_seq=64) as s:
+        s.generate_ex(short, cdna4.GenerateCfg(4))
+        grown = s.generate_ex(long_, cdna4.GenerateCfg(6), with_logits=True)
+    with cdna4.Session(d, max_seq=64) as s:
+        fresh = s.generate_ex(long_, cdna4.GenerateCfg(6), with_logits=True)
+    assert grown["tokens"] == fresh["tokens"]
+    assert np.array_equal(grown["logits"], fresh["logits"])
+
+
 def test_eos_and_full_cache_stop_generation(model):
     d, meta, _ = model
     ids = _prompt(meta, 12, 3)
