@@ -385,7 +385,6 @@ __global__ __launch_bounds__(1024) void argmax_keys(const unsigned long long* __
                                                     int* __restrict__ tokens, int step, int* __restrict__ state,
                                                     const uint16_t* __restrict__ embed, float* __restrict__ next_row,
                                                     int H, int V) {
-    __shared__ int tok_s;
     unsigned long long best = 0;
     for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 1024) {
         unsigned long long k[8];
@@ -401,29 +400,29 @@ __global__ __launch_bounds__(1024) void argmax_keys(const unsigned long long* __
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) scratch[wave] = ((unsigned long long)mhi << 32) | mlo;
     __syncthreads();
-    if (threadIdx.x < 64) {
-        const unsigned long long k = threadIdx.x < 16 ? scratch[threadIdx.x] : 0ull;
+    // Every wave folds the 16 wave maxima itself, so the winner needs no broadcast.
+    {
+        const unsigned lane = threadIdx.x & 63;
+        const unsigned long long k = lane < 16 ? scratch[lane] : 0ull;
         hi = (uint32_t)(k >> 32);
         lo = (uint32_t)k;
-        const uint32_t h2 = (uint32_t)allreduce((int)(hi ^ 0x80000000u), Max{}) ^ 0x80000000u;
-        const uint32_t l2 = (uint32_t)allreduce((int)((hi == h2 ? lo : 0u) ^ 0x80000000u), Max{}) ^ 0x80000000u;
-        if (threadIdx.x == 0) {
-            const int tok = (int)(0xffffffffu - l2);
-            tok_s = tok;
-            ids[0] = tok;
-            if (state) step = state[1];
-            if (tokens) tokens[step] = tok;
-            if (state) {
-                state[0] += 1;
-                state[1] = step + 1;
-            }
+    }
+    const uint32_t h2 = (uint32_t)allreduce((int)(hi ^ 0x80000000u), Max{}) ^ 0x80000000u;
+    const uint32_t l2 = (uint32_t)allreduce((int)((hi == h2 ? lo : 0u) ^ 0x80000000u), Max{}) ^ 0x80000000u;
+    const int tok = (int)(0xffffffffu - l2);
+    if (threadIdx.x == 0) {
+        ids[0] = tok;
+        if (state) step = state[1];
+        if (tokens) tokens[step] = tok;
+        if (state) {
+            state[0] += 1;
+            state[1] = step + 1;
         }
     }
     // The next step's input: the chosen token's embedding row as fp32 (H % 8 == 0), so the step
     // needs no separate gather launch.
     if (!embed) return;
-    __syncthreads();
-    const int id = min(max(tok_s, 0), V - 1);
+    const int id = min(max(tok, 0), V - 1);
     const uint16_t* src = embed + (size_t)id * H;
     for (int c = threadIdx.x; c < H / 8; c += 1024) {
         const u32x4 v = *(const u32x4*)(src + c * 8);

@@ -183,9 +183,14 @@ int reduce_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) 
 
 // ---- scan (decoupled look-back, single-wave workgroups) ------------------------------
 // 16-byte loads per lane (tile = 64 U 16 B). The look-back costs about the same per tile whatever
-// its size, so tiles are as large as two waves per SIMD allow: 24 vectors (96 values per lane) for
-// 32/64-bit inputs, 16 vectors (128 fp32 values) for 16-bit ones (12 measured 2.4 TB/s, 16 2.76).
-template <int DT> struct ScanTile { static constexpr int U = (Elem<DT>::VEC == 8) ? 16 : 24; };
+// its size, so tiles are as large as the register file allows at two to three waves per SIMD:
+// 32 vectors (128 values per lane, ~150 VGPRs, three waves) for 32/64-bit inputs, 24 vectors (192
+// fp32 values, ~210 VGPRs, two waves) for 16-bit ones. Measured at 2^26: 24 / 36 / 40 vectors
+// for 32-bit inputs ran 3-8 % slower than 32, 16 / 20 vectors for 16-bit ones 3-7 % slower than 24.
+// Misaligned calls load element by element, which needs more registers per value: their tiles
+// are half as large (no accumulator-register spills).
+template <int DT> struct ScanTile { static constexpr int U = (Elem<DT>::VEC == 8) ? 24 : 32; };
+template <int DT, bool kVec> constexpr int scan_u() { return kVec ? ScanTile<DT>::U : ScanTile<DT>::U / 2; }
 
 // Per-tile look-back state. A tile publishes its aggregate into agg and, once known, its inclusive
 // prefix into pre. Every 64-bit word carries a tag in its upper half (1 = aggregate, 2 = prefix)
@@ -302,7 +307,7 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
     using Acc = typename E::Acc;
     using Out = typename E::Out;
     constexpr int VEC = E::VEC;
-    constexpr int U = ScanTile<DT>::U;
+    constexpr int U = scan_u<DT, kVec>();
     constexpr size_t TILE = (size_t)64 * VEC * U;
     const typename E::In* in = (const typename E::In*)in_;
     Out* out = (Out*)out_;
@@ -312,16 +317,41 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
     const size_t tile = blockIdx.x;
     const size_t base = tile * TILE;
 
+    // Aligned calls (kVec): n counts whole 16-byte vectors' elements only (the host scans the
+    // remaining n % VEC elements in scan_tail). Every tile but the last is full and takes a
+    // straight-line path of 16-byte loads at fixed offsets from one base, all issued before any
+    // arithmetic; the last tile guards each vector with a 32-bit tile-local index against the
+    // uniform vector count. Misaligned calls go element by element.
+    const typename E::In* tin = in + base;
+    const bool full = kVec && base + TILE <= n;
+    const uint32_t rem = base + TILE <= n ? (uint32_t)TILE : (uint32_t)(n - base);  // elements
     Acc v[U][VEC];
+    if constexpr (kVec) {
+        const u32x4* src = (const u32x4*)tin + lane;
+        if (full) {
 #pragma unroll
-    for (int j = 0; j < U; ++j) {
-        const size_t e0 = base + ((size_t)j * 64 + lane) * VEC;
-        if (kVec && e0 + VEC <= n) {
-            E::unpack(__builtin_nontemporal_load((const u32x4*)(in + e0)), v[j]);
+            for (int j = 0; j < U; ++j) E::unpack(__builtin_nontemporal_load(src + j * 64), v[j]);
+            __builtin_amdgcn_sched_barrier(0);
         } else {
+            const uint32_t nv = rem / VEC;
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) v[j][e] = (e0 + e < n) ? E::load1(in + e0 + e) : id;
+            for (int j = 0; j < U; ++j) {
+                if ((uint32_t)j * 64 + lane < nv) {
+                    E::unpack(__builtin_nontemporal_load(src + j * 64), v[j]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) v[j][e] = id;
+                }
+            }
         }
+    } else {
+#pragma unroll
+        for (int j = 0; j < U; ++j)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                const uint32_t i = ((uint32_t)j * 64 + lane) * VEC + e;
+                v[j][e] = i < rem ? E::load1(tin + i) : id;
+            }
     }
     // Tile-local inclusive scan in registers.
     Acc run = id;
@@ -337,6 +367,12 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
         for (int e = 0; e < VEC; ++e) v[j][e] = op(pre, v[j][e]);
         run = op(run, wave::xlane::lane63(inc));             // chunk total, on every lane
     }
+    // Materialise the scanned values here: left alone, the compiler sinks the last addition of
+    // every element past the look-back loop and keeps two extra values per chunk live across it.
+#pragma unroll
+    for (int j = 0; j < U; ++j)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) asm volatile("" : "+v"(v[j][e]));
     const Acc tile_total = run;
     Acc excl = id;
     if (tile == 0) {
@@ -346,42 +382,74 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
         excl = look_back<Acc>(st, tile, op);
         publish(st.pre, tile, op(excl, tile_total), kTagPre);
     }
+    Out* tout = out + base;
+    if constexpr (kVec) {
+        constexpr int kWords = (int)(sizeof(Out) * VEC / 16);
+        u32x4* dst = (u32x4*)tout + lane * kWords;
+        const uint32_t nv = rem / VEC;
 #pragma unroll
-    for (int j = 0; j < U; ++j) {
-        const size_t e0 = base + ((size_t)j * 64 + lane) * VEC;
-        Out o[VEC];
+        for (int j = 0; j < U; ++j) {
+            if (full || (uint32_t)j * 64 + lane < nv) {
+                Out o[VEC];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) o[e] = (Out)op(excl, v[j][e]);
-        if (kVec && e0 + VEC <= n) {
-            constexpr int kWords = (int)(sizeof(Out) * VEC / 16);
+                for (int e = 0; e < VEC; ++e) o[e] = (Out)op(excl, v[j][e]);
 #pragma unroll
-            for (int w = 0; w < kWords; ++w) {
-                u32x4 q;
-                __builtin_memcpy(&q, (const char*)o + 16 * w, 16);
-                __builtin_nontemporal_store(q, (u32x4*)(out + e0) + w);
+                for (int w = 0; w < kWords; ++w) {
+                    u32x4 q;
+                    __builtin_memcpy(&q, (const char*)o + 16 * w, 16);
+                    __builtin_nontemporal_store(q, dst + j * 64 * kWords + w);
+                }
             }
-        } else {
+        }
+    } else {
 #pragma unroll
-            for (int e = 0; e < VEC; ++e)
-                if (e0 + e < n) out[e0 + e] = o[e];
+        for (int j = 0; j < U; ++j)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                const uint32_t i = ((uint32_t)j * 64 + lane) * VEC + e;
+                if (i < rem) tout[i] = (Out)op(excl, v[j][e]);
+            }
+    }
+}
+
+// The last n % VEC (< VEC) elements of an aligned call, after scan_tiles has published every
+// tile's inclusive prefix: lane 0 continues the running value from the last tile's prefix.
+template <int DT, class Op>
+__global__ __launch_bounds__(64) void scan_tail(const void* __restrict__ in_, size_t from, size_t n,
+                                                 void* __restrict__ out_, ScanState st, size_t ntiles) {
+    using E = Elem<DT>;
+    using Acc = typename E::Acc;
+    using Out = typename E::Out;
+    const typename E::In* in = (const typename E::In*)in_;
+    Out* out = (Out*)out_;
+    Op op;
+    Acc acc = Op::template identity<Acc>();
+    bool ok = true;
+    if (ntiles > 0) ok = read_slot<Acc>(st.pre, (long long)ntiles - 1, kTagPre, acc);
+    if (threadIdx.x == 0) {
+        if (!ok) __hip_atomic_store(st.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (size_t i = from; i < n; ++i) {
+            acc = op(acc, E::load1(in + i));
+            out[i] = (Out)acc;
         }
     }
 }
 
-template <int DT>
+template <int DT, bool kVec>
 size_t scan_tiles_for(size_t n) {
-    const size_t tile = (size_t)64 * Elem<DT>::VEC * ScanTile<DT>::U;
+    const size_t tile = (size_t)64 * Elem<DT>::VEC * scan_u<DT, kVec>();
     return (n + tile - 1) / tile;
 }
 
+// Tile count the workspace is sized for: the misaligned (smaller) tiles', the larger count.
 size_t scan_ntiles(size_t n, int dtype) {
     switch (dtype) {
-        case CDNA4_F32: return scan_tiles_for<CDNA4_F32>(n);
-        case CDNA4_I32: return scan_tiles_for<CDNA4_I32>(n);
-        case CDNA4_F64: return scan_tiles_for<CDNA4_F64>(n);
-        case CDNA4_I64: return scan_tiles_for<CDNA4_I64>(n);
-        case CDNA4_F16: return scan_tiles_for<CDNA4_F16>(n);
-        case CDNA4_BF16: return scan_tiles_for<CDNA4_BF16>(n);
+        case CDNA4_F32: return scan_tiles_for<CDNA4_F32, false>(n);
+        case CDNA4_I32: return scan_tiles_for<CDNA4_I32, false>(n);
+        case CDNA4_F64: return scan_tiles_for<CDNA4_F64, false>(n);
+        case CDNA4_I64: return scan_tiles_for<CDNA4_I64, false>(n);
+        case CDNA4_F16: return scan_tiles_for<CDNA4_F16, false>(n);
+        case CDNA4_BF16: return scan_tiles_for<CDNA4_BF16, false>(n);
         default: return 0;
     }
 }
@@ -394,9 +462,14 @@ size_t scan_ws_bytes(size_t ntiles) { return 256 + 2 * align256(ntiles * 16); }
 template <int DT, class Op>
 int scan_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
     using Acc = typename Elem<DT>::Acc;
-    const size_t ntiles = scan_tiles_for<DT>(n);
-    if (ntiles == 0) return 0;
-    if (ntiles > 0x7fffffffull) return CDNA4_ERR_INVALID_VALUE;
+    constexpr size_t VEC = Elem<DT>::VEC;
+    if (n == 0) return 0;
+    if (scan_tiles_for<DT, false>(n) > 0x7fffffffull) return CDNA4_ERR_INVALID_VALUE;
+    // 16-byte aligned calls scan the whole vectors in scan_tiles and the last n % VEC elements
+    // in scan_tail; misaligned calls scan everything element by element in scan_tiles.
+    const bool vec = ((uintptr_t)in % 16) == 0 && ((uintptr_t)out % 16) == 0;
+    const size_t n_main = vec ? n - n % VEC : n;
+    const size_t ntiles = vec ? scan_tiles_for<DT, true>(n_main) : scan_tiles_for<DT, false>(n_main);
     char* w = (char*)ws;
     ScanState st;
     st.error = (uint32_t*)w;
@@ -404,12 +477,14 @@ int scan_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
     st.pre = (uint64_t*)(w + 256 + align256(ntiles * 16));
     // Both slot arrays are cleared in one pass (the pre array directly follows the agg array).
     const size_t nwords = (align256(ntiles * 16) + ntiles * Words<Acc>::NW * 8) / 8;
-    scan_clear<<<ceil_div(nwords, 256), 256, 0, s>>>(st.agg, nwords, st.error);
-    const bool vec = ((uintptr_t)in % 16) == 0 && ((uintptr_t)out % 16) == 0;
-    if (vec)
-        scan_tiles<DT, Op, true><<<(unsigned)ntiles, 64, 0, s>>>(in, n, out, st);
-    else
-        scan_tiles<DT, Op, false><<<(unsigned)ntiles, 64, 0, s>>>(in, n, out, st);
+    scan_clear<<<(unsigned)(nwords == 0 ? 1 : ceil_div(nwords, 256)), 256, 0, s>>>(st.agg, nwords, st.error);
+    if (ntiles > 0) {
+        if (vec)
+            scan_tiles<DT, Op, true><<<(unsigned)ntiles, 64, 0, s>>>(in, n_main, out, st);
+        else
+            scan_tiles<DT, Op, false><<<(unsigned)ntiles, 64, 0, s>>>(in, n_main, out, st);
+    }
+    if (n_main < n) scan_tail<DT, Op><<<1, 64, 0, s>>>(in, n_main, n, out, st, ntiles);
     return launch_status();
 }
 

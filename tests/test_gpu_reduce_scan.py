@@ -69,6 +69,28 @@ def test_scan_sizes(dtype, op):
             assert np.max(np.abs(got.astype(np.float64) - want)) <= tol
 
 
+@pytest.mark.parametrize("dtype", [oracle.I32, oracle.I64, oracle.F32, oracle.F64, oracle.F16, oracle.BF16])
+def test_scan_tile_boundaries(dtype):
+    # Inputs around multiples of every tile size the kernels use (64 lanes x 12-32 vectors of 2, 4
+    # or 8 elements): the last tile full, one vector short, one element over, and a remainder below
+    # one vector that the one-wave epilogue scans after the tiles. Odd sizes also run misaligned
+    # (one element in), which takes the element-wise kernel with half-size tiles.
+    sizes = sorted({m * k + d for m in (2048, 3072, 4096, 6144, 8192, 12288, 16384) for k in (1, 2)
+                    for d in (-8, -1, 0, 1, 3, 7)})
+    for i, n in enumerate(sizes):
+        h, t = make(dtype, n, 900 + i, offset=n % 2)
+        got = cdna4.scan_inclusive(t, "sum").cpu().numpy()
+        want = oracle.scan_inclusive(oracle.SUM, dtype, h)
+        if dtype in (oracle.I32, oracle.I64):
+            assert np.array_equal(got, want), n
+        else:
+            tol = 1e-13 * n if dtype == oracle.F64 else 2e-5 * max(1.0, np.sqrt(n))
+            assert np.max(np.abs(got.astype(np.float64) - want)) <= tol, n
+        if dtype in (oracle.I32, oracle.F32):
+            got = cdna4.scan_inclusive(t, "max").cpu().numpy()
+            assert np.array_equal(got, oracle.scan_inclusive(oracle.MAX, dtype, h)), n
+
+
 def test_scan_repeated_calls_reuse_workspace():
     # Flags in the workspace are cleared by each call: the same workspace serves many calls.
     n = 300007
