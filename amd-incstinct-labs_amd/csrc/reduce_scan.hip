@@ -182,14 +182,31 @@ int reduce_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) 
 }
 
 // ---- scan (decoupled look-back, single-wave workgroups) ------------------------------
-// 16-byte loads per lane (tile = 64 U 16 B). The look-back costs about the same per tile whatever
-// its size, so tiles are as large as the register file allows at two to three waves per SIMD:
-// 32 vectors (128 values per lane, ~150 VGPRs, three waves) for 32/64-bit inputs, 24 vectors (192
-// fp32 values, ~210 VGPRs, two waves) for 16-bit ones. Measured at 2^26: 24 / 36 / 40 vectors
-// for 32-bit inputs ran 3-8 % slower than 32, 16 / 20 vectors for 16-bit ones 3-7 % slower than 24.
-// Misaligned calls load element by element, which needs more registers per value: their tiles
-// are half as large (no accumulator-register spills).
-template <int DT> struct ScanTile { static constexpr int U = (Elem<DT>::VEC == 8) ? 24 : 32; };
+// Scan layout per element type: 16-bit inputs load 8 bytes (4 values) per lane and vector, so
+// each lane's fp32 output vector leaves as one 16-byte store and every store instruction writes
+// 1 KiB of contiguous lines (16-byte loads of 8 values left each lane's 32-byte output as two
+// stores 32 bytes apart, and the half-filled lines were written twice).
+using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+template <int DT> struct ScanElem : Elem<DT> { using Load = u32x4; };
+template <int DT> struct ScanElem16 : Elem<DT> {
+    using Load = u32x2;
+    static constexpr int VEC = 4;
+    __device__ static void unpack(const u32x2& v, float (&o)[4]) {
+        const uint32_t w[2] = {v[0], v[1]};
+        float x[8];
+        u32x4 q = {w[0], w[1], 0u, 0u};
+        Elem<DT>::unpack(q, x);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = x[i];
+    }
+};
+template <> struct ScanElem<CDNA4_F16> : ScanElem16<CDNA4_F16> {};
+template <> struct ScanElem<CDNA4_BF16> : ScanElem16<CDNA4_BF16> {};
+// Tile = 64 lanes x U vectors per lane. The look-back costs about the same per tile whatever its
+// size, so tiles are as large as the register file allows at three waves per SIMD: 32 vectors
+// (128 values per lane, ~150 VGPRs) for every input type. Measured at 2^26: 24 / 36 / 40 vectors
+// for 32-bit inputs ran 3-8 % slower than 32, and 40 for 16-bit ones (two waves) 4-6 % slower.
+template <int DT> struct ScanTile { static constexpr int U = 32; };
 template <int DT, bool kVec> constexpr int scan_u() { return kVec ? ScanTile<DT>::U : ScanTile<DT>::U / 2; }
 
 // Per-tile look-back state. A tile publishes its aggregate into agg and, once known, its inclusive
@@ -303,7 +320,7 @@ __device__ Acc look_back(const ScanState& st, size_t tile, Op op) {
 template <int DT, class Op, bool kVec>
 __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, size_t n,
                                                   void* __restrict__ out_, ScanState st) {
-    using E = Elem<DT>;
+    using E = ScanElem<DT>;
     using Acc = typename E::Acc;
     using Out = typename E::Out;
     constexpr int VEC = E::VEC;
@@ -317,17 +334,17 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
     const size_t tile = blockIdx.x;
     const size_t base = tile * TILE;
 
-    // Aligned calls (kVec): n counts whole 16-byte vectors' elements only (the host scans the
-    // remaining n % VEC elements in scan_tail). Every tile but the last is full and takes a
-    // straight-line path of 16-byte loads at fixed offsets from one base, all issued before any
-    // arithmetic; the last tile guards each vector with a 32-bit tile-local index against the
+    // Aligned calls (kVec): n counts the elements of whole VEC-element vectors only (the host
+    // scans the remaining n % VEC elements in scan_tail). Every tile but the last is full and
+    // takes a straight-line path of vector loads at fixed offsets from one base, all issued
+    // before any arithmetic; the last tile guards each vector with a 32-bit tile-local index against the
     // uniform vector count. Misaligned calls go element by element.
     const typename E::In* tin = in + base;
     const bool full = kVec && base + TILE <= n;
     const uint32_t rem = base + TILE <= n ? (uint32_t)TILE : (uint32_t)(n - base);  // elements
     Acc v[U][VEC];
     if constexpr (kVec) {
-        const u32x4* src = (const u32x4*)tin + lane;
+        const typename E::Load* src = (const typename E::Load*)tin + lane;
         if (full) {
 #pragma unroll
             for (int j = 0; j < U; ++j) E::unpack(__builtin_nontemporal_load(src + j * 64), v[j]);
@@ -437,7 +454,7 @@ __global__ __launch_bounds__(64) void scan_tail(const void* __restrict__ in_, si
 
 template <int DT, bool kVec>
 size_t scan_tiles_for(size_t n) {
-    const size_t tile = (size_t)64 * Elem<DT>::VEC * scan_u<DT, kVec>();
+    const size_t tile = (size_t)64 * ScanElem<DT>::VEC * scan_u<DT, kVec>();
     return (n + tile - 1) / tile;
 }
 
@@ -462,7 +479,7 @@ size_t scan_ws_bytes(size_t ntiles) { return 256 + 2 * align256(ntiles * 16); }
 template <int DT, class Op>
 int scan_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
     using Acc = typename Elem<DT>::Acc;
-    constexpr size_t VEC = Elem<DT>::VEC;
+    constexpr size_t VEC = ScanElem<DT>::VEC;
     if (n == 0) return 0;
     if (scan_tiles_for<DT, false>(n) > 0x7fffffffull) return CDNA4_ERR_INVALID_VALUE;
     // 16-byte aligned calls scan the whole vectors in scan_tiles and the last n % VEC elements
