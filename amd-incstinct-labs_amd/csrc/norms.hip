@@ -14,6 +14,7 @@ namespace cdna4 {
 namespace {
 
 using wave::xlane::allreduce;
+using wave::xlane::row_allreduce;
 using wave::xlane::Sum;
 
 constexpr int kNormWaves = 4;   // rows per 256-thread block, one wave per row
@@ -55,6 +56,29 @@ __global__ __launch_bounds__(256) void rmsnorm_vec(const float* __restrict__ X, 
             o.w = v[k].w * inv * f16_bits_to_f32(wb.y >> 16);
             *(float4*)(y + c) = o;
         }
+    }
+}
+
+// H <= 64 (H % 4 == 0): one 16-lane DPP row per norm row, four rows per wave, one float4 per lane,
+// so short rows keep all 64 lanes busy. Lanes of rows past M run on zeros (the row reductions need
+// every lane of the row) and store nothing.
+constexpr int kRows16 = 16;   // rows per 256-thread block
+__global__ __launch_bounds__(256) void rmsnorm_row16(const float* __restrict__ X, const uint16_t* __restrict__ W,
+                                                     float* __restrict__ Y, int M, int H, float eps) {
+    const int c = (int)(threadIdx.x & 15u) * 4;
+    const int row = blockIdx.x * kRows16 + (int)(threadIdx.x >> 4);
+    const bool in = row < M && c < H;
+    const float4 v = in ? *(const float4*)(X + (size_t)row * H + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float ss = row_allreduce((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w), Sum{});
+    const float inv = rsqrtf(ss / (float)H + eps);
+    if (in) {
+        const uint2 wb = *(const uint2*)(W + c);
+        float4 o;
+        o.x = v.x * inv * f16_bits_to_f32(wb.x & 0xffffu);
+        o.y = v.y * inv * f16_bits_to_f32(wb.x >> 16);
+        o.z = v.z * inv * f16_bits_to_f32(wb.y & 0xffffu);
+        o.w = v.w * inv * f16_bits_to_f32(wb.y >> 16);
+        *(float4*)(Y + (size_t)row * H + c) = o;
     }
 }
 
@@ -111,6 +135,32 @@ __global__ __launch_bounds__(256) void layernorm_vec(const float* __restrict__ X
             o.w = (v[k].w - mean) * inv * g.w + bb.w;
             *(float4*)(y + c) = o;
         }
+    }
+}
+
+__global__ __launch_bounds__(256) void layernorm_row16(const float* __restrict__ X, const float* __restrict__ G,
+                                                       const float* __restrict__ B, float* __restrict__ Y, int M,
+                                                       int H, float eps) {
+    const int c = (int)(threadIdx.x & 15u) * 4;
+    const int row = blockIdx.x * kRows16 + (int)(threadIdx.x >> 4);
+    const bool in = row < M && c < H;
+    const float4 v = in ? *(const float4*)(X + (size_t)row * H + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float mean = row_allreduce((v.x + v.y) + (v.z + v.w), Sum{}) / (float)H;
+    // Second pass over the register-cached deviations (padding lanes contribute 0).
+    float q = 0.f;
+    if (c < H) {
+        const float a = v.x - mean, b = v.y - mean, d = v.z - mean, e = v.w - mean;
+        q = (a * a + b * b) + (d * d + e * e);
+    }
+    const float inv = rsqrtf(row_allreduce(q, Sum{}) / (float)H + eps);
+    if (in) {
+        const float4 g = *(const float4*)(G + c), bb = *(const float4*)(B + c);
+        float4 o;
+        o.x = (v.x - mean) * inv * g.x + bb.x;
+        o.y = (v.y - mean) * inv * g.y + bb.y;
+        o.z = (v.z - mean) * inv * g.z + bb.z;
+        o.w = (v.w - mean) * inv * g.w + bb.w;
+        *(float4*)(Y + (size_t)row * H + c) = o;
     }
 }
 
@@ -197,6 +247,10 @@ extern "C" int cdna3_rmsnorm_f32(const float* X, const void* W, float* Y, int M,
         rmsnorm_any<<<grid, 256, 0, s>>>(X, w, Y, M, H, eps);
         return launch_status();
     }
+    if (H <= 64) {
+        rmsnorm_row16<<<ceil_div((size_t)M, kRows16), 256, 0, s>>>(X, w, Y, M, H, eps);
+        return launch_status();
+    }
     return dispatch_nv(H, [&](auto nv) {
         rmsnorm_vec<decltype(nv)::value><<<grid, 256, 0, s>>>(X, w, Y, M, H, eps);
         return launch_status();
@@ -213,6 +267,10 @@ extern "C" int cdna3_layernorm_f32(const float* X, const float* gamma, const flo
     const bool vec = (H % 4 == 0) && H <= 4096 && aligned16(X) && aligned16(Y) && aligned16(gamma) && aligned16(beta);
     if (!vec) {
         layernorm_any<<<grid, 256, 0, s>>>(X, gamma, beta, Y, M, H, eps);
+        return launch_status();
+    }
+    if (H <= 64) {
+        layernorm_row16<<<ceil_div((size_t)M, kRows16), 256, 0, s>>>(X, gamma, beta, Y, M, H, eps);
         return launch_status();
     }
     return dispatch_nv(H, [&](auto nv) {

@@ -17,6 +17,9 @@ Also reported in the same line:
   cfg1:   BASELINE config 1, the reference's FA2 configuration, fp32 and fp16 arms;
   copy_1GiB: a plain device copy, the achievable-bandwidth reference and the known-size kernel
           that calibrates the HBM traffic counters;
+  norms:  the runtime's two-pass LayerNorm and RMSNorm at the reference's LayerNorm benchmark
+          shapes (65536 rows x 64 and x 512 f32 columns), with the reference's published
+          LayerNorm latencies (MI300X) beside them;
   llm:    BASELINE config 5, the small-LLM runtime (12 layers, d 768, 12 heads of 64, MLP 3072,
           vocab 32000, random-init fp16 weights N(0, 0.02), LayerNorm gains 1 and betas 0): greedy
           decode of 128 tokens after a 512-token prompt of seeded random ids, in tokens/s over the
@@ -52,9 +55,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", default="all",
-                   help="all, or a comma-separated subset of prefill,decode,dpp,cfg1,copy,llm")
+                   help="all, or a comma-separated subset of prefill,decode,dpp,cfg1,copy,norms,llm")
     args = p.parse_args()
-    legs = {"prefill", "decode", "dpp", "cfg1", "copy", "llm"}
+    legs = {"prefill", "decode", "dpp", "cfg1", "copy", "norms", "llm"}
     args.legs = legs if args.only == "all" else set(args.only.split(","))
     if not args.legs <= legs:
         p.error(f"--only: unknown legs {sorted(args.legs - legs)}")
@@ -363,6 +366,37 @@ def bench_copy(torch, steps, warmup):
             "bytes_read": 4 * n, "bytes_written": 4 * n}
 
 
+def bench_norms(torch, cdna4, steps, warmup):
+    """The runtime norms at the reference's LayerNorm benchmark shapes (65536 rows x 64 and x 512
+    f32 columns; research/wave-primitives/benchmarks/bench_layernorm.hip, published in
+    docs/paper-draft.md:447,450 as 35.7 and 65.3 us on MI300X): two-pass LayerNorm (eps 1e-5, f32
+    gamma/beta) and RMSNorm (eps 1e-6, fp16 weights). Inputs and outputs rotate over >= 1 GiB so
+    the Infinity Cache cannot serve repeats. Algorithmic bytes 2*M*H*4 (read X, write Y)."""
+    M = 65536
+    ref_us = {64: 35.7, 512: 65.3}
+    g = torch.Generator(device="cuda").manual_seed(9)
+    out = {"config": {"workload": "reference LayerNorm benchmark shapes", "rows": M, "dtype": "f32"}}
+    for H in (64, 512):
+        nb = max(2, (1 << 30) // (2 * M * H * 4))
+        xs = [torch.randn(M, H, device="cuda", generator=g) for _ in range(nb)]
+        ys = [torch.empty(M, H, device="cuda") for _ in range(nb)]
+        gamma = torch.rand(H, device="cuda", generator=g) + 0.5
+        beta = torch.randn(H, device="cuda", generator=g)
+        w16 = (torch.rand(H, device="cuda", generator=g) + 0.5).half()
+        nbytes = 2 * M * H * 4
+        entry = {}
+        for name, fn in (("layernorm", lambda i=0: cdna4.layernorm_f32(xs[i % nb], gamma, beta, out=ys[i % nb])),
+                         ("rmsnorm", lambda i=0: cdna4.rmsnorm_f32(xs[i % nb], w16, out=ys[i % nb]))):
+            ms, _ = time_launches(torch, fn, steps, warmup)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            entry[name] = {"us": round(ms * 1e3, 2), "GBs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        entry["layernorm"]["reference_us_mi300x"] = ref_us[H]
+        out[f"{M}x{H}"] = entry
+        del xs, ys
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_llm(steps):
     """BASELINE config 5 through cdna4.Session (the C ABI session): `steps` generations of 128
     tokens after the same 512-token prompt, after one untimed warm-up generation. Decode tokens/s
@@ -454,6 +488,8 @@ def main():
         result["cfg1"] = bench_cfg1(torch, cdna4, args.steps, args.warmup)
     if "copy" in args.legs:
         result["copy_1GiB"] = bench_copy(torch, args.steps, args.warmup)
+    if "norms" in args.legs:
+        result["norms"] = bench_norms(torch, cdna4, args.steps, args.warmup)
     if "llm" in args.legs:
         if args.no_cpu_baseline:
             os.environ["CDNA4_NO_CPU_BASELINE"] = "1"
