@@ -7,7 +7,8 @@ cdna3_attn_prefill launch over the whole batch, inputs resident in HBM.
 Also reported in the same line:
   decode: BASELINE config 4 (batch 32, 32 q heads / 8 kv heads, D 128, N 8192 fp16) in GB/s of
           algorithmic KV + q/o bytes, with its HBM roofline fraction and PyTorch's flash SDPA
-          timed on the same tensors;
+          timed on the same tensors, and the reference's own batch-1 decode shape beside its
+          published MI300X latency;
   dpp:    BASELINE config 2 (device-wide reduce_{sum,max,min} and inclusive scan_sum over 2^26
           elements of f32, f64, i32, i64, f16, bf16, rotating >= 1 GiB of inputs so the 256 MB
           Infinity Cache cannot serve repeats) in GB/s of algorithmic bytes;
@@ -289,7 +290,25 @@ def bench_decode(torch, cdna4, steps, warmup):
         sdpa = {"torch_sdpa_gbs": tgbs, "backend": "flash", "torch": torch.__version__, "speedup": gbs / tgbs}
     except (ImportError, RuntimeError, TypeError):
         pass
-    return {"value": gbs, "unit": "GB/s", "avg_us": avg_ms * 1e3, "vs_torch_sdpa": sdpa,
+    del kv
+    torch.cuda.empty_cache()
+    # The reference's own decode benchmark shape (batch 1, 32q/8kv, D 128, N 8192: 803.4 us on
+    # MI300X, research/flash-attention-mi300x/results/2026-06-15_fa_decode_mi300x.txt:17); 33.5 MB
+    # of K/V per call, so 32 sets rotate through 1 GiB.
+    cfg1b = cdna4.DecodeCfg(D, N, HQ, HK, 1, 0)
+    q1 = q[:1].contiguous()
+    kv1 = [(torch.randn(1, HK, N, D, device="cuda", dtype=torch.float16, generator=g),
+            torch.randn(1, HK, N, D, device="cuda", dtype=torch.float16, generator=g)) for _ in range(32)]
+    o1 = torch.empty_like(q1)
+    ws1 = torch.empty(cdna4.decode_workspace_size(cfg1b), dtype=torch.uint8, device="cuda")
+    ms1, _ = time_launches(
+        torch, lambda i=0: cdna4.decode(q1, kv1[i % 32][0], kv1[i % 32][1], o1, cfg1b, workspace=ws1), steps, warmup)
+    nb1 = 2.0 * HK * N * D * 2 + 2.0 * HQ * D * 2
+    batch1 = {"us": ms1 * 1e3, "GBs": nb1 / (ms1 * 1e-3) / 1e9, "reference_us_mi300x": 803.4,
+              "config": {"batch": 1, "q_heads": HQ, "kv_heads": HK, "head_dim": D, "kv_len": N, "dtype": "fp16"}}
+    del kv1
+    torch.cuda.empty_cache()
+    return {"value": gbs, "unit": "GB/s", "avg_us": avg_ms * 1e3, "vs_torch_sdpa": sdpa, "batch1": batch1,
             "config": {"workload": "flash decode, BASELINE config 4", "batch": B, "q_heads": HQ, "kv_heads": HK,
                        "head_dim": D, "kv_len": N, "dtype": "fp16"},
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
