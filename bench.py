@@ -371,6 +371,9 @@ def bench_cfg1(torch, cdna4, steps, warmup):
         tf = flop / (ms * 1e-3) / 1e12
         out[name] = {"us": round(ms * 1e3, 2), "TFLOPS": round(tf, 2), "frac": round(tf / peak, 4),
                      "peak": peak, "peak_unit": "TFLOP/s"}
+    # The reference's best FA2 step at this shape (fp16 in, fp32 accumulation; `fa_dme`, MI300X):
+    # research/flash-attention-mi300x/results/2026-06-05_fa_steps_mi300x.txt:10-15.
+    out["fp16"]["reference_us_mi300x"] = 82.4
     return out
 
 
