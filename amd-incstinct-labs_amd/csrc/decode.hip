@@ -227,11 +227,28 @@ __global__ __launch_bounds__(64) void decode_merge(const float* __restrict__ par
     float acc[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-#pragma unroll 8   // eight partials' loads in flight at once (the loop was a chain of dependent latencies)
-    for (int i = 0; i < P; ++i) {
-        const float w = exp2f(ml[2 * i] - Mref);
+    // Up to 64 partials per pass: lane j computes partial j's weight once (0 for lanes past the
+    // count) and the loop takes it back with v_readlane (no LDS). Sixteen partials' rows are loaded
+    // before any is used; indices past the count re-read the last row, weighted 0.
+    for (int i0 = 0; i0 < P; i0 += 64) {
+        const int n = min(64, P - i0);
+        const float wl = ((int)lane < n) ? exp2f(ml[2 * (i0 + (int)lane)] - Mref) : 0.f;
+        const float* pi = po + (size_t)i0 * D + lane * EPL;
+        for (int j0 = 0; j0 < n; j0 += 16) {   // j0 <= 48, so j0 + jj <= 63 below
+            float v[16][EPL];
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[e] = fmaf(w, po[(size_t)i * D + lane * EPL + e], acc[e]);
+            for (int jj = 0; jj < 16; ++jj) {
+                const int j = min(j0 + jj, n - 1);
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) v[jj][e] = pi[(size_t)j * D + e];
+            }
+#pragma unroll
+            for (int jj = 0; jj < 16; ++jj) {
+                const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), j0 + jj));
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[e] = fmaf(w, v[jj][e], acc[e]);
+            }
+        }
     }
     const float inv = (L > 0.f) ? 1.f / L : 1.f;
     uint16_t* o = (uint16_t*)out + bh * D + lane * EPL;
