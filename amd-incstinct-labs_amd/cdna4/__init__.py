@@ -36,6 +36,7 @@ __all__ = [
     "scan_inclusive", "scan_workspace_size", "rmsnorm_f32", "layernorm_f32", "rope_f16",
     "rope_table_f32", "flash_attn", "flash_attn_decode", "CDNA4Error", "PrefillStrides", "prefill_strided",
     "scatter_kv_f16", "repack_f16", "rope_append_kv_f16", "ModelCfg", "GenerateCfg", "Session",
+    "PlanInfo", "prefill_plan", "decode_plan", "scan_status", "KERNEL_NAMES",
 ]
 
 # Element types and operators (include/cdna4_attn.h).
@@ -91,6 +92,22 @@ class ModelCfg(ctypes.Structure):
         return {n: getattr(self, n) for n, _ in self._fields_}
 
 
+class PlanInfo(ctypes.Structure):
+    """cdna3_plan_info: the kernel a call would launch (CDNA4_KERNEL_*), its waves per workgroup,
+    rows (prefill: queries per work item; decode: keys per split), split-K partials, grid and
+    workspace bytes."""
+    _fields_ = [("kernel", ctypes.c_int), ("waves", ctypes.c_int), ("rows", ctypes.c_int),
+                ("partials", ctypes.c_int), ("grid", ctypes.c_longlong), ("workspace", ctypes.c_size_t)]
+
+    @property
+    def name(self) -> str:
+        return KERNEL_NAMES.get(self.kernel, "?")
+
+
+# CDNA4_KERNEL_* (include/cdna4_attn.h)
+KERNEL_NAMES = {1: "fa_mfma_8w", 2: "fa_mfma_4w", 3: "fa_small", 4: "fa_f32", 5: "decode_split", 6: "decode_wg"}
+
+
 def DecodeDmeCfg(D: int, N: int, nQHeads: int, nKVHeads: int, stride_kv: int, batch: int = 1) -> DecodeCfg:
     """The reference's DecodeDmeCfg {D, N, nQHeads, nKVHeads, stride_kv}
     (detail/fa_decode_dme_kernel.hpp:45-48) as a DecodeCfg."""
@@ -115,6 +132,9 @@ def _declare(l: ctypes.CDLL) -> None:
                                                ctypes.POINTER(PrefillStrides), c_int, vp]),
         "cdna3_attn_decode_workspace_size": (c_size, [ctypes.POINTER(DecodeCfg)]),
         "cdna3_attn_decode": (c_int, [vp, vp, vp, vp, ctypes.POINTER(DecodeCfg), c_int, vp, c_size, vp]),
+        "cdna3_attn_prefill_plan": (c_int, [ctypes.POINTER(PrefillCfg), c_int, ctypes.POINTER(PlanInfo)]),
+        "cdna3_attn_decode_plan": (c_int, [ctypes.POINTER(DecodeCfg), c_int, c_int, ctypes.POINTER(PlanInfo)]),
+        "cdna3_scan_status": (c_int, [vp, ctypes.POINTER(c_int), vp]),
         "cdna3_reduce_workspace_size": (c_size, [c_size, c_int]),
         "cdna3_reduce": (c_int, [c_int, c_int, vp, c_size, vp, vp, c_size, vp]),
         "cdna3_scan_workspace_size": (c_size, [c_size, c_int]),
@@ -234,10 +254,12 @@ def decode_workspace_size(cfg: DecodeCfg) -> int:
 
 
 def decode(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, o: torch.Tensor, cfg: DecodeCfg,
-           workspace: Optional[torch.Tensor] = None, stream=None) -> None:
+           workspace="auto", stream=None) -> None:
     """cdna3::attn::decode with batch: q, o [batch][nQH][D]; K, V [batch][nKVH][stride][D];
-    fp16 or bf16. `workspace` (uint8, >= decode_workspace_size(cfg) bytes) holds split-K
-    partials; without one the library uses its own per-device buffer."""
+    fp16 or bf16. `workspace`: "auto" (default) allocates the split-K workspace from torch's
+    caching allocator on the current stream; a uint8 tensor of >= decode_workspace_size(cfg)
+    bytes is used as given; None runs the one-launch plan that needs no workspace (the
+    reference launchers' contract)."""
     _dev(q, K, V, o)
     dt = _dtype(q)
     if not (K.dtype == V.dtype == o.dtype == q.dtype):
@@ -247,6 +269,11 @@ def decode(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, o: torch.Tensor, c
         raise ValueError("q/o smaller than the configuration")
     if min(K.numel(), V.numel()) < cfg.batch * cfg.nKVHeads * stride * cfg.D:
         raise ValueError("K/V smaller than the configuration")
+    if isinstance(workspace, str):
+        if workspace != "auto":
+            raise ValueError("workspace must be 'auto', None or a uint8 tensor")
+        need = decode_workspace_size(cfg)
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device) if need > 0 else None
     ws_bytes = 0
     if workspace is not None:
         _dev(workspace)
@@ -255,7 +282,26 @@ def decode(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, o: torch.Tensor, c
                                    ws_bytes, _stream(stream)), "cdna3_attn_decode")
 
 
-def decode_dme(q, K, V, o, cfg: DecodeCfg, workspace=None, stream=None) -> None:
+def prefill_plan(cfg: PrefillCfg, dtype=BF16) -> PlanInfo:
+    """The kernel cdna3_attn_prefill would launch for cfg on the current device."""
+    if isinstance(dtype, torch.dtype):
+        dtype = _TORCH_DTYPES[dtype]
+    out = PlanInfo()
+    _check(lib().cdna3_attn_prefill_plan(ctypes.byref(cfg), dtype, ctypes.byref(out)), "cdna3_attn_prefill_plan")
+    return out
+
+
+def decode_plan(cfg: DecodeCfg, dtype=F16, with_workspace: bool = True) -> PlanInfo:
+    """The kernels cdna3_attn_decode would launch for cfg, with or without a workspace."""
+    if isinstance(dtype, torch.dtype):
+        dtype = _TORCH_DTYPES[dtype]
+    out = PlanInfo()
+    _check(lib().cdna3_attn_decode_plan(ctypes.byref(cfg), dtype, 1 if with_workspace else 0, ctypes.byref(out)),
+           "cdna3_attn_decode_plan")
+    return out
+
+
+def decode_dme(q, K, V, o, cfg: DecodeCfg, workspace="auto", stream=None) -> None:
     """cdna3::attn::decode_dme: decode reading a strided [nKVH][stride_kv][D] cache in place."""
     decode(q, K, V, o, cfg, workspace, stream)
 
@@ -290,8 +336,11 @@ def reduce(x: torch.Tensor, op="sum", out: Optional[torch.Tensor] = None,
 
 
 def scan_inclusive(x: torch.Tensor, op="sum", out: Optional[torch.Tensor] = None,
-                   workspace: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
-    """Inclusive scan of a whole contiguous array; fp16/bf16 accumulate (and return) fp32."""
+                   workspace: Optional[torch.Tensor] = None, stream=None, check: bool = True) -> torch.Tensor:
+    """Inclusive scan of a whole contiguous array; fp16/bf16 accumulate (and return) fp32.
+    With check (the default) the call synchronises the stream and raises CDNA4Error if the scan's
+    look-back reported a wait past its bound (cdna3_scan_status), so a wrong result can never be
+    returned silently; check=False leaves the call asynchronous (test with scan_status later)."""
     _dev(x)
     dt, o = _dtype(x), _OPS[op]
     n = x.numel()
@@ -301,7 +350,18 @@ def scan_inclusive(x: torch.Tensor, op="sum", out: Optional[torch.Tensor] = None
         workspace = torch.empty(max(1, scan_workspace_size(n, dt)), dtype=torch.uint8, device=x.device)
     _check(lib().cdna3_scan_inclusive(o, dt, _ptr(x), n, _ptr(out), _ptr(workspace), workspace.numel(),
                                       _stream(stream)), "cdna3_scan_inclusive")
+    if check and n > 0:
+        st = scan_status(workspace, stream)
+        if st != 0:
+            raise CDNA4Error("cdna3_scan_inclusive: look-back wait exceeded its bound; result invalid", 1)
     return out
+
+
+def scan_status(workspace: torch.Tensor, stream=None) -> int:
+    """cdna3_scan_status: 0 when the last scan on this workspace is valid (synchronises)."""
+    st = ctypes.c_int(-1)
+    _check(lib().cdna3_scan_status(_ptr(workspace), ctypes.byref(st), _stream(stream)), "cdna3_scan_status")
+    return st.value
 
 
 # ---- runtime norms and RoPE --------------------------------------------------------------

@@ -70,7 +70,8 @@ def _flash_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
     if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
         raise RuntimeError("q and the caches must share one dtype")
     o = torch.empty((nqh, D), dtype=q.dtype, device=q.device)
-    decode(q, k_cache, v_cache, o, DecodeCfg(D, N, nqh, nkvh, 1, 0))
+    # The split-K workspace comes from torch's caching allocator on the current stream.
+    decode(q, k_cache, v_cache, o, DecodeCfg(D, N, nqh, nkvh, 1, 0), workspace="auto")
     return o
 
 

@@ -18,7 +18,6 @@
 //     denominator formed by the wave butterfly.
 #include "attn_tile.hpp"
 #include "attn_stream.hpp"
-#include <mutex>
 #include <math.h>
 
 namespace cdna4 {
@@ -262,7 +261,8 @@ __global__ __launch_bounds__(64) void decode_merge(const float* __restrict__ par
 struct Plan { int G, HB, KPW, P; size_t ws_bytes; bool wg; };
 
 // Waves per workgroup of the short-cache variant (its LDS holds W rings of two K and V stages)
-// and the longest cache it takes: at most kWgChunks 32-key chunks per wave.
+// and the longest cache it takes when a split-K workspace is available: at most kWgChunks 32-key
+// chunks per wave.
 template <int D> constexpr int wg_waves() { return D == 64 ? 8 : 4; }
 constexpr int kWgChunks = 8;
 
@@ -270,7 +270,11 @@ constexpr int kWgChunks = 8;
 // split, a multiple of the 32-key chunk, sized so that the whole grid is one round of resident
 // workgroups (kDecPerCU per CU): every workgroup streams from start to end with no second round
 // and no tail of stragglers, which measured markedly faster than many short splits.
-bool plan_decode(const cdna3_decode_cfg& c, Plan& p) {
+// split_k == false (a call without a workspace) always takes the one-launch variant, which needs
+// no memory beyond q, K, V and o: such a call never allocates and shares no buffer with any other
+// call, so it is re-entrant across streams and capturable. Long caches then stream through one
+// workgroup per (batch, kv head, head group) instead of a split-K grid.
+bool plan_decode(const cdna3_decode_cfg& c, bool split_k, Plan& p) {
     if (c.D != 64 && c.D != 128) return false;
     if (c.N < 1 || c.nQHeads < 1 || c.nKVHeads < 1 || c.batch < 1) return false;
     if (c.nQHeads % c.nKVHeads) return false;
@@ -279,7 +283,7 @@ bool plan_decode(const cdna3_decode_cfg& c, Plan& p) {
     p.G = c.nQHeads / c.nKVHeads;
     p.HB = (p.G + 15) / 16;
     const int W = c.D == 64 ? wg_waves<64>() : wg_waves<128>();
-    p.wg = c.N <= W * kWgChunks * kDecT;
+    p.wg = !split_k || c.N <= W * kWgChunks * kDecT;
     if (p.wg) {   // one workgroup per (batch, kv head, head group); W contiguous key ranges
         p.KPW = wg_keys_per_wave(c.N, W);
         p.P = 1;
@@ -307,7 +311,7 @@ int launch_decode(const cdna3_decode_cfg& c, const Plan& p, const void* q, const
     a.q = q; a.K = K; a.V = V;
     const size_t nml = (size_t)c.batch * c.nQHeads * p.P * 2;
     a.part_ml = (float*)ws;
-    a.part_o = (float*)((char*)ws + ((nml * sizeof(float) + 255) & ~(size_t)255));
+    a.part_o = ws ? (float*)((char*)ws + ((nml * sizeof(float) + 255) & ~(size_t)255)) : nullptr;
     a.N = c.N; a.nQH = c.nQHeads; a.nKVH = c.nKVHeads; a.stride = c.stride_kv == 0 ? c.N : c.stride_kv;
     a.G = p.G; a.HB = p.HB; a.KPW = p.KPW; a.P = p.P;
     a.sc = kLog2e / sqrtf((float)D);
@@ -318,35 +322,27 @@ int launch_decode(const cdna3_decode_cfg& c, const Plan& p, const void* q, const
         decode_wg<D, kBf16, wg_waves<D>()><<<grid, 64 * wg_waves<D>(), 0, s>>>(a, o);
         return launch_status();
     }
+    if (!ws) return CDNA4_ERR_INVALID_VALUE;
     decode_mfma<D, kBf16, kDecStages><<<grid, 64, 0, s>>>(a);
     decode_merge<D, kBf16><<<(unsigned)((size_t)c.batch * c.nQHeads), 64, 0, s>>>(a.part_ml, a.part_o, o, p.P);
     return launch_status();
 }
 
-// Per-device fallback workspace for callers that pass none (the reference launchers take
-// no workspace argument). Grown on demand, kept until process exit.
-struct FallbackWs { std::mutex mu; void* ptr[64] = {}; size_t bytes[64] = {}; };
-FallbackWs g_ws;
-
-int fallback_workspace(size_t need, void** out) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return (int)e;
-    if (dev < 0 || dev >= 64) return CDNA4_ERR_INVALID_VALUE;
-    std::lock_guard<std::mutex> lk(g_ws.mu);
-    if (g_ws.bytes[dev] < need) {
-        // The old buffer may still be read by queued work on another stream: leak it
-        // rather than free it under that work. Growth is geometric, so this is bounded.
-        size_t sz = g_ws.bytes[dev] ? g_ws.bytes[dev] * 2 : (size_t)1 << 20;
-        while (sz < need) sz *= 2;
-        void* p = nullptr;
-        e = hipMalloc(&p, sz);
-        if (e != hipSuccess) return (int)e;
-        g_ws.ptr[dev] = p;
-        g_ws.bytes[dev] = sz;
-    }
-    *out = g_ws.ptr[dev];
+int check_decode_args(const void* q, const void* K, const void* V, void* o, int dtype) {
+    if (dtype != CDNA4_F16 && dtype != CDNA4_BF16) return CDNA4_ERR_INVALID_VALUE;
+    if (!q || !K || !V || !o) return CDNA4_ERR_INVALID_VALUE;
+    // 16-byte loads of q/K/V rows.
+    if ((((uintptr_t)q | (uintptr_t)K | (uintptr_t)V) & 15u) != 0) return CDNA4_ERR_INVALID_VALUE;
+    if (((uintptr_t)o & 3u) != 0) return CDNA4_ERR_INVALID_VALUE;
     return 0;
+}
+
+int run_decode(const cdna3_decode_cfg& c, const Plan& p, const void* q, const void* K, const void* V, void* o,
+               int dtype, void* ws, hipStream_t s) {
+    const bool bf = dtype == CDNA4_BF16;
+    if (c.D == 128) return bf ? launch_decode<128, true>(c, p, q, K, V, o, ws, s)
+                              : launch_decode<128, false>(c, p, q, K, V, o, ws, s);
+    return bf ? launch_decode<64, true>(c, p, q, K, V, o, ws, s) : launch_decode<64, false>(c, p, q, K, V, o, ws, s);
 }
 
 }  // namespace
@@ -355,7 +351,7 @@ int fallback_workspace(size_t need, void** out) {
 // with the same arguments apart from the length itself. -1 for an invalid configuration.
 long long attn_decode_plan_key(const cdna3_decode_cfg& c) {
     Plan p;
-    if (!plan_decode(c, p)) return -1;
+    if (!plan_decode(c, true, p)) return -1;
     return p.wg ? 1 : ((long long)p.P << 32) | (long long)p.KPW;
 }
 
@@ -365,7 +361,7 @@ long long attn_decode_plan_key(const cdna3_decode_cfg& c) {
 int attn_decode_replayable(const void* q, const void* K, const void* V, void* o, const cdna3_decode_cfg& c, int dtype,
                            void* ws, size_t ws_bytes, const int* len_pos, hipStream_t s) {
     Plan p;
-    if (!plan_decode(c, p) || !len_pos || ws_bytes < p.ws_bytes + 256) return CDNA4_ERR_INVALID_VALUE;
+    if (!plan_decode(c, true, p) || !len_pos || ws_bytes < p.ws_bytes + 256) return CDNA4_ERR_INVALID_VALUE;
     const bool bf = dtype == CDNA4_BF16;
     if (c.D == 128) return bf ? launch_decode<128, true>(c, p, q, K, V, o, ws, s, len_pos)
                               : launch_decode<128, false>(c, p, q, K, V, o, ws, s, len_pos);
@@ -379,29 +375,30 @@ using namespace cdna4;
 
 extern "C" size_t cdna3_attn_decode_workspace_size(const cdna3_decode_cfg* cfg) {
     Plan p;
-    if (!cfg || !plan_decode(*cfg, p)) return 0;
+    if (!cfg || !plan_decode(*cfg, true, p)) return 0;
     return p.ws_bytes + 256;
 }
 
 extern "C" int cdna3_attn_decode(const void* q, const void* K, const void* V, void* o, const cdna3_decode_cfg* cfg,
                                  int dtype, void* workspace, size_t ws_bytes, cdna4_stream_t stream) {
     Plan p;
-    if (!cfg || !plan_decode(*cfg, p)) return CDNA4_ERR_INVALID_VALUE;
-    if (dtype != CDNA4_F16 && dtype != CDNA4_BF16) return CDNA4_ERR_INVALID_VALUE;
-    if (!q || !K || !V || !o) return CDNA4_ERR_INVALID_VALUE;
-    // 16-byte loads of q/K/V rows.
-    if ((((uintptr_t)q | (uintptr_t)K | (uintptr_t)V) & 15u) != 0) return CDNA4_ERR_INVALID_VALUE;
-    if (((uintptr_t)o & 3u) != 0) return CDNA4_ERR_INVALID_VALUE;
-    const size_t need = p.ws_bytes + 256;
-    if (workspace != nullptr && ws_bytes < need) return CDNA4_ERR_INVALID_VALUE;
+    if (!cfg || !plan_decode(*cfg, workspace != nullptr, p)) return CDNA4_ERR_INVALID_VALUE;
+    if (int e = check_decode_args(q, K, V, o, dtype)) return e;
+    if (workspace != nullptr && ws_bytes < p.ws_bytes + 256) return CDNA4_ERR_INVALID_VALUE;
     if (int e = check_device()) return e;
-    if (workspace == nullptr) {
-        if (int e = fallback_workspace(need, &workspace)) return e;
-    }
-    hipStream_t s = (hipStream_t)stream;
-    const bool bf = dtype == CDNA4_BF16;
-    if (cfg->D == 128) return bf ? launch_decode<128, true>(*cfg, p, q, K, V, o, workspace, s)
-                                 : launch_decode<128, false>(*cfg, p, q, K, V, o, workspace, s);
-    return bf ? launch_decode<64, true>(*cfg, p, q, K, V, o, workspace, s)
-              : launch_decode<64, false>(*cfg, p, q, K, V, o, workspace, s);
+    return run_decode(*cfg, p, q, K, V, o, dtype, workspace, (hipStream_t)stream);
+}
+
+extern "C" int cdna3_attn_decode_plan(const cdna3_decode_cfg* cfg, int dtype, int with_workspace,
+                                      cdna3_plan_info* out) {
+    Plan p;
+    if (!cfg || !out || !plan_decode(*cfg, with_workspace != 0, p)) return CDNA4_ERR_INVALID_VALUE;
+    if (dtype != CDNA4_F16 && dtype != CDNA4_BF16) return CDNA4_ERR_INVALID_VALUE;
+    out->kernel = p.wg ? CDNA4_KERNEL_DECODE_WG : CDNA4_KERNEL_DECODE_SPLIT;
+    out->waves = p.wg ? (cfg->D == 64 ? wg_waves<64>() : wg_waves<128>()) : 1;
+    out->rows = p.KPW;
+    out->partials = p.P;
+    out->grid = (long long)p.P * cfg->nKVHeads * p.HB * cfg->batch;
+    out->workspace = p.wg ? 0 : p.ws_bytes + 256;
+    return 0;
 }

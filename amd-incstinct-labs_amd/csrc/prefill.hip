@@ -509,10 +509,38 @@ __global__ __launch_bounds__(64 * W) void fa_small(PrefillArgs a) {
     }
 }
 
-template <int D, int W, int QT, bool kBf16>
-int launch_mfma(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& st, const void* Q, const void* K,
-                const void* V, void* O, hipStream_t s) {
-    constexpr int BM = W * QT * 16;
+// Kernel choice for the 16-bit path: 8 waves x 32 queries (two waves per SIMD) when that gives
+// >= 2 workgroups per CU; 4 waves x 16 queries for mid-size problems; for problems whose 64-query
+// blocks would not fill the CUs twice over, 16 queries per workgroup with the keys split over its
+// waves (the large form when one round of workgroups covers the grid).
+struct PrefillPlan { int kernel, waves, rows; long long grid; };
+
+template <int D>
+PrefillPlan plan_mfma(const cdna3_prefill_cfg& c) {
+    const long long heads = (long long)c.batch * c.nQHeads;
+    const int cus = device_cus();
+    PrefillPlan p;
+    if (heads * ((c.seqQ + 255) / 256) >= 512) {
+        p.kernel = CDNA4_KERNEL_PREFILL_MFMA_8W; p.waves = 8; p.rows = 256;
+        p.grid = heads * ((c.seqQ + 255) / 256);
+        // One resident workgroup per CU at W = 8 (LDS and VGPRs allow no second), so a grid of one
+        // workgroup per CU (a multiple of 8, see the item mapping) runs every item without
+        // relaunch gaps between workgroups.
+        const int pcus = cus & ~7;
+        if (pcus >= 8 && p.grid > pcus) p.grid = pcus;
+    } else if (heads * ((c.seqQ + 63) / 64) >= 2LL * cus) {
+        p.kernel = CDNA4_KERNEL_PREFILL_MFMA_4W; p.waves = 4; p.rows = 64;
+        p.grid = heads * ((c.seqQ + 63) / 64);
+    } else {
+        p.kernel = CDNA4_KERNEL_PREFILL_SMALL; p.rows = 16;
+        p.grid = heads * ((c.seqQ + 15) / 16);
+        p.waves = small_waves<D>(p.grid <= cus);
+    }
+    return p;
+}
+
+PrefillArgs make_args(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& st, const void* Q, const void* K,
+                      const void* V, void* O, int rows) {
     PrefillArgs a;
     a.Q = (const uint16_t*)Q; a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.O = (uint16_t*)O;
     a.q_bs = st.q_batch; a.q_hs = st.q_head; a.q_rs = st.q_row;
@@ -520,48 +548,34 @@ int launch_mfma(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& st, con
     a.o_bs = st.o_batch; a.o_hs = st.o_head; a.o_rs = st.o_row;
     a.seqQ = c.seqQ; a.seqK = c.seqK; a.nQH = c.nQHeads; a.nKVH = c.nKVHeads; a.batch = c.batch;
     a.causal = c.causal ? 1 : 0;
-    a.nqb = (c.seqQ + BM - 1) / BM;
-    const long long nbh = (long long)c.batch * c.nQHeads;
-    a.xcd_map = (nbh % 8 == 0) ? 1 : 0;
-    a.sc = kLog2e / sqrtf((float)D);
-    const long long blocks = nbh * a.nqb;
-    if (blocks > 0x7fffffffLL) return CDNA4_ERR_INVALID_VALUE;
-    // One resident workgroup per CU at W = 8 (LDS and VGPRs allow no second), so a grid of one
-    // workgroup per CU (a multiple of 8, see the item mapping) runs every item without relaunch
-    // gaps between workgroups.
-    long long grid = blocks;
-    const int cus = device_cus() & ~7;
-    if (W == 8 && cus >= 8 && grid > cus) grid = cus;
-    fa_mfma<D, W, QT, kBf16><<<(unsigned)grid, 64 * W, 0, s>>>(a);
-    return launch_status();
+    a.nqb = (c.seqQ + rows - 1) / rows;
+    a.xcd_map = 0;
+    a.sc = kLog2e / sqrtf((float)c.D);
+    return a;
 }
 
 template <int D, bool kBf16>
 int dispatch_mfma(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& st, const void* Q, const void* K,
                   const void* V, void* O, hipStream_t s) {
-    // 8 waves x 32 queries (two waves per SIMD) when that gives >= 2 workgroups per CU; 4 waves x
-    // 16 queries for mid-size problems; for problems whose 64-query blocks would not fill the CUs
-    // twice over, 16 queries per workgroup with the keys split over its waves.
-    const long long heads = (long long)c.batch * c.nQHeads;
-    const long long big_blocks = heads * ((c.seqQ + 255) / 256);
-    if (big_blocks >= 512) return launch_mfma<D, 8, 2, kBf16>(c, st, Q, K, V, O, s);
-    if (heads * ((c.seqQ + 63) / 64) >= 2LL * device_cus()) return launch_mfma<D, 4, 1, kBf16>(c, st, Q, K, V, O, s);
-    PrefillArgs a;
-    a.Q = (const uint16_t*)Q; a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.O = (uint16_t*)O;
-    a.q_bs = st.q_batch; a.q_hs = st.q_head; a.q_rs = st.q_row;
-    a.k_bs = st.kv_batch; a.k_hs = st.kv_head; a.k_rs = st.kv_row;
-    a.o_bs = st.o_batch; a.o_hs = st.o_head; a.o_rs = st.o_row;
-    a.seqQ = c.seqQ; a.seqK = c.seqK; a.nQH = c.nQHeads; a.nKVH = c.nKVHeads; a.batch = c.batch;
-    a.causal = c.causal ? 1 : 0;
-    a.nqb = (c.seqQ + 15) / 16;
-    a.xcd_map = 0;
-    a.sc = kLog2e / sqrtf((float)D);
-    const long long blocks = heads * a.nqb;
-    if (blocks > 0x7fffffffLL) return CDNA4_ERR_INVALID_VALUE;
-    if (blocks <= device_cus())
-        fa_small<D, kBf16, small_waves<D>(true)><<<(unsigned)blocks, 64 * small_waves<D>(true), 0, s>>>(a);
-    else
-        fa_small<D, kBf16, small_waves<D>(false)><<<(unsigned)blocks, 64 * small_waves<D>(false), 0, s>>>(a);
+    const PrefillPlan p = plan_mfma<D>(c);
+    PrefillArgs a = make_args(c, st, Q, K, V, O, p.rows);
+    const long long nbh = (long long)c.batch * c.nQHeads;
+    if (nbh * a.nqb > 0x7fffffffLL) return CDNA4_ERR_INVALID_VALUE;
+    switch (p.kernel) {
+        case CDNA4_KERNEL_PREFILL_MFMA_8W:
+            a.xcd_map = (nbh % 8 == 0) ? 1 : 0;
+            fa_mfma<D, 8, 2, kBf16><<<(unsigned)p.grid, 64 * 8, 0, s>>>(a);
+            break;
+        case CDNA4_KERNEL_PREFILL_MFMA_4W:
+            a.xcd_map = (nbh % 8 == 0) ? 1 : 0;
+            fa_mfma<D, 4, 1, kBf16><<<(unsigned)p.grid, 64 * 4, 0, s>>>(a);
+            break;
+        default:
+            if (p.waves == small_waves<D>(true))
+                fa_small<D, kBf16, small_waves<D>(true)><<<(unsigned)p.grid, 64 * small_waves<D>(true), 0, s>>>(a);
+            else
+                fa_small<D, kBf16, small_waves<D>(false)><<<(unsigned)p.grid, 64 * small_waves<D>(false), 0, s>>>(a);
+    }
     return launch_status();
 }
 
@@ -647,4 +661,29 @@ extern "C" int cdna3_attn_prefill_strided(const void* Q, const void* K, const vo
     if (c.D == 128)
         return bf ? dispatch_mfma<128, true>(c, st, Q, K, V, O, s) : dispatch_mfma<128, false>(c, st, Q, K, V, O, s);
     return bf ? dispatch_mfma<64, true>(c, st, Q, K, V, O, s) : dispatch_mfma<64, false>(c, st, Q, K, V, O, s);
+}
+
+extern "C" int cdna3_attn_prefill_plan(const cdna3_prefill_cfg* cfg, int dtype, cdna3_plan_info* out) {
+    if (!cfg || !out) return CDNA4_ERR_INVALID_VALUE;
+    const cdna3_prefill_cfg& c = *cfg;
+    if (c.D != 64 && c.D != 128) return CDNA4_ERR_INVALID_VALUE;
+    if (c.seqQ < 1 || c.seqK < 1 || c.nQHeads < 1 || c.nKVHeads < 1 || c.batch < 1) return CDNA4_ERR_INVALID_VALUE;
+    if (c.nQHeads % c.nKVHeads || (c.causal && c.seqQ != c.seqK)) return CDNA4_ERR_INVALID_VALUE;
+    if (dtype == CDNA4_F32) {
+        out->kernel = CDNA4_KERNEL_PREFILL_F32;
+        out->waves = kF32Waves;
+        out->rows = kF32Br;
+        out->grid = (long long)c.batch * c.nQHeads * ((c.seqQ + kF32Br - 1) / kF32Br);
+    } else if (dtype == CDNA4_F16 || dtype == CDNA4_BF16) {
+        const PrefillPlan p = c.D == 128 ? plan_mfma<128>(c) : plan_mfma<64>(c);
+        out->kernel = p.kernel;
+        out->waves = p.waves;
+        out->rows = p.rows;
+        out->grid = p.grid;
+    } else {
+        return CDNA4_ERR_INVALID_VALUE;
+    }
+    out->partials = 1;
+    out->workspace = 0;
+    return 0;
 }

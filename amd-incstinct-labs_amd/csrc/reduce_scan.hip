@@ -562,3 +562,15 @@ extern "C" int cdna3_scan_inclusive(int op, int dtype, const void* in, size_t n,
     if (int e = check_device()) return e;
     return by_dtype<ScanF>(op, dtype, in, n, out, workspace, (hipStream_t)stream);
 }
+
+extern "C" int cdna3_scan_status(const void* workspace, int* status, cdna4_stream_t stream) {
+    if (workspace == nullptr || status == nullptr) return CDNA4_ERR_INVALID_VALUE;
+    if (int e = check_device()) return e;
+    uint32_t word = 0;
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = hipMemcpyAsync(&word, workspace, sizeof(word), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return (int)e;
+    *status = (int)word;
+    return 0;
+}

@@ -82,7 +82,15 @@ def time_launches(torch, fn, steps, warmup):
     return total / steps, total
 
 
+TRAFFIC_SOURCE = ("profiles/traffic.json: HBM bytes per launch from an earlier rocprofv3 --pmc FETCH_SIZE / "
+                  "WRITE_SIZE run of this kernel at this workload, calibrated on a 1 GiB copy; not measured "
+                  "in this run")
+
+
 def load_traffic(name):
+    """HBM bytes per launch recorded for a kernel in profiles/traffic.json (None when absent). The
+    counters cannot be read inside this run (rocprofv3 --pmc is a separate profiling pass), so the
+    roofline objects name this source next to the figure."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
@@ -312,7 +320,8 @@ def bench_decode(torch, cdna4, steps, warmup):
             "config": {"workload": "flash decode, BASELINE config 4", "batch": B, "q_heads": HQ, "kv_heads": HK,
                        "head_dim": D, "kv_len": N, "dtype": "fp16"},
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": gbs / PEAK_HBM_GBS, "traffic": load_traffic("decode")}}
+                         "frac": gbs / PEAK_HBM_GBS, "traffic": load_traffic("decode"),
+                         "traffic_source": TRAFFIC_SOURCE}}
 
 
 def bench_dpp(torch, cdna4, steps, warmup):
@@ -491,7 +500,8 @@ def main():
                        "config": p["config"],
                        "roofline": {"bound": "mfma", "achieved": p["tflops"], "peak": PEAK_BF16_TFLOPS,
                                     "unit": "TFLOP/s", "frac": p["tflops"] / PEAK_BF16_TFLOPS,
-                                    "traffic": load_traffic("prefill"), "kernel_avg_ms": p["avg_ms"]}})
+                                    "traffic": load_traffic("prefill"), "traffic_source": TRAFFIC_SOURCE,
+                                    "kernel_avg_ms": p["avg_ms"]}})
         del p
         torch.cuda.empty_cache()
         p16 = bench_prefill(torch, cdna4, max(5, args.steps // 2), max(3, args.warmup // 2), torch.float16)

@@ -10,10 +10,12 @@
 // Behaviour differences from the reference, all documented in cdna4_attn.h:
 //   * any seqQ / seqK >= 1 is computed in full (the reference silently truncated shapes that
 //     were not multiples of its tiles); causal requires seqQ == seqK;
-//   * decode and decode_dme share one split-K kernel; their split-K partials live in a
-//     per-device buffer the library allocates on first use (the reference launchers take no
-//     workspace). Pass one through decode(..., workspace, bytes, stream) to avoid that.
-// New overloads: bf16 tensors, a batch dimension (DecodeCfg::batch), fp32 prefill.
+//   * decode and decode_dme without a workspace run one launch that needs no memory beyond
+//     q, K, V and o, like the reference's (no allocation, nothing shared between calls);
+//     the overloads taking (workspace, bytes) split long caches over a split-K grid instead,
+//     which is much faster for a few long sequences (decode_workspace_size gives the bytes).
+// New overloads: bf16 tensors, a batch dimension (DecodeCfg::batch), fp32 prefill, split-K
+// workspaces.
 #include <hip/hip_runtime_api.h>
 #include <hip/hip_fp16.h>
 #include <hip/hip_bf16.h>
@@ -85,7 +87,7 @@ inline hipError_t decode(const __hip_bfloat16* q, const __hip_bfloat16* K, const
     return detail::decode_any(q, K, V, o, cdna3_decode_cfg{cfg.D, cfg.N, cfg.nQHeads, cfg.nKVHeads, cfg.batch, 0},
                               CDNA4_BF16, nullptr, 0, stream);
 }
-// Caller-owned split-K workspace (>= decode_workspace_size(cfg) bytes): no library allocation.
+// Caller-owned split-K workspace (>= decode_workspace_size(cfg) bytes, no initialisation).
 inline size_t decode_workspace_size(const DecodeCfg& cfg) {
     const cdna3_decode_cfg c{cfg.D, cfg.N, cfg.nQHeads, cfg.nKVHeads, cfg.batch, 0};
     return cdna3_attn_decode_workspace_size(&c);
@@ -95,12 +97,27 @@ inline hipError_t decode(const __half* q, const __half* K, const __half* V, __ha
     return detail::decode_any(q, K, V, o, cdna3_decode_cfg{cfg.D, cfg.N, cfg.nQHeads, cfg.nKVHeads, cfg.batch, 0},
                               CDNA4_F16, workspace, ws_bytes, stream);
 }
+inline hipError_t decode(const __hip_bfloat16* q, const __hip_bfloat16* K, const __hip_bfloat16* V,
+                         __hip_bfloat16* o, const DecodeCfg& cfg, void* workspace, size_t ws_bytes,
+                         hipStream_t stream) {
+    return detail::decode_any(q, K, V, o, cdna3_decode_cfg{cfg.D, cfg.N, cfg.nQHeads, cfg.nKVHeads, cfg.batch, 0},
+                              CDNA4_BF16, workspace, ws_bytes, stream);
+}
 
 // K/V layout [nKVHeads, stride_kv, D] head-major; pass K_layer(li, 0) as in the reference.
 inline hipError_t decode_dme(const __half* q, const __half* K, const __half* V, __half* o, const DecodeDmeCfg& cfg,
                              hipStream_t stream = nullptr) {
     return detail::decode_any(q, K, V, o, cdna3_decode_cfg{cfg.D, cfg.N, cfg.nQHeads, cfg.nKVHeads, 1, cfg.stride_kv},
                               CDNA4_F16, nullptr, 0, stream);
+}
+inline size_t decode_dme_workspace_size(const DecodeDmeCfg& cfg) {
+    const cdna3_decode_cfg c{cfg.D, cfg.N, cfg.nQHeads, cfg.nKVHeads, 1, cfg.stride_kv};
+    return cdna3_attn_decode_workspace_size(&c);
+}
+inline hipError_t decode_dme(const __half* q, const __half* K, const __half* V, __half* o, const DecodeDmeCfg& cfg,
+                             void* workspace, size_t ws_bytes, hipStream_t stream) {
+    return detail::decode_any(q, K, V, o, cdna3_decode_cfg{cfg.D, cfg.N, cfg.nQHeads, cfg.nKVHeads, 1, cfg.stride_kv},
+                              CDNA4_F16, workspace, ws_bytes, stream);
 }
 
 }  // namespace attn

@@ -11,8 +11,8 @@
 //                                                              K, V [nKVH][N][D]
 // Differences: any seq >= 1 is computed (the reference required seq % 16 == 0 and dropped the
 // tail otherwise); W, the reference's split-KV wave count (2 or 4), is validated as there but the
-// library chooses its own split; decode uses the library's per-device split-K buffer (allocated
-// once, on first use).
+// library chooses its own plan; decode runs the one-launch plan that needs no workspace (no
+// allocation, nothing shared between calls), as the reference's launcher did.
 #include <hip/hip_runtime_api.h>
 #include <hip/hip_fp16.h>
 #include "../cdna4_attn.h"

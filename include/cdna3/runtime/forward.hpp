@@ -1,17 +1,25 @@
 #pragma once
-// cdna3/runtime/forward.hpp — the runtime's norm and RoPE entry points (gfx950), host side.
+// cdna3/runtime/forward.hpp — the runtime's norm, RoPE and KV-layout entry points (gfx950).
 //
-// The reference launched __global__ kernels directly (cdna3-prims/include/cdna3/runtime/
-// forward.hpp:34-56 rmsnorm_f32_kernel, :135-148 rope_kernel; the two-pass DPP layernorm of
-// research/wave-primitives/benchmarks/bench_layernorm.hip:51-114; host table fill_rope in
-// session.hpp:120-135). Here they are host functions over libcdna4_attn.so:
-//   hipLaunchKernelGGL(rmsnorm_f32_kernel, dim3(M), dim3(256), 0, s, X, W, Y, M, H, eps)
-//     -> cdna3::runtime::rmsnorm_f32(X, W, Y, M, H, eps, s)
-//   hipLaunchKernelGGL(rope_kernel, grid, 256, 0, s, T, cos, sin, seq, heads, D)
-//     -> cdna3::runtime::rope_f16(T, cos, sin, seq, heads, D, s)
+// The reference's layer loop launches __global__ kernels from this header directly
+// (cdna3-prims/include/cdna3/runtime/forward.hpp:34-56 rmsnorm_f32_kernel, :135-148 rope_kernel,
+// :190-239 repack / scatter_kv / pack_kv kernels; launched by session.hpp:168-250). Two forms:
+//   * host functions over libcdna4_attn.so (any host compiler), e.g.
+//       cdna3::runtime::rmsnorm_f32(X, W, Y, M, H, eps, s)
+//       cdna3::runtime::rope_f16(T, cos, sin, seq, heads, D, s)
+//     plus the device-side fill_rope (rope_table_f32) and the fused RoPE + K/V append;
+//   * in HIP source (hipcc), the kernels themselves under the reference's names and signatures,
+//     so code that does
+//       hipLaunchKernelGGL(rmsnorm_f32_kernel, dim3(M), dim3(256), 0, s, X, W, Y, M, H, eps)
+//       hipLaunchKernelGGL(rope_kernel, dim3((seq*heads*D + 255)/256), dim3(256), 0, s, T, cos, sin,
+//                          seq, heads, D)
+//     compiles and runs unchanged on gfx950 (see forward_kernels.hpp for their design).
 #include <hip/hip_runtime_api.h>
 #include <hip/hip_fp16.h>
 #include "../../cdna4_attn.h"
+#if defined(__HIP__)
+#include "forward_kernels.hpp"
+#endif
 
 namespace cdna3 {
 namespace runtime {

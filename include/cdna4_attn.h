@@ -8,7 +8,8 @@
  *   - returns 0 (hipSuccess) or a hipError_t value: CDNA4_ERR_INVALID_VALUE (1) for a
  *     shape, dtype or op it does not support, CDNA4_ERR_INVALID_DEVICE_FUNCTION (98)
  *     when the current device is not gfx950, otherwise the launch error;
- *   - never allocates, except cdna3_attn_decode with workspace == NULL (see there).
+ *   - never allocates device memory and keeps no device buffers between calls (the session
+ *     API below owns the memory of its session);
  * All entry points are re-entrant from any host thread; ordering comes from the stream.
  *
  * Tensor layouts are row-major and contiguous unless a stride is given.
@@ -26,7 +27,7 @@ extern "C" {
 /* hipStream_t is `struct ihipStream_t*`; this typedef is layout-identical. */
 typedef struct ihipStream_t* cdna4_stream_t;
 
-#define CDNA4_ABI_VERSION 1
+#define CDNA4_ABI_VERSION 2
 
 enum {
     CDNA4_OK = 0,
@@ -121,15 +122,46 @@ int cdna3_attn_prefill_strided(const void* Q, const void* K, const void* V, void
  * (attention.hpp:152-173); the reference has no batch dimension (batch == 1 here).
  * q, o: [batch][nQHeads][D]; K, V: [batch][nKVHeads][stride_kv][D] (first N rows of
  * each head are read). dtype CDNA4_F16 or CDNA4_BF16 (q, K, V, o alike).
- * Split-K partial results go to `workspace` (ws_bytes >= the size returned by
- * cdna3_attn_decode_workspace_size; the contents need no initialisation). With
- * workspace == NULL the library uses a per-device buffer it allocates on first use
- * and keeps until process exit; that form is not safe under stream capture.
+ * With a workspace (ws_bytes >= cdna3_attn_decode_workspace_size(cfg); the contents need no
+ * initialisation), long caches are split over a grid of single-wave workgroups that leave
+ * (m, l, O) partials in it, merged by a second kernel. With workspace == NULL the call takes
+ * the one-launch plan, which needs no memory beyond q, K, V and o: one workgroup per (batch,
+ * kv head, group of 16 query heads) streams the whole cache, like the reference's launchers,
+ * which take no workspace. Both forms are capturable and re-entrant across streams (a
+ * workspace must not be shared by calls that overlap).
  */
 size_t cdna3_attn_decode_workspace_size(const cdna3_decode_cfg* cfg);
 int cdna3_attn_decode(const void* q, const void* K, const void* V, void* o,
                       const cdna3_decode_cfg* cfg, int dtype,
                       void* workspace, size_t ws_bytes, cdna4_stream_t stream);
+
+/* ---- kernel plans (introspection) ---------------------------------------------
+ * No counterpart in the reference (its launchers had one kernel each). Report which kernel a
+ * call with the same arguments would launch on the current device, without launching it, so
+ * tests and profilers can assert the kernel they mean to cover. Returns 0 or
+ * CDNA4_ERR_INVALID_VALUE for arguments the entry point would reject.
+ */
+enum {
+    CDNA4_KERNEL_PREFILL_MFMA_8W = 1,  /* fa_mfma: 8 waves x 32 queries, persistent XCD-local grid */
+    CDNA4_KERNEL_PREFILL_MFMA_4W = 2,  /* fa_mfma: 4 waves x 16 queries, one workgroup per block */
+    CDNA4_KERNEL_PREFILL_SMALL = 3,    /* fa_small: 16 queries per workgroup, keys split over its waves */
+    CDNA4_KERNEL_PREFILL_F32 = 4,      /* fa_f32: fp32 matrix-core kernel */
+    CDNA4_KERNEL_DECODE_SPLIT = 5,     /* decode_mfma split-K grid + decode_merge */
+    CDNA4_KERNEL_DECODE_WG = 6         /* decode_wg: one launch, no workspace */
+};
+
+typedef struct {
+    int kernel;        /* CDNA4_KERNEL_* */
+    int waves;         /* waves per workgroup */
+    int rows;          /* prefill: query rows per work item; decode: keys per split (per wave for WG) */
+    int partials;      /* decode: split-K partials per query head (1 for one launch); prefill: 1 */
+    long long grid;    /* workgroups launched */
+    size_t workspace;  /* bytes of workspace the plan needs (0: none) */
+} cdna3_plan_info;
+
+int cdna3_attn_prefill_plan(const cdna3_prefill_cfg* cfg, int dtype, cdna3_plan_info* out);
+int cdna3_attn_decode_plan(const cdna3_decode_cfg* cfg, int dtype, int with_workspace,
+                           cdna3_plan_info* out);
 
 /* ---- device-wide reduce / scan on the wave64 DPP primitives ------------------
  * Device-wide counterparts of wave::dpp::reduce_* / scan_inclusive_* (research/
@@ -140,6 +172,10 @@ int cdna3_attn_decode(const void* q, const void* K, const void* V, void* o,
  * reduce: `out` receives one element. scan: `out` receives n elements.
  * n == 0: reduce writes the operator's identity; scan writes nothing.
  * Workspace: >= the returned size, no initialisation needed.
+ * Scan status: the scan's decoupled look-back waits a bounded time for a predecessor tile; if a
+ * wait ever exceeds that bound the result is not valid and the first 32-bit word of the
+ * workspace is set non-zero (each scan call clears it first). cdna3_scan_status synchronises
+ * `stream` and returns that word in *status (0 = the last scan on this workspace is valid).
  */
 size_t cdna3_reduce_workspace_size(size_t n, int dtype);
 int cdna3_reduce(int op, int dtype, const void* in, size_t n, void* out,
@@ -147,6 +183,7 @@ int cdna3_reduce(int op, int dtype, const void* in, size_t n, void* out,
 size_t cdna3_scan_workspace_size(size_t n, int dtype);
 int cdna3_scan_inclusive(int op, int dtype, const void* in, size_t n, void* out,
                          void* workspace, size_t ws_bytes, cdna4_stream_t stream);
+int cdna3_scan_status(const void* workspace, int* status, cdna4_stream_t stream);
 
 /* ---- runtime norms and RoPE ---------------------------------------------------
  * cdna3_rmsnorm_f32 replaces rmsnorm_f32_kernel (cdna3-prims/include/cdna3/runtime/

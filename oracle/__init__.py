@@ -236,6 +236,11 @@ def rope_append_kv(q_bits, k_bits, v_bits, K_cache_bits, V_cache_bits, cos, sin,
 
 # ---- the reference's own CPU references (oracle/_ref) ------------------------------------------
 
+def ref_available(name: str) -> bool:
+    """True when oracle/_ref/lib<name>.so was built here; checks the file only, loads nothing."""
+    return os.path.exists(os.path.join(HERE, "_ref", f"lib{name}.so"))
+
+
 def ref_lib(name: str) -> Optional[ctypes.CDLL]:
     """oracle/_ref/lib<name>.so if it was built here from /root/reference, else None."""
     if name not in _REF:

@@ -29,7 +29,7 @@ def test_library_exports_every_header_symbol():
 
 
 def test_version_and_error_strings():
-    assert cdna4.abi_version() == 1
+    assert cdna4.abi_version() == 2
     assert "invalid" in cdna4.error_string(1)
     assert "gfx950" in cdna4.error_string(98)
     assert cdna4.error_string(0) == "success"

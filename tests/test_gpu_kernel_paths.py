@@ -1,0 +1,293 @@
+"""Every kernel the prefill and decode dispatchers can pick, against the CPU oracle.
+
+Each case first asks the library which kernel it will launch (cdna3_attn_prefill_plan /
+cdna3_attn_decode_plan) and asserts the one the case is meant to cover, then compares the GPU
+output with the oracle (the restated cpu_prefill / cpu_decode of
+cdna3-prims/tests/validate_attention_api.hip:27-72) on the same rounded inputs. Large prefill
+shapes are checked on a seeded subsample of query rows of every (or every listed) head, with the
+output pre-filled with NaN so that an unwritten row anywhere in the tensor fails the finiteness
+check. Bounds: gpu_util.tolerance (fp16 2e-3, bf16 2e-3 + 2 x 2^-9, in units of max(1, |ref|)).
+"""
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+import torch
+
+import cdna4
+import oracle
+from gpu_util import DEV, max_rel_err, tolerance
+
+pytestmark = pytest.mark.gpu
+
+_POOL = ThreadPoolExecutor(max_workers=8)   # the oracle is C called through ctypes (GIL released)
+
+
+def _randn(shape, dtype, g):
+    return torch.randn(*shape, device=DEV, generator=g).to(dtype)
+
+
+def _rows(SQ, seed, n_random=64):
+    """Query rows checked per head: the first 128, the middle, the last 64 and seeded random rows."""
+    rows = set(range(min(SQ, 128))) | {SQ // 2 - 1, SQ // 2} | set(range(max(0, SQ - 64), SQ))
+    rows |= set(int(r) for r in oracle.integers(seed, n_random, 0, SQ - 1))
+    return sorted(r for r in rows if 0 <= r < SQ)
+
+
+def _oracle_heads(q, k, v, heads, rows, D, SQ, SK, HQ, HK, causal):
+    """Oracle rows of the listed (batch, head) pairs, computed per head in parallel."""
+    grp = HQ // HK
+    req = np.array([[0, 0, r] for r in rows], np.int32)
+
+    def one(bh):
+        b, h = bh
+        return oracle.prefill_rows(q[b, h], k[b, h // grp], v[b, h // grp], D, SQ, SK, 1, 1, 1, causal, req)
+
+    return dict(zip(heads, _POOL.map(one, heads)))
+
+
+def check_prefill(D, SQ, SK, HQ, HK, B, causal, dtype, kernel, seed=0, heads=None):
+    cfg = cdna4.PrefillCfg(D, SQ, SK, HQ, HK, B, causal)
+    plan = cdna4.prefill_plan(cfg, dtype)
+    print(f"prefill D{D} SQ{SQ} SK{SK} HQ{HQ} HK{HK} B{B} causal{causal} {dtype} -> {plan.name} "
+          f"(grid {plan.grid})", flush=True)
+    assert plan.name == kernel
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    Q = _randn((B, HQ, SQ, D), dtype, g)
+    K = _randn((B, HK, SK, D), dtype, g)
+    V = _randn((B, HK, SK, D), dtype, g)
+    O = torch.full_like(Q, float("nan"))
+    cdna4.prefill(Q, K, V, O, cfg)
+    torch.cuda.synchronize()
+    assert torch.isfinite(O.float()).all(), "unwritten or non-finite output rows"
+    heads = heads or [(b, h) for b in range(B) for h in range(HQ)]
+    rows = _rows(SQ, seed + 1)
+    q, k, v = (t.float().cpu().numpy() for t in (Q, K, V))
+    want = _oracle_heads(q, k, v, heads, rows, D, SQ, SK, HQ, HK, causal)
+    o = O.float().cpu().numpy()
+    worst = max(max_rel_err(o[b, h, rows], want[(b, h)]) for b, h in heads)
+    print(f"  {len(heads)} heads x {len(rows)} rows: max err {worst:.2e}", flush=True)
+    assert worst <= tolerance(dtype)
+
+
+# ---- fa_mfma<D, 8, 2>: batch * heads * ceil(seqQ / 256) >= 512 --------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fa_mfma_8w_d128_causal_mha(dtype):
+    check_prefill(128, 4096, 4096, 32, 32, 2, 1, dtype, "fa_mfma_8w", seed=1,
+                  heads=[(b, h) for b in (0, 1) for h in range(0, 32, 3)])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fa_mfma_8w_d128_noncausal(dtype):
+    check_prefill(128, 4096, 4096, 32, 32, 1, 0, dtype, "fa_mfma_8w", seed=2, heads=[(0, h) for h in range(0, 32, 4)])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fa_mfma_8w_gqa_4to1_causal(dtype):
+    check_prefill(128, 4096, 4096, 32, 8, 1, 1, dtype, "fa_mfma_8w", seed=3, heads=[(0, h) for h in range(32)])
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fa_mfma_8w_d64(dtype, causal):
+    check_prefill(64, 2048, 2048, 64, 64, 1, causal, dtype, "fa_mfma_8w", seed=4, heads=[(0, h) for h in range(0, 64, 5)])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fa_mfma_8w_ragged_causal(dtype):
+    # seqQ = seqK = 4093: the last q block and the last K/V tile are partial inside fa_mfma.
+    check_prefill(128, 4093, 4093, 32, 32, 2, 1, dtype, "fa_mfma_8w", seed=5,
+                  heads=[(0, 0), (0, 17), (1, 8), (1, 31)])
+
+
+def test_fa_mfma_8w_ragged_cross_attention():
+    # seqQ != seqK, neither a multiple of a tile, GQA 4:1, non-causal (heads not a multiple of 8:
+    # the item mapping without the XCD grouping).
+    check_prefill(64, 4096 + 37, 3001, 36, 9, 1, 0, torch.float16, "fa_mfma_8w", seed=6,
+                  heads=[(0, 0), (0, 4), (0, 20), (0, 35)])
+
+
+# ---- fa_mfma<D, 4, 1>: mid-size problems --------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fa_mfma_4w_d128_causal(dtype):
+    check_prefill(128, 4096, 4096, 8, 8, 1, 1, dtype, "fa_mfma_4w", seed=7)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fa_mfma_4w_d64_gqa_noncausal(dtype):
+    check_prefill(64, 2048, 2048, 16, 4, 1, 0, dtype, "fa_mfma_4w", seed=8)
+
+
+def test_fa_mfma_4w_ragged_causal():
+    check_prefill(128, 4093, 4093, 8, 2, 1, 1, torch.float16, "fa_mfma_4w", seed=9)
+
+
+def test_fa_mfma_4w_cross_attention():
+    check_prefill(64, 4096, 1003, 8, 8, 1, 0, torch.bfloat16, "fa_mfma_4w", seed=10)
+
+
+# ---- fa_small: both workgroup forms -------------------------------------------------------------
+
+@pytest.mark.parametrize("D,SQ,HQ,HK,B", [(128, 512, 8, 8, 1), (64, 700, 12, 4, 2)])
+def test_fa_small_forms(D, SQ, HQ, HK, B):
+    cfg = cdna4.PrefillCfg(D, SQ, SQ, HQ, HK, B, 1)
+    waves = cdna4.prefill_plan(cfg, torch.float16).waves
+    print(f"fa_small waves {waves}", flush=True)
+    check_prefill(D, SQ, SQ, HQ, HK, B, 1, torch.float16, "fa_small", seed=11)
+
+
+# ---- the strided entry point (the runtime's prompt path) against the oracle ----------------------
+
+@pytest.mark.parametrize("D,S,HQ,HK,dtype,kernel", [(64, 2048, 16, 4, torch.float16, "fa_mfma_4w"),
+                                                     (128, 4096, 32, 8, torch.bfloat16, "fa_mfma_8w"),
+                                                     (64, 300, 12, 12, torch.float16, "fa_small")])
+def test_prefill_strided_against_oracle(D, S, HQ, HK, dtype, kernel):
+    max_seq = (S + 100 + 7) // 8 * 8
+    cfg = cdna4.PrefillCfg(D, S, S, HQ, HK, 1, 1)
+    plan = cdna4.prefill_plan(cfg, dtype)
+    print(f"strided prefill D{D} S{S} {HQ}/{HK} -> {plan.name}", flush=True)
+    assert plan.name == kernel
+    g = torch.Generator(device=DEV).manual_seed(S + D)
+    Q = _randn((HQ, S, D), dtype, g)
+    Kc = _randn((HK, max_seq, D), dtype, g)
+    Vc = _randn((HK, max_seq, D), dtype, g)
+    O_tok = torch.full((S, HQ, D), float("nan"), device=DEV, dtype=dtype)
+    st = cdna4.PrefillStrides(HQ * S * D, S * D, D, HK * max_seq * D, max_seq * D, D, S * HQ * D, D, HQ * D)
+    cdna4.prefill_strided(Q, Kc, Vc, O_tok, cfg, st)
+    torch.cuda.synchronize()
+    assert torch.isfinite(O_tok.float()).all()
+    rows = _rows(S, 3)
+    q = Q.float().cpu().numpy()[None]
+    k = Kc[:, :S].float().cpu().numpy()[None]
+    v = Vc[:, :S].float().cpu().numpy()[None]
+    heads = [(0, h) for h in range(HQ)]
+    want = _oracle_heads(q, k, v, heads, rows, D, S, S, HQ, HK, 1)
+    o = O_tok.float().cpu().numpy()
+    worst = max(max_rel_err(o[rows, h], want[(0, h)]) for _, h in heads)
+    print(f"  max err {worst:.2e}", flush=True)
+    assert worst <= tolerance(dtype)
+
+
+# ---- BASELINE config 3 at full size: every head of batches 0 and 3 -------------------------------
+
+def test_prefill_config3_subsample_every_head_of_batches_0_and_3():
+    # B4 H32 S8192 D128 causal bf16 N(0,1); rows 0..127, 4095, 8191 and 256 seeded random rows.
+    B, H, S, D = 4, 32, 8192, 128
+    cfg = cdna4.PrefillCfg(D, S, S, H, H, B, 1)
+    plan = cdna4.prefill_plan(cfg, torch.bfloat16)
+    print(f"config 3 -> {plan.name} (grid {plan.grid})", flush=True)
+    assert plan.name == "fa_mfma_8w"
+    g = torch.Generator(device=DEV).manual_seed(2024)
+    Q = _randn((B, H, S, D), torch.bfloat16, g)
+    K = _randn((B, H, S, D), torch.bfloat16, g)
+    V = _randn((B, H, S, D), torch.bfloat16, g)
+    O = torch.full_like(Q, float("nan"))
+    cdna4.prefill(Q, K, V, O, cfg)
+    torch.cuda.synchronize()
+    assert torch.isfinite(O.float()).all()
+    rows = sorted(set(range(128)) | {4095, 8191} | set(int(r) for r in oracle.integers(77, 256, 0, S - 1)))
+    worst = 0.0
+    for b in (0, 3):
+        q, k, v = (T[b:b + 1].float().cpu().numpy() for T in (Q, K, V))
+        want = _oracle_heads(q, k, v, [(0, h) for h in range(H)], rows, D, S, S, H, H, 1)
+        o = O[b].float().cpu().numpy()
+        worst = max(worst, max(max_rel_err(o[h, rows], want[(0, h)]) for h in range(H)))
+        print(f"  batch {b}: max err so far {worst:.2e}", flush=True)
+    assert worst <= tolerance(torch.bfloat16)
+
+
+# ---- decode: split-K grid (decode_mfma + decode_merge) and the one-launch plan --------------------
+
+def check_decode(D, N, HQ, HK, B, dtype, kernel, stride=0, seed=7, workspace="auto"):
+    st = stride or N
+    cfg = cdna4.DecodeCfg(D, N, HQ, HK, B, stride)
+    plan = cdna4.decode_plan(cfg, dtype, with_workspace=workspace is not None)
+    print(f"decode D{D} N{N} stride{st} {HQ}/{HK} B{B} {dtype} ws={workspace is not None} -> {plan.name} "
+          f"(P {plan.partials}, keys/split {plan.rows})", flush=True)
+    assert plan.name == kernel
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    q = _randn((B, HQ, D), dtype, g)
+    K = _randn((B, HK, st, D), dtype, g)
+    V = _randn((B, HK, st, D), dtype, g)
+    o = torch.full_like(q, float("nan"))
+    cdna4.decode(q, K, V, o, cfg, workspace=workspace)
+    torch.cuda.synchronize()
+    want = oracle.decode(q.float().cpu().numpy(), K.float().cpu().numpy(), V.float().cpu().numpy(), D, N, HQ, HK,
+                         B, stride)
+    err = max_rel_err(o.float().cpu().numpy(), want)
+    print(f"  max err {err:.2e}", flush=True)
+    assert err <= tolerance(dtype)
+    return plan
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_split_strided_cache(dtype):
+    # decode_dme's cache layout [nKVH][stride_kv][D] with stride_kv > N (the runtime's long-context
+    # decode), N not a multiple of the 32-key chunk.
+    check_decode(128, 5000, 32, 8, 2, dtype, "decode_split", stride=8192)
+
+
+@pytest.mark.parametrize("HQ,HK", [(8, 8), (64, 8), (32, 1), (40, 2)])
+def test_decode_split_gqa_groups(HQ, HK):
+    # G = 1, 8, 32 (two 16-head column blocks per kv head) and 20 (a partial second block).
+    check_decode(128, 4096, HQ, HK, 2, torch.float16, "decode_split", seed=HQ)
+
+
+def test_decode_split_d64_ragged():
+    check_decode(64, 4097, 12, 4, 3, torch.float16, "decode_split")
+
+
+def test_decode_split_n8191():
+    check_decode(128, 8191, 32, 8, 1, torch.bfloat16, "decode_split")
+
+
+def test_decode_split_more_than_64_partials():
+    # batch 1 with one kv head: P > 64, so the merge runs several 64-partial passes.
+    plan = check_decode(128, 65536, 4, 1, 1, torch.float16, "decode_split", seed=3)
+    assert plan.partials > 64
+
+
+@pytest.mark.parametrize("N,HQ,HK,B", [(8192, 32, 8, 1), (3000, 40, 2, 2), (4097, 12, 12, 1)])
+def test_decode_without_workspace_one_launch(N, HQ, HK, B):
+    # The reference launchers' contract: no workspace, one launch, any cache length.
+    D = 64 if HQ == 12 else 128
+    check_decode(D, N, HQ, HK, B, torch.float16, "decode_wg", workspace=None)
+
+
+def test_decode_without_workspace_strided():
+    check_decode(128, 1500, 32, 8, 2, torch.bfloat16, "decode_wg", stride=2048, workspace=None)
+
+
+def test_decode_two_streams_with_different_inputs():
+    # Calls on two streams at once, each with its own inputs: split-K calls with workspaces from
+    # torch's allocator on their streams, and workspace-less calls. Every output is checked.
+    D, N, HQ, HK = 128, 6000, 32, 8
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    cases = []
+    for i, s in enumerate(streams):
+        g = torch.Generator(device=DEV).manual_seed(100 + i)
+        with torch.cuda.stream(s):
+            q = _randn((1, HQ, D), torch.float16, g)
+            K = _randn((1, HK, N, D), torch.float16, g)
+            V = _randn((1, HK, N, D), torch.float16, g)
+        cases.append((s, q, K, V))
+    torch.cuda.synchronize()
+    cfg = cdna4.DecodeCfg(D, N, HQ, HK, 1)
+    outs = {}
+    for rep in range(4):
+        for i, (s, q, K, V) in enumerate(cases):
+            with torch.cuda.stream(s):
+                o_ws = torch.empty_like(q)
+                o_nows = torch.empty_like(q)
+                cdna4.decode(q, K, V, o_ws, cfg)
+                cdna4.decode(q, K, V, o_nows, cfg, workspace=None)
+                outs[(rep, i)] = (o_ws, o_nows)
+    torch.cuda.synchronize()
+    for i, (s, q, K, V) in enumerate(cases):
+        want = oracle.decode(q.float().cpu().numpy(), K.float().cpu().numpy(), V.float().cpu().numpy(), D, N, HQ,
+                             HK)
+        for rep in range(4):
+            for o in outs[(rep, i)]:
+                assert max_rel_err(o.float().cpu().numpy(), want) <= tolerance(torch.float16)
