@@ -36,7 +36,8 @@ __all__ = [
     "scan_inclusive", "scan_workspace_size", "rmsnorm_f32", "layernorm_f32", "rope_f16",
     "rope_table_f32", "flash_attn", "flash_attn_decode", "CDNA4Error", "PrefillStrides", "prefill_strided",
     "scatter_kv_f16", "repack_f16", "rope_append_kv_f16", "ModelCfg", "GenerateCfg", "Session",
-    "PlanInfo", "prefill_plan", "decode_plan", "scan_status", "KERNEL_NAMES",
+    "PlanInfo", "prefill_plan", "decode_plan", "scan_status", "KERNEL_NAMES", "decode_noalloc",
+    "decode_noalloc_max_bytes",
 ]
 
 # Element types and operators (include/cdna4_attn.h).
@@ -132,6 +133,8 @@ def _declare(l: ctypes.CDLL) -> None:
                                                ctypes.POINTER(PrefillStrides), c_int, vp]),
         "cdna3_attn_decode_workspace_size": (c_size, [ctypes.POINTER(DecodeCfg)]),
         "cdna3_attn_decode": (c_int, [vp, vp, vp, vp, ctypes.POINTER(DecodeCfg), c_int, vp, c_size, vp]),
+        "cdna3_attn_decode_noalloc": (c_int, [vp, vp, vp, vp, ctypes.POINTER(DecodeCfg), c_int, vp]),
+        "cdna3_attn_decode_noalloc_max_bytes": (c_size, []),
         "cdna3_attn_prefill_plan": (c_int, [ctypes.POINTER(PrefillCfg), c_int, ctypes.POINTER(PlanInfo)]),
         "cdna3_attn_decode_plan": (c_int, [ctypes.POINTER(DecodeCfg), c_int, c_int, ctypes.POINTER(PlanInfo)]),
         "cdna3_scan_status": (c_int, [vp, ctypes.POINTER(c_int), vp]),
@@ -280,6 +283,27 @@ def decode(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, o: torch.Tensor, c
         ws_bytes = workspace.numel() * workspace.element_size()
     _check(lib().cdna3_attn_decode(_ptr(q), _ptr(K), _ptr(V), _ptr(o), ctypes.byref(cfg), dt, _ptr(workspace),
                                    ws_bytes, _stream(stream)), "cdna3_attn_decode")
+
+
+def decode_noalloc(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, o: torch.Tensor, cfg: DecodeCfg,
+                   stream=None) -> None:
+    """cdna3_attn_decode_noalloc: the split-K decode with its partials in the library's static
+    per-GPU scratch array; allocates nothing. Calls that overlap on one GPU race (serialise them)."""
+    _dev(q, K, V, o)
+    dt = _dtype(q)
+    if not (K.dtype == V.dtype == o.dtype == q.dtype):
+        raise ValueError("q, K, V, o must share one dtype")
+    stride = cfg.stride_kv or cfg.N
+    if q.numel() < cfg.batch * cfg.nQHeads * cfg.D or o.numel() < cfg.batch * cfg.nQHeads * cfg.D:
+        raise ValueError("q/o smaller than the configuration")
+    if min(K.numel(), V.numel()) < cfg.batch * cfg.nKVHeads * stride * cfg.D:
+        raise ValueError("K/V smaller than the configuration")
+    _check(lib().cdna3_attn_decode_noalloc(_ptr(q), _ptr(K), _ptr(V), _ptr(o), ctypes.byref(cfg), dt,
+                                           _stream(stream)), "cdna3_attn_decode_noalloc")
+
+
+def decode_noalloc_max_bytes() -> int:
+    return int(lib().cdna3_attn_decode_noalloc_max_bytes())
 
 
 def prefill_plan(cfg: PrefillCfg, dtype=BF16) -> PlanInfo:

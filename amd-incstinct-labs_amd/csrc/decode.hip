@@ -18,6 +18,7 @@
 //     denominator formed by the wave butterfly.
 #include "attn_tile.hpp"
 #include "attn_stream.hpp"
+#include <atomic>
 #include <math.h>
 
 namespace cdna4 {
@@ -345,6 +346,37 @@ int run_decode(const cdna3_decode_cfg& c, const Plan& p, const void* q, const vo
     return bf ? launch_decode<64, true>(c, p, q, K, V, o, ws, s) : launch_decode<64, false>(c, p, q, K, V, o, ws, s);
 }
 
+// ---- allocation-free entry point: split-K partials in a static device array --------------------
+//
+// For callers that cannot allocate (code under graph capture that must not call hipMalloc, tight
+// serving loops): the split-K partials of cdna3_attn_decode_noalloc live in this file-scope array,
+// one copy per GPU, held until the process ends. Host code never passes `scratch` itself (its
+// host-side name is not a device address); it passes the address hipGetSymbolAddress returns for
+// the current device, looked up once per device. The partials are written before they are read,
+// so nothing needs clearing between calls.
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxScratchDevices];
+
+int scratch_address(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxScratchDevices) return CDNA4_ERR_INVALID_VALUE;
+    void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        // Two threads may race here on first use; both obtain the same address.
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (p == nullptr) return CDNA4_ERR_INVALID_VALUE;
+        g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return 0;
+}
+
 }  // namespace
 
 // Plan identity for replayed launches: two cache lengths with the same key launch the same grid
@@ -401,4 +433,21 @@ extern "C" int cdna3_attn_decode_plan(const cdna3_decode_cfg* cfg, int dtype, in
     out->grid = (long long)p.P * cfg->nKVHeads * p.HB * cfg->batch;
     out->workspace = p.wg ? 0 : p.ws_bytes + 256;
     return 0;
+}
+
+extern "C" size_t cdna3_attn_decode_noalloc_max_bytes(void) { return kScratchBytes; }
+
+extern "C" int cdna3_attn_decode_noalloc(const void* q, const void* K, const void* V, void* o,
+                                         const cdna3_decode_cfg* cfg, int dtype, cdna4_stream_t stream) {
+    Plan p;
+    if (!cfg || !plan_decode(*cfg, true, p)) return CDNA4_ERR_INVALID_VALUE;
+    if (int e = check_decode_args(q, K, V, o, dtype)) return e;
+    const size_t need = p.wg ? 0 : p.ws_bytes + 256;
+    if (need > kScratchBytes) return CDNA4_ERR_SCRATCH_TOO_SMALL;
+    if (int e = check_device()) return e;
+    void* ws = nullptr;
+    if (!p.wg) {
+        if (int e = scratch_address(&ws)) return e;
+    }
+    return run_decode(*cfg, p, q, K, V, o, dtype, ws, (hipStream_t)stream);
 }

@@ -32,6 +32,8 @@ typedef struct ihipStream_t* cdna4_stream_t;
 enum {
     CDNA4_OK = 0,
     CDNA4_ERR_INVALID_VALUE = 1,
+    CDNA4_ERR_SCRATCH_TOO_SMALL = 2,   /* hipErrorOutOfMemory: the call needs more than the
+                                          static scratch of cdna3_attn_decode_noalloc holds */
     CDNA4_ERR_INVALID_DEVICE_FUNCTION = 98
 };
 
@@ -134,6 +136,21 @@ size_t cdna3_attn_decode_workspace_size(const cdna3_decode_cfg* cfg);
 int cdna3_attn_decode(const void* q, const void* K, const void* V, void* o,
                       const cdna3_decode_cfg* cfg, int dtype,
                       void* workspace, size_t ws_bytes, cdna4_stream_t stream);
+
+/*
+ * cdna3_attn_decode_noalloc: no counterpart in the reference. For callers that cannot allocate
+ * (code under HIP graph capture that must not call hipMalloc, tight serving loops, harnesses that
+ * forbid allocation): the split-K computation of cdna3_attn_decode with a workspace, with its
+ * partials in a static device array of the library (cdna3_attn_decode_noalloc_max_bytes(), 16 MiB
+ * per GPU, held until the process ends) instead of a caller's workspace. The caller passes only
+ * q, K, V and o; the call never allocates. Returns CDNA4_ERR_SCRATCH_TOO_SMALL when the plan's
+ * partials (cdna3_attn_decode_workspace_size(cfg)) exceed the array. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (concurrent streams, or host threads launching
+ * on different streams) race and must be serialised by the caller.
+ */
+size_t cdna3_attn_decode_noalloc_max_bytes(void);
+int cdna3_attn_decode_noalloc(const void* q, const void* K, const void* V, void* o,
+                              const cdna3_decode_cfg* cfg, int dtype, cdna4_stream_t stream);
 
 /* ---- kernel plans (introspection) ---------------------------------------------
  * No counterpart in the reference (its launchers had one kernel each). Report which kernel a
