@@ -138,6 +138,10 @@ def _declare(l: ctypes.CDLL) -> None:
         "cdna3_attn_prefill_plan": (c_int, [ctypes.POINTER(PrefillCfg), c_int, ctypes.POINTER(PlanInfo)]),
         "cdna3_attn_decode_plan": (c_int, [ctypes.POINTER(DecodeCfg), c_int, c_int, ctypes.POINTER(PlanInfo)]),
         "cdna3_scan_status": (c_int, [vp, ctypes.POINTER(c_int), vp]),
+        "cdna3_model_load": (c_int, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+        "cdna3_model_free": (None, [vp]),
+        "cdna3_model_config": (c_int, [vp, vp]),
+        "cdna3_model_weights_get": (c_int, [vp, vp]),
         "cdna3_reduce_workspace_size": (c_size, [c_size, c_int]),
         "cdna3_reduce": (c_int, [c_int, c_int, vp, c_size, vp, vp, c_size, vp]),
         "cdna3_scan_workspace_size": (c_size, [c_size, c_int]),

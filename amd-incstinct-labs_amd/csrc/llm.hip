@@ -168,8 +168,8 @@ __global__ __launch_bounds__(256) void norm_cast(const float* __restrict__ X, co
 //   kSiluMul   x = norm(hidden) rounded to fp16; rows n (gate) and F + n (up):
 //              act16[n] = fp16(silu(y_gate) * y_up)
 //   kLogits    x = final norm(hidden) in fp32 (unrounded, as the reference's lm_head reads it);
-//              rows 2u, 2u + 1: logits[r] = y, and the wave's (max, first index) pair goes to
-//              the argmax partials
+//              rows 2u, 2u + 1: logits[r] = fp16(y) (the reference's fp16 logits store), and the
+//              wave's best (value, index) key goes to the argmax partials
 enum GemvKind { kQKV = 0, kSiluMul = 1, kLogits = 2 };
 
 struct GemvArgs {
@@ -193,11 +193,23 @@ struct GemvArgs {
     unsigned long long* partial;   // one (orderable value, ~index) key per wave
 };
 
-// Orderable 64-bit key of (value, index): a larger value wins, then a smaller index.
+// Orderable 64-bit key of (value, index) that reproduces the reference's greedy choice
+// (argmax_kernel, cdna3-prims/include/cdna3/runtime/forward.hpp:244-262): 256 threads each keep the
+// first strict maximum of the indices t, t + 256, ..., then a tree merges thread t + s into t for
+// s = 128, 64, ..., 1, keeping t on ties. Among equal values, thread t therefore wins over every
+// tied thread whose index, bit-reversed over 8 bits, is larger; within a thread the smaller index
+// wins. The key orders a larger value first, then the smaller (bitrev8(i % 256), i / 256), stored
+// complemented in the low word.
+__device__ __forceinline__ uint32_t bitrev8(uint32_t x) { return __builtin_bitreverse32(x) >> 24; }
 __device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
     uint32_t u = __builtin_bit_cast(uint32_t, v);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)u << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
+    const uint32_t ord = bitrev8((uint32_t)i & 255u) << 24 | ((uint32_t)i >> 8);
+    return ((unsigned long long)u << 32) | (uint32_t)(0xffffffffu - ord);
+}
+__device__ __forceinline__ int argmax_index(uint32_t low_word) {
+    const uint32_t ord = 0xffffffffu - low_word;
+    return (int)((ord & 0xffffffu) * 256u + bitrev8(ord >> 24));
 }
 
 // Rows (r0, r1) of row pair p of a GEMV kind (see above).
@@ -286,13 +298,16 @@ __global__ __launch_bounds__(256) void gemv2(GemvArgs a) {
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
             if (unit * NP + p >= a.pairs) continue;
-            lg[r0[p]] = y0[p];
-            if (r1[p] != r0[p]) lg[r1[p]] = y1[p];
-            const unsigned long long k0 = argmax_key(y0[p], r0[p]), k1 = argmax_key(y1[p], r1[p]);
+            // The reference stores the logits as fp16 (gemm_f32in_f16out_kernel) and takes the
+            // argmax of those values.
+            const float v0 = (float)(_Float16)y0[p], v1 = (float)(_Float16)y1[p];
+            lg[r0[p]] = v0;
+            if (r1[p] != r0[p]) lg[r1[p]] = v1;
+            const unsigned long long k0 = argmax_key(v0, r0[p]), k1 = argmax_key(v1, r1[p]);
             const unsigned long long k = k0 > k1 ? k0 : k1;
             best = k > best ? k : best;
         }
-        a.partial[unit] = best;   // the wave's (max, first index) key for the argmax
+        a.partial[unit] = best;   // the wave's best (value, index) key for the argmax
         return;
     }
 #pragma unroll
@@ -409,7 +424,7 @@ __global__ __launch_bounds__(1024) void argmax_keys(const unsigned long long* __
     }
     const uint32_t h2 = (uint32_t)allreduce((int)(hi ^ 0x80000000u), Max{}) ^ 0x80000000u;
     const uint32_t l2 = (uint32_t)allreduce((int)((hi == h2 ? lo : 0u) ^ 0x80000000u), Max{}) ^ 0x80000000u;
-    const int tok = (int)(0xffffffffu - l2);
+    const int tok = argmax_index(l2);
     if (threadIdx.x == 0) {
         ids[0] = tok;
         if (state) step = state[1];

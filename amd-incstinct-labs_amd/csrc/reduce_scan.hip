@@ -12,6 +12,8 @@
 //           a time (one per lane) and writes the output. A small fill kernel clears the
 //           tile flags first.
 #include "common.hpp"
+#include <stdlib.h>
+#include "scan_layout.hpp"
 #include "wave_primitives/detail/xlane.hpp"
 
 namespace cdna4 {
@@ -220,9 +222,21 @@ struct ScanState {
     uint64_t* agg;    // per tile: NW words
     uint64_t* pre;    // per tile: NW words
     uint32_t* error;  // set when a look-back wait exceeds its bound
+    uint32_t spin_limit;   // sleeps a look-back waits for a predecessor before it gives up
 };
 
 constexpr uint32_t kSpinLimit = 1u << 22;
+
+// The look-back's wait bound: kSpinLimit, or CDNA4_SCAN_SPIN_LIMIT from the environment when set
+// (read on every call), so a test can force the timeout path from the host with a tiny bound while
+// every kernel still runs to completion.
+uint32_t scan_spin_limit() {
+    const char* e = getenv("CDNA4_SCAN_SPIN_LIMIT");
+    if (!e || !*e) return kSpinLimit;
+    char* end = nullptr;
+    const unsigned long v = strtoul(e, &end, 10);
+    return (end && *end == 0 && v <= kSpinLimit) ? (uint32_t)v : kSpinLimit;
+}
 constexpr uint64_t kTagAgg = 1, kTagPre = 2;
 
 template <typename Acc> struct Words { static constexpr int NW = sizeof(Acc) / 4; };
@@ -257,7 +271,7 @@ __device__ __forceinline__ void publish(uint64_t* slots, size_t t, Acc v, uint64
     if (lane < (unsigned)NW) {
         const uint64_t bits = to_bits(v);
         const uint32_t half = (uint32_t)(lane == 0 ? bits : bits >> 32);
-        st_word(slots + t * NW + lane, (tag << 32) | half);
+        st_word(slots + scan_layout::slot_word(t, NW, lane), (tag << 32) | half);
     }
 }
 
@@ -265,11 +279,11 @@ __device__ __forceinline__ void publish(uint64_t* slots, size_t t, Acc v, uint64
 template <typename Acc>
 __device__ __forceinline__ bool read_slot(const uint64_t* slots, long long t, uint64_t tag, Acc& v) {
     constexpr int NW = Words<Acc>::NW;
-    const uint64_t w0 = ld_word(slots + t * NW);
+    const uint64_t w0 = ld_word(slots + scan_layout::slot_word((size_t)t, NW, 0));
     uint64_t bits = (uint32_t)w0;
     bool ok = (w0 >> 32) == tag;
     if constexpr (NW == 2) {
-        const uint64_t w1 = ld_word(slots + t * NW + 1);
+        const uint64_t w1 = ld_word(slots + scan_layout::slot_word((size_t)t, NW, 1));
         ok = ok && (w1 >> 32) == tag;
         bits |= (uint64_t)(uint32_t)w1 << 32;
     }
@@ -302,7 +316,7 @@ __device__ Acc look_back(const ScanState& st, size_t tile, Op op) {
             mzero = __ballot(s == 0u);
             const uint64_t below = mpre ? ((mpre & (~mpre + 1ull)) - 1ull) : ~0ull;  // lanes before first prefix
             if ((mzero & below) == 0ull) break;
-            if (spin >= kSpinLimit) {
+            if (spin >= st.spin_limit) {
                 if (lane == 0) __hip_atomic_store(st.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
@@ -325,14 +339,14 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
     using Out = typename E::Out;
     constexpr int VEC = E::VEC;
     constexpr int U = scan_u<DT, kVec>();
-    constexpr size_t TILE = (size_t)64 * VEC * U;
+    constexpr size_t TILE = scan_layout::tile_elems(VEC, U);
     const typename E::In* in = (const typename E::In*)in_;
     Out* out = (Out*)out_;
     Op op;
     const Acc id = Op::template identity<Acc>();
     const unsigned lane = threadIdx.x;
     const size_t tile = blockIdx.x;
-    const size_t base = tile * TILE;
+    const size_t base = scan_layout::tile_base(tile, TILE);
 
     // Aligned calls (kVec): n counts the elements of whole VEC-element vectors only (the host
     // scans the remaining n % VEC elements in scan_tail). Every tile but the last is full and
@@ -340,8 +354,8 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
     // before any arithmetic; the last tile guards each vector with a 32-bit tile-local index against the
     // uniform vector count. Misaligned calls go element by element.
     const typename E::In* tin = in + base;
-    const bool full = kVec && base + TILE <= n;
-    const uint32_t rem = base + TILE <= n ? (uint32_t)TILE : (uint32_t)(n - base);  // elements
+    const bool full = kVec && scan_layout::tile_full(base, TILE, n);
+    const uint32_t rem = scan_layout::tile_rem(base, TILE, n);  // elements
     Acc v[U][VEC];
     if constexpr (kVec) {
         const typename E::Load* src = (const typename E::Load*)tin + lane;
@@ -350,10 +364,9 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
             for (int j = 0; j < U; ++j) E::unpack(__builtin_nontemporal_load(src + j * 64), v[j]);
             __builtin_amdgcn_sched_barrier(0);
         } else {
-            const uint32_t nv = rem / VEC;
 #pragma unroll
             for (int j = 0; j < U; ++j) {
-                if ((uint32_t)j * 64 + lane < nv) {
+                if (scan_layout::vec_live(false, j, lane, rem, VEC)) {
                     E::unpack(__builtin_nontemporal_load(src + j * 64), v[j]);
                 } else {
 #pragma unroll
@@ -366,7 +379,7 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
         for (int j = 0; j < U; ++j)
 #pragma unroll
             for (int e = 0; e < VEC; ++e) {
-                const uint32_t i = ((uint32_t)j * 64 + lane) * VEC + e;
+                const uint32_t i = scan_layout::elem_in_tile(j, lane, e, VEC);
                 v[j][e] = i < rem ? E::load1(tin + i) : id;
             }
     }
@@ -403,10 +416,9 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
     if constexpr (kVec) {
         constexpr int kWords = (int)(sizeof(Out) * VEC / 16);
         u32x4* dst = (u32x4*)tout + lane * kWords;
-        const uint32_t nv = rem / VEC;
 #pragma unroll
         for (int j = 0; j < U; ++j) {
-            if (full || (uint32_t)j * 64 + lane < nv) {
+            if (scan_layout::vec_live(full, j, lane, rem, VEC)) {
                 Out o[VEC];
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) o[e] = (Out)op(excl, v[j][e]);
@@ -423,7 +435,7 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
         for (int j = 0; j < U; ++j)
 #pragma unroll
             for (int e = 0; e < VEC; ++e) {
-                const uint32_t i = ((uint32_t)j * 64 + lane) * VEC + e;
+                const uint32_t i = scan_layout::elem_in_tile(j, lane, e, VEC);
                 if (i < rem) tout[i] = (Out)op(excl, v[j][e]);
             }
     }
@@ -454,8 +466,7 @@ __global__ __launch_bounds__(64) void scan_tail(const void* __restrict__ in_, si
 
 template <int DT, bool kVec>
 size_t scan_tiles_for(size_t n) {
-    const size_t tile = (size_t)64 * ScanElem<DT>::VEC * scan_u<DT, kVec>();
-    return (n + tile - 1) / tile;
+    return scan_layout::tiles_for(n, ScanElem<DT>::VEC, scan_u<DT, kVec>());
 }
 
 // Tile count the workspace is sized for: the misaligned (smaller) tiles', the larger count.
@@ -471,10 +482,9 @@ size_t scan_ntiles(size_t n, int dtype) {
     }
 }
 
-// Workspace layout: [error: u32, padded to 256 B][agg: ntiles x 2 words][pre: ntiles x 2 words]
-// (64-bit values use both words of a tile, 32-bit values the first).
-size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-size_t scan_ws_bytes(size_t ntiles) { return 256 + 2 * align256(ntiles * 16); }
+// Workspace layout (scan_layout.hpp): [error: u32, padded to 256 B][agg: ntiles x 2 words]
+// [pre: ntiles x 2 words] (64-bit values use both words of a tile, 32-bit values the first).
+size_t scan_ws_bytes(size_t ntiles) { return scan_layout::ws_bytes(ntiles); }
 
 template <int DT, class Op>
 int scan_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
@@ -485,15 +495,16 @@ int scan_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
     // 16-byte aligned calls scan the whole vectors in scan_tiles and the last n % VEC elements
     // in scan_tail; misaligned calls scan everything element by element in scan_tiles.
     const bool vec = ((uintptr_t)in % 16) == 0 && ((uintptr_t)out % 16) == 0;
-    const size_t n_main = vec ? n - n % VEC : n;
+    const size_t n_main = scan_layout::main_elems(n, vec, (int)VEC);
     const size_t ntiles = vec ? scan_tiles_for<DT, true>(n_main) : scan_tiles_for<DT, false>(n_main);
     char* w = (char*)ws;
     ScanState st;
     st.error = (uint32_t*)w;
-    st.agg = (uint64_t*)(w + 256);
-    st.pre = (uint64_t*)(w + 256 + align256(ntiles * 16));
+    st.spin_limit = scan_spin_limit();
+    st.agg = (uint64_t*)(w + scan_layout::agg_offset());
+    st.pre = (uint64_t*)(w + scan_layout::pre_offset(ntiles));
     // Both slot arrays are cleared in one pass (the pre array directly follows the agg array).
-    const size_t nwords = (align256(ntiles * 16) + ntiles * Words<Acc>::NW * 8) / 8;
+    const size_t nwords = scan_layout::clear_words(ntiles, Words<Acc>::NW);
     scan_clear<<<(unsigned)(nwords == 0 ? 1 : ceil_div(nwords, 256)), 256, 0, s>>>(st.agg, nwords, st.error);
     if (ntiles > 0) {
         if (vec)

@@ -1,0 +1,51 @@
+// Index and workspace arithmetic of the device-wide scan (reduce_scan.hip), as constexpr functions
+// shared by the kernels, their launcher and a host-side replay (tests/native/scan_layout_check.cpp)
+// that walks every load, store and tile-slot address of every tile for given sizes and checks it
+// against the buffer and workspace sizes. Plain C++: clang compiles constexpr functions for host
+// and device alike.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+namespace cdna4 {
+namespace scan_layout {
+
+constexpr size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// A tile is 64 lanes x U vectors of VEC elements.
+constexpr size_t tile_elems(int vec, int u) { return (size_t)64 * vec * u; }
+constexpr size_t tiles_for(size_t n, int vec, int u) { return (n + tile_elems(vec, u) - 1) / tile_elems(vec, u); }
+
+// Workspace: [error word, padded to 256 B][agg slots: align256(ntiles * 16)][pre slots: ntiles * 16],
+// two 64-bit words per tile and array (one used by 32-bit values).
+constexpr size_t ws_bytes(size_t ntiles) { return 256 + 2 * align256(ntiles * 16); }
+constexpr size_t agg_offset() { return 256; }
+constexpr size_t pre_offset(size_t ntiles) { return 256 + align256(ntiles * 16); }
+// 64-bit words the clear kernel zeroes from the start of the agg array: the whole agg array and
+// the used part of the pre array that follows it.
+constexpr size_t clear_words(size_t ntiles, int nw) { return (align256(ntiles * 16) + ntiles * (size_t)nw * 8) / 8; }
+
+// Aligned calls scan whole VEC-element vectors in the tiles and the last n % VEC elements in a
+// one-wave tail; misaligned calls scan everything element by element.
+constexpr size_t main_elems(size_t n, bool vec, int VEC) { return vec ? n - n % (size_t)VEC : n; }
+
+// Tile t starts at element t * TILE; the elements it covers (TILE, or fewer for the last tile).
+constexpr size_t tile_base(size_t tile, size_t TILE) { return tile * TILE; }
+constexpr bool tile_full(size_t base, size_t TILE, size_t n) { return base + TILE <= n; }
+constexpr uint32_t tile_rem(size_t base, size_t TILE, size_t n) {
+    return base + TILE <= n ? (uint32_t)TILE : (uint32_t)(n - base);
+}
+// Vector j of lane `lane` in a tile: its index among the tile's vectors, and the guard of the last
+// (partial) tile: the vector is read and written only when it lies wholly inside the tile.
+constexpr uint32_t vec_in_tile(int j, unsigned lane) { return (uint32_t)j * 64 + lane; }
+constexpr bool vec_live(bool full, int j, unsigned lane, uint32_t rem, int VEC) {
+    return full || vec_in_tile(j, lane) < rem / (uint32_t)VEC;
+}
+// Element e of vector j of a lane on the element-wise (misaligned) path, and its guard.
+constexpr uint32_t elem_in_tile(int j, unsigned lane, int e, int VEC) { return vec_in_tile(j, lane) * (uint32_t)VEC + e; }
+
+// 64-bit word w of tile t's slot (NW words per slot).
+constexpr size_t slot_word(size_t tile, int nw, unsigned w) { return tile * (size_t)nw + w; }
+
+}  // namespace scan_layout
+}  // namespace cdna4

@@ -547,3 +547,114 @@ extern "C" int cdna3_session_prefill_logits(cdna3_session* s, const int* ids, in
     CK(hipMemcpyAsync(logits, S.logits, (size_t)S.c.vocab_size * 4, hipMemcpyDeviceToHost, S.stream));
     return (int)hipStreamSynchronize(S.stream);
 }
+
+// ---- ModelLoader: the model's tensors as the reference's loader leaves them ------------------------
+// cdna3-prims/include/cdna3/runtime/model_loader.hpp:130-193: meta.json plus one raw fp16 .bin per
+// tensor, each uploaded to its own device buffer under its own name (no concatenation; the session
+// above builds its own fused layout instead). Optional q/k/v biases (qkv_bias) are NULL when absent.
+struct cdna3_model {
+    cdna3_model_cfg c{};
+    std::vector<void*> allocs;
+    std::vector<cdna3_layer_weights> layers;
+    cdna3_model_weights view{};
+
+    void release() {
+        for (void* p : allocs) (void)hipFree(p);
+        allocs.clear();
+    }
+    int upload(const std::string& path, size_t count, void** dst) {
+        std::vector<uint16_t> h;
+        if (!read_f16(path, count, h)) return CDNA4_ERR_INVALID_VALUE;
+        CK(hipMalloc(dst, count * 2 ? count * 2 : 16));
+        allocs.push_back(*dst);
+        CK(hipMemcpy(*dst, h.data(), count * 2, hipMemcpyHostToDevice));
+        return 0;
+    }
+    int load(const std::string& dir) {
+        std::map<std::string, std::string> meta;
+        if (!parse_meta(dir + "/meta.json", meta)) return CDNA4_ERR_INVALID_VALUE;
+        auto geti = [&](const char* k, int def) { return meta.count(k) ? atoi(meta[k].c_str()) : def; };
+        c.n_layers = geti("n_layers", 0);
+        c.hidden = geti("hidden", 0);
+        c.n_heads = geti("n_heads", 0);
+        c.n_kv_heads = geti("n_kv_heads", c.n_heads);
+        c.head_dim = geti("head_dim", c.n_heads ? c.hidden / c.n_heads : 0);
+        c.ffn_dim = geti("ffn_dim", 0);
+        c.vocab_size = geti("vocab_size", 0);
+        c.rope_theta = meta.count("rope_theta") ? (float)atof(meta["rope_theta"].c_str()) : 10000.f;
+        c.qkv_bias = meta.count("qkv_bias") && (meta["qkv_bias"] == "1" || meta["qkv_bias"] == "true");
+        c.layernorm = meta.count("norm") && meta["norm"] == "layernorm";
+        c.norm_eps = meta.count("norm_eps") ? (float)atof(meta["norm_eps"].c_str()) : (c.layernorm ? 1e-5f : 1e-6f);
+        if (c.n_layers < 1 || c.hidden < 1 || c.n_heads < 1 || c.n_kv_heads < 1 || c.head_dim < 1 || c.ffn_dim < 1 ||
+            c.vocab_size < 1)
+            return CDNA4_ERR_INVALID_VALUE;
+        const size_t H = c.hidden, F = c.ffn_dim, V = c.vocab_size;
+        const size_t qd = (size_t)c.n_heads * c.head_dim, kvd = (size_t)c.n_kv_heads * c.head_dim;
+        auto p = [&](const std::string& name) { return dir + "/" + name + ".bin"; };
+        CK(upload(p("embed_tokens"), V * H, &view.embed_tokens));
+        CK(upload(p("lm_head"), V * H, &view.lm_head));
+        CK(upload(p("final_norm"), H, &view.final_norm));
+        layers.assign(c.n_layers, cdna3_layer_weights{});
+        for (int i = 0; i < c.n_layers; ++i) {
+            const std::string lp = "layer_" + std::to_string(i) + "_";
+            cdna3_layer_weights& l = layers[i];
+            CK(upload(p(lp + "q_proj"), qd * H, &l.Wq));
+            CK(upload(p(lp + "k_proj"), kvd * H, &l.Wk));
+            CK(upload(p(lp + "v_proj"), kvd * H, &l.Wv));
+            CK(upload(p(lp + "o_proj"), H * qd, &l.Wo));
+            if (c.qkv_bias) {
+                CK(upload(p(lp + "q_bias"), qd, &l.bq));
+                CK(upload(p(lp + "k_bias"), kvd, &l.bk));
+                CK(upload(p(lp + "v_bias"), kvd, &l.bv));
+            }
+            CK(upload(p(lp + "gate_proj"), F * H, &l.Wgate));
+            CK(upload(p(lp + "up_proj"), F * H, &l.Wup));
+            CK(upload(p(lp + "down_proj"), H * F, &l.Wdown));
+            CK(upload(p(lp + "norm_attn"), H, &l.norm_attn));
+            CK(upload(p(lp + "norm_mlp"), H, &l.norm_mlp));
+        }
+        view.n_layers = c.n_layers;
+        view.layers = layers.data();
+        return 0;
+    }
+};
+
+extern "C" int cdna3_model_load(const char* model_dir, cdna3_model** out) {
+    if (!model_dir || !out) return CDNA4_ERR_INVALID_VALUE;
+    *out = nullptr;
+    cdna3_model* m = nullptr;
+    int e = 0;
+    try {
+        m = new cdna3_model();
+        e = m->load(model_dir);
+    } catch (const std::exception&) {
+        e = (int)hipErrorOutOfMemory;
+    }
+    if (e != 0) {
+        if (m) {
+            m->release();
+            delete m;
+        }
+        return e;
+    }
+    *out = m;
+    return 0;
+}
+
+extern "C" void cdna3_model_free(cdna3_model* m) {
+    if (!m) return;
+    m->release();
+    delete m;
+}
+
+extern "C" int cdna3_model_config(const cdna3_model* m, cdna3_model_cfg* out) {
+    if (!m || !out) return CDNA4_ERR_INVALID_VALUE;
+    *out = m->c;
+    return 0;
+}
+
+extern "C" int cdna3_model_weights_get(const cdna3_model* m, cdna3_model_weights* out) {
+    if (!m || !out) return CDNA4_ERR_INVALID_VALUE;
+    *out = m->view;
+    return 0;
+}

@@ -354,8 +354,12 @@ def bench_dpp(torch, cdna4, steps, warmup):
                                   steps, warmup)
             gbs = n * esize / (ms * 1e-3) / 1e9
             entry[f"reduce_{op}"] = {"GBs": round(gbs, 1), "us": round(ms * 1e3, 2), "frac": round(gbs / PEAK_HBM_GBS, 4)}
-        ms, _ = time_launches(torch, lambda i=0: cdna4.scan_inclusive(xs[i % nbuf], "sum", out=outn, workspace=wsn),
-                              steps, warmup)
+        # Asynchronous calls in the timed region; the look-back status word of the last call is read
+        # once afterwards (cdna3_scan_status) and must be clear.
+        ms, _ = time_launches(torch, lambda i=0: cdna4.scan_inclusive(xs[i % nbuf], "sum", out=outn, workspace=wsn,
+                                                                      check=False), steps, warmup)
+        if cdna4.scan_status(wsn) != 0:
+            raise RuntimeError(f"scan look-back status set ({name})")
         gbs = n * (esize + osize) / (ms * 1e-3) / 1e9
         entry["scan_sum"] = {"GBs": round(gbs, 1), "us": round(ms * 1e3, 2), "frac": round(gbs / PEAK_HBM_GBS, 4)}
         result[name] = entry

@@ -15,16 +15,10 @@
 #include <string>
 #include <vector>
 #include "../../cdna4_attn.h"
+#include "model_config.hpp"
 
 namespace cdna3 {
 namespace runtime {
-
-struct ModelConfig {
-    int n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn_dim, vocab_size;
-    float rope_theta;
-    bool qkv_bias, layernorm;
-    float norm_eps;
-};
 
 struct GenerateCfg {
     int max_new_tokens = 64;
@@ -67,7 +61,7 @@ public:
         return seq;
     }
 
-    // Prefill only: fp32 logits of the last prompt token (session.hpp:298-317).
+    // Prefill only: logits of the last prompt token, fp16 values widened to float (session.hpp:298-317).
     std::vector<float> prefill_logits(const std::vector<int>& input_ids) {
         std::vector<float> logits(config().vocab_size);
         check(cdna3_session_prefill_logits(s_, input_ids.data(), (int)input_ids.size(), logits.data()),

@@ -193,6 +193,8 @@ int cdna3_attn_decode_plan(const cdna3_decode_cfg* cfg, int dtype, int with_work
  * wait ever exceeds that bound the result is not valid and the first 32-bit word of the
  * workspace is set non-zero (each scan call clears it first). cdna3_scan_status synchronises
  * `stream` and returns that word in *status (0 = the last scan on this workspace is valid).
+ * The bound is 2^22 sleeps per wait; CDNA4_SCAN_SPIN_LIMIT in the environment (read on every
+ * call) lowers it, so that tests can force the timeout path.
  */
 size_t cdna3_reduce_workspace_size(size_t n, int dtype);
 int cdna3_reduce(int op, int dtype, const void* in, size_t n, void* out,
@@ -261,8 +263,10 @@ int cdna3_rope_append_kv_f16(const void* q, const void* k, const void* v, void* 
  * LayerNorm (eps 1e-5) instead of RMSNorm (eps 1e-6), with optional *_norm_*_bias /
  * final_norm_bias tensors as beta; "norm_eps" overrides eps.
  * Numerics follow the reference: fp32 residual stream, fp16 activations into each projection
- * with fp32 accumulation, fp16 Q/K/V and KV cache, fp32 SiLU product; logits are kept in fp32
- * and argmax takes the first index of the maximum.
+ * with fp32 accumulation, fp16 Q/K/V and KV cache, fp32 SiLU product; logits are accumulated in
+ * fp32 and stored as fp16 (returned widened to fp32), and the greedy argmax breaks ties as the
+ * reference's argmax_kernel does (forward.hpp:244-262: the smallest index mod 256, then the
+ * smallest index).
  * The session owns one HIP stream, a rocBLAS handle, the weights and the KV cache
  * [layers][n_kv_heads][max_seq][head_dim]. Calls on one session must not overlap.
  */
@@ -287,17 +291,46 @@ int cdna3_session_config(const cdna3_session* session, cdna3_model_cfg* out);
  * the generated tokens only (the reference returns the prompt followed by them) to out_tokens
  * (room for max_new_tokens) and their count to *n_out. Stops after an eos_token_id (>= 0) has
  * been produced, or when the cache is full (n_ids + steps == max_seq), as the reference does.
- * Optional outputs (NULL to skip): step_logits, host [max_new_tokens][vocab] fp32 logits of each
+ * Optional outputs (NULL to skip): step_logits, host [max_new_tokens][vocab] logits (fp16 values as fp32) of each
  * step; ttft_ms, device time from the prompt upload to the first token; decode_ms, device time
  * of the remaining steps. Invalid: n_ids < 1 or > max_seq, ids out of [0, vocab). */
 int cdna3_session_generate(cdna3_session* session, const int* ids, int n_ids, int max_new_tokens,
                            int eos_token_id, int* out_tokens, int* n_out, float* step_logits,
                            float* ttft_ms, float* decode_ms);
 
-/* Session::prefill_logits (session.hpp:298-317): prefill only; host fp32 logits [vocab] of the
- * last prompt token. */
+/* Session::prefill_logits (session.hpp:298-317): prefill only; host logits [vocab] of the last
+ * prompt token (the fp16 values, widened to fp32, as the reference returns them). */
 int cdna3_session_prefill_logits(cdna3_session* session, const int* ids, int n_ids,
                                  float* logits);
+
+/* ---- model loader ----------------------------------------------------------------
+ * Replaces cdna3::runtime::ModelLoader (cdna3-prims/include/cdna3/runtime/model_loader.hpp:
+ * 130-193): reads the same directory format as cdna3_session_create and uploads every tensor to
+ * its own fp16 device buffer on the current device, under the reference's names (q/k/v biases
+ * NULL unless qkv_bias). The buffers stay valid until cdna3_model_free. Invalid: unreadable
+ * meta.json, non-positive sizes, missing or short tensor files.
+ */
+typedef struct cdna3_model cdna3_model;
+
+typedef struct {
+    void *Wq, *Wk, *Wv, *Wo;     /* [n_heads*head_dim][hidden], [n_kv*hd][hidden] x2, [hidden][n_heads*hd] */
+    void *bq, *bk, *bv;          /* NULL without qkv_bias */
+    void *Wgate, *Wup, *Wdown;   /* [ffn][hidden] x2, [hidden][ffn] */
+    void *norm_attn, *norm_mlp;  /* [hidden] */
+} cdna3_layer_weights;
+
+typedef struct {
+    void* embed_tokens;                 /* [vocab][hidden] */
+    void* lm_head;                      /* [vocab][hidden] */
+    void* final_norm;                   /* [hidden] */
+    int n_layers;
+    const cdna3_layer_weights* layers;  /* n_layers entries, owned by the model */
+} cdna3_model_weights;
+
+int cdna3_model_load(const char* model_dir, cdna3_model** out);
+void cdna3_model_free(cdna3_model* model);
+int cdna3_model_config(const cdna3_model* model, cdna3_model_cfg* out);
+int cdna3_model_weights_get(const cdna3_model* model, cdna3_model_weights* out);
 
 #ifdef __cplusplus
 }

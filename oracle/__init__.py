@@ -296,6 +296,29 @@ class _OrcLLM(ctypes.Structure):
                                   "n2b")]
 
 
+def reference_argmax(logits) -> int:
+    """argmax_kernel (cdna3-prims/include/cdna3/runtime/forward.hpp:244-262), one block of 256
+    threads, restated step by step: thread t keeps the first strictly larger value of logits[t],
+    logits[t + 256], ... starting from -1e30 (index 0), then a tree over the threads in which the
+    right partner replaces the left only when strictly larger (strides 128, 64, ..., 1)."""
+    x = np.ascontiguousarray(logits, np.float32).reshape(-1)
+    bv = np.full(256, np.float32(-1e30), np.float32)
+    bi = np.zeros(256, np.int64)
+    for t in range(min(256, x.size)):
+        col = x[t::256]
+        run = np.maximum.accumulate(col)
+        first = int(np.argmax(col == run[-1]))          # first index of the column maximum
+        if run[-1] > bv[t]:
+            bv[t], bi[t] = run[-1], t + 256 * first
+    s = 128
+    while s > 0:
+        for t in range(s):
+            if bv[t + s] > bv[t]:
+                bv[t], bi[t] = bv[t + s], bi[t + s]
+        s //= 2
+    return int(bi[0])
+
+
 class LLM:
     """CPU forward of the runtime's decoder (llm.c: Session::run_layers with the reference's
     rounding points). `meta` and `tensors` are a model directory's meta.json dict and its fp16
@@ -346,7 +369,8 @@ class LLM:
         self.pos = 0
 
     def forward(self, ids, all_logits: bool = False) -> np.ndarray:
-        """Runs ids at the next cache positions; fp32 logits [T][vocab] (all_logits) or [vocab]."""
+        """Runs ids at the next cache positions; logits [T][vocab] (all_logits) or [vocab], fp32
+        arrays holding the fp16 values the reference stores."""
         ids = np.ascontiguousarray(np.asarray(ids, np.int32).reshape(-1))
         T = ids.size
         out = np.empty((T if all_logits else 1) * self.vocab, np.float32)
@@ -358,9 +382,10 @@ class LLM:
         return out.reshape(T, self.vocab) if all_logits else out
 
     def greedy(self, ids, max_new_tokens: int) -> list:
-        """Session::generate's loop on the CPU (first index of the maximum on ties)."""
+        """Session::generate's loop on the CPU (session.hpp:262-296), greedy_from_last's argmax as
+        the reference breaks ties (reference_argmax)."""
         self.reset()
-        toks = [int(np.argmax(self.forward(ids)))]
+        toks = [reference_argmax(self.forward(ids))]
         while len(toks) < max_new_tokens and self.pos < self.max_seq:
-            toks.append(int(np.argmax(self.forward([toks[-1]]))))
+            toks.append(reference_argmax(self.forward([toks[-1]])))
         return toks

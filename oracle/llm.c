@@ -18,9 +18,10 @@
  *     MLP                 gate/up f32 (:112-141), silu_mul_f32_kernel (forward.hpp:154-160), f16
  *                         cast, down f32, residual
  *     final norm          fp32 (session.hpp:233-236)
- *   greedy_from_last      session.hpp:320-331: logits = final-norm(hidden) . lm_head^T in fp32
- *                         from the fp32 normed row (gemm_f32in_f16out_kernel, forward.hpp:70-86);
- *                         the reference's fp16 store of the logits is not modelled.
+ *   greedy_from_last      session.hpp:320-331: logits = final-norm(hidden) . lm_head^T, fp32
+ *                         accumulation from the fp32 normed row, stored as fp16
+ *                         (gemm_f32in_f16out_kernel, forward.hpp:70-86); the argmax over them
+ *                         (argmax_kernel, forward.hpp:244-262) is restated in oracle/__init__.py.
  * Extension (no reference counterpart): "layernorm" models use the two-pass LayerNorm of
  * research/wave-primitives/benchmarks/bench_layernorm.hip:51-114 (eps 1e-5) with f16 gamma/beta.
  * The embedding row is widened to fp32 (embed_gather_f32_kernel, forward.hpp:174-183).
@@ -199,6 +200,7 @@ int orc_llm_forward(const orc_llm* m, const int* ids, int T, int pos0, uint16_t*
         const int nt = T - t0;
         norm_rows(m, h + (size_t)t0 * H, m->fnorm, m->fnorm_b, xn, nt);
         matvec_rows(xn, nt, m->lm_head, V, H, logits);
+        for (size_t i = 0; i < (size_t)nt * V; ++i) logits[i] = r16(logits[i]);   /* the fp16 logits store */
     }
 out:
     free(h); free(xn); free(q); free(k); free(v); free(att); free(g); free(u); free(y);

@@ -55,6 +55,10 @@ def hooks() -> ctypes.CDLL:
         l.hook_ballot.argtypes = [vp, vp, ctypes.c_int, vp]
         l.hook_mfma.argtypes = [ctypes.c_int, vp, vp, vp, vp]
         l.hook_dme.argtypes = [vp] * 7
+        l.hook_dme_forms.argtypes = [vp] * 6 + [ctypes.c_int, vp]
+        l.hook_online_softmax.argtypes = [vp, vp, ctypes.c_int, vp, vp]
+        l.hook_mma_tile.argtypes = [ctypes.c_int, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp]
+        l.hook_runtime_kernels.argtypes = [ctypes.c_int, vp, vp, vp, vp] + [ctypes.c_int] * 5 + [ctypes.c_float, vp]
         _HOOKS = l
     return _HOOKS
 

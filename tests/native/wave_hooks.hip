@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <cdna3/cdna3.hpp>
 #include <cdna3/examples/fused_softmax.hpp>
+#include <cdna3/examples/async_tiled_gemm.hpp>
+#include <cdna3/runtime/forward.hpp>
 #include <stdint.h>
 
 namespace {
@@ -188,5 +190,134 @@ extern "C" int hook_dme(const void* src, void* dst, const float* fsrc, float* fd
                         void* stream) {
     dme_kernel<<<1, 64, 0, (hipStream_t)stream>>>((const uint8_t*)src, (uint8_t*)dst, fsrc, fdst, (const __half*)hsrc,
                                                   (__half*)hdst);
+    return (int)hipGetLastError();
+}
+
+// ---- dme forms the reference's kernels call -------------------------------------------------
+// One wave: copy_element / copy_element_stream of lane L's float into tile[L] (the documented
+// per-lane form), copy_tile_1d_stream of 256 floats; each tile copied back out.
+__global__ void dme_elem_kernel(const float* __restrict__ src, float* __restrict__ out) {
+    __shared__ __attribute__((aligned(16))) float t0[64];
+    __shared__ __attribute__((aligned(16))) float t1[64];
+    __shared__ __attribute__((aligned(16))) float t2[256];
+    const int L = threadIdx.x;
+    dme::copy_element(src + L, &t0[L]);
+    dme::copy_element_stream(src + 64 + L, &t1[L]);
+    dme::copy_tile_1d_stream<float, 256>(src + 128, t2);
+    dme::wait();
+    __syncthreads();
+    out[L] = t0[L];
+    out[64 + L] = t1[L];
+    for (int i = L; i < 256; i += 64) out[128 + i] = t2[i];
+}
+
+// Two waves: prefetch_tile2d_fp16<32, 64> of one packed tile.
+__global__ void dme_tile2d_kernel(const __half* __restrict__ src, __half* __restrict__ out) {
+    __shared__ __attribute__((aligned(16))) __half tile[32 * 64];
+    dme::prefetch_tile2d_fp16<32, 64>(src, tile, threadIdx.x, blockDim.x);
+    dme::wait();
+    __syncthreads();
+    for (int i = threadIdx.x; i < 32 * 64; i += blockDim.x) out[i] = tile[i];
+}
+
+// Two waves: AsyncTile2D<16, 64> ping/pong over n_tiles consecutive tiles; each iteration copies
+// the current buffer out while the next tile is in flight.
+__global__ void dme_async_tile_kernel(const __half* __restrict__ src, __half* __restrict__ out, int n_tiles) {
+    __shared__ __attribute__((aligned(16))) __half buf[2][16 * 64];
+    dme::AsyncTile2D<16, 64> t;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    t.prologue(src, buf, tid, nt);
+    for (int j = 0; j < n_tiles; ++j) {
+        t.prefetch_next(src, buf, j + 1, n_tiles, tid, nt);
+        for (int i = tid; i < 16 * 64; i += nt) out[(size_t)j * 16 * 64 + i] = buf[t.cur()][i];
+        t.wait_next(j + 1, n_tiles);
+        t.advance();
+    }
+}
+
+// One wave: online_softmax_step over n_tiles 64-wide tiles of scores s with values v; out = {m,
+// l, sum_k softmax(s)_k v_k} after the last tile.
+__global__ void online_softmax_kernel(const float* __restrict__ s, const float* __restrict__ v, int n_tiles,
+                                      float* __restrict__ out) {
+    const int L = threadIdx.x;
+    float m = -INFINITY, l = 0.f, acc = 0.f;
+    for (int t = 0; t < n_tiles; ++t) {
+        float p;
+        const float resc = cdna3::ex::online_softmax_step(s[t * 64 + L], m, l, p);
+        acc = acc * resc + wave::dpp::reduce_sum_bcast(p * v[t * 64 + L]);
+    }
+    if (L == 0) {
+        out[0] = m;
+        out[1] = l;
+        out[2] = acc / l;
+    }
+}
+
+__global__ void mma_tile_kernel(const __half* A, const __half* B, float* C, int ldA, int ldB, int ldC) {
+    cdna3::ex::mma_tile_accumulate(A, B, C, threadIdx.x, ldA, ldB, ldC);
+}
+template <typename T>
+__global__ void mma_tile_k32_kernel(const T* A, const T* B, float* C, int ldA, int ldB, int ldC) {
+    cdna3::ex::mma_tile_accumulate_k32<T>(A, B, C, threadIdx.x, ldA, ldB, ldC);
+}
+
+extern "C" int hook_dme_forms(const float* fsrc, float* fout, const void* hsrc, void* hout, const void* asrc,
+                              void* aout, int n_tiles, void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    dme_elem_kernel<<<1, 64, 0, s>>>(fsrc, fout);
+    dme_tile2d_kernel<<<1, 128, 0, s>>>((const __half*)hsrc, (__half*)hout);
+    dme_async_tile_kernel<<<1, 128, 0, s>>>((const __half*)asrc, (__half*)aout, n_tiles);
+    return (int)hipGetLastError();
+}
+
+extern "C" int hook_online_softmax(const float* s, const float* v, int n_tiles, float* out, void* stream) {
+    online_softmax_kernel<<<1, 64, 0, (hipStream_t)stream>>>(s, v, n_tiles, out);
+    return (int)hipGetLastError();
+}
+
+// which: 0 = mma_tile_accumulate (16x16x16 f16), 1 / 2 = mma_tile_accumulate_k32 f16 / bf16.
+extern "C" int hook_mma_tile(int which, const void* A, const void* B, float* C, int ldA, int ldB, int ldC,
+                             void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    switch (which) {
+        case 0: mma_tile_kernel<<<1, 64, 0, s>>>((const __half*)A, (const __half*)B, C, ldA, ldB, ldC); break;
+        case 1: mma_tile_k32_kernel<_Float16><<<1, 64, 0, s>>>((const _Float16*)A, (const _Float16*)B, C, ldA, ldB, ldC); break;
+        case 2: mma_tile_k32_kernel<__bf16><<<1, 64, 0, s>>>((const __bf16*)A, (const __bf16*)B, C, ldA, ldB, ldC); break;
+        default: return 1;
+    }
+    return (int)hipGetLastError();
+}
+
+// The runtime's __global__ kernels of <cdna3/runtime/forward.hpp>, launched as the reference's
+// layer loop launches them (session.hpp:168-177, :193-207, :246-249): grid M x 256 threads for the
+// norm, one 256-thread block per 256 elements for the rest.
+extern "C" int hook_runtime_kernels(int which, const void* a, void* b, const void* c, const void* d, int i0, int i1,
+                                    int i2, int i3, int i4, float f, void* stream) {
+    using namespace cdna3::runtime;
+    hipStream_t s = (hipStream_t)stream;
+    auto grid1d = [](long long n) { return dim3((unsigned)((n + 255) / 256)); };
+    switch (which) {
+        case 0:   // rmsnorm_f32_kernel(X, W, Y, M, H, eps), block i2 threads (the reference: 256)
+            hipLaunchKernelGGL(rmsnorm_f32_kernel, dim3(i0), dim3(i2), 0, s, (const float*)a, (const __half*)c,
+                               (float*)b, i0, i1, f);
+            break;
+        case 1:   // rope_kernel(T, cos, sin, seq, heads, D) in place on b
+            hipLaunchKernelGGL(rope_kernel, grid1d((long long)i0 * i1 * i2), dim3(256), 0, s, (__half*)b,
+                               (const float*)c, (const float*)d, i0, i1, i2);
+            break;
+        case 2:   // repack_kernel(src, dst, seq, heads, D, dir)
+            hipLaunchKernelGGL(repack_kernel, grid1d((long long)i0 * i1 * i2), dim3(256), 0, s, (const __half*)a,
+                               (__half*)b, i0, i1, i2, i3);
+            break;
+        case 3:   // scatter_kv_kernel(src, cache, T, heads, D, pos0, max_seq)
+            hipLaunchKernelGGL(scatter_kv_kernel, grid1d((long long)i0 * i1 * i2), dim3(256), 0, s,
+                               (const __half*)a, (__half*)b, i0, i1, i2, i3, i4);
+            break;
+        case 4:   // pack_kv_kernel(cache, packed, heads, N, D, max_seq)
+            hipLaunchKernelGGL(pack_kv_kernel, grid1d((long long)i0 * i1 * i2), dim3(256), 0, s, (const __half*)a,
+                               (__half*)b, i0, i1, i2, i3);
+            break;
+        default: return 1;
+    }
     return (int)hipGetLastError();
 }

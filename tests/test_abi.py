@@ -79,13 +79,44 @@ def test_invalid_arguments_rejected_without_gpu():
     assert l.cdna3_repack_f16(p, p, 4, 2, 64, 2, None) == 1                                 # direction
     assert l.cdna3_rope_append_kv_f16(p, p, p, p, p, p, p, p, 4, 8, 2, 63, 0, 16, None) == 1  # odd D
     assert l.cdna3_rope_append_kv_f16(p, p, p, p, p, p, p, p, 4, 8, 2, 64, 14, 16, None) == 1  # past the cache
+    assert l.cdna3_attn_decode_noalloc(p, p, p, p, ctypes.byref(dcfg), cdna4.F32, None) == 1       # dtype
+    big = cdna4.DecodeCfg(128, 4096, 64, 4, 1024)                                                   # 34 MB of partials
+    assert l.cdna3_attn_decode_noalloc(p, p, p, p, ctypes.byref(big), cdna4.F16, None) == 2
+    info = cdna4.PlanInfo()
+    assert l.cdna3_attn_prefill_plan(ctypes.byref(bad[0]), cdna4.BF16, ctypes.byref(info)) == 1
+    assert l.cdna3_attn_decode_plan(ctypes.byref(dcfg), cdna4.F32, 1, ctypes.byref(info)) == 1
+    st = ctypes.c_int(0)
+    assert l.cdna3_scan_status(None, ctypes.byref(st), None) == 1
+    m = ctypes.c_void_p()
+    assert l.cdna3_model_load(b"/nonexistent/model", ctypes.byref(m)) == 1 and not m.value
+    assert l.cdna3_model_config(None, None) == 1
+    l.cdna3_model_free(None)   # no-op
+
+
+def test_kernel_plans_without_gpu():
+    # The dispatch thresholds (for a 256-CU MI355X): 8 waves x 32 queries once batch * heads *
+    # ceil(seqQ / 256) >= 512, 4 waves x 16 queries for mid sizes, fa_small below; decode splits
+    # long caches only when given a workspace.
+    plan = lambda *c: cdna4.prefill_plan(cdna4.PrefillCfg(*c), cdna4.BF16)
+    assert plan(128, 8192, 8192, 32, 32, 4, 1).name == "fa_mfma_8w"
+    assert plan(128, 4096, 4096, 8, 8, 1, 1).name == "fa_mfma_4w"
+    assert plan(64, 512, 512, 8, 8, 1, 0).name == "fa_small"
+    assert cdna4.prefill_plan(cdna4.PrefillCfg(64, 512, 512, 8, 8, 1, 0), cdna4.F32).name == "fa_f32"
+    d = cdna4.DecodeCfg(128, 8192, 32, 8, 1)
+    split, one = cdna4.decode_plan(d, cdna4.F16, True), cdna4.decode_plan(d, cdna4.F16, False)
+    assert split.name == "decode_split" and split.partials > 1 and split.workspace == cdna4.decode_workspace_size(d)
+    assert one.name == "decode_wg" and one.partials == 1 and one.workspace == 0
 
 
 def test_cpp_headers_compile_host_only(tmp_path):
     src = tmp_path / "use.cpp"
     src.write_text(
         "#include <cdna3/attention.hpp>\n#include <cdna3/runtime/forward.hpp>\n#include <cdna3/runtime/session.hpp>\n"
-        "#include <cdna3/llm_integration.hpp>\n"
+        "#include <cdna3/llm_integration.hpp>\n#include <cdna3/runtime/kv_cache.hpp>\n"
+        "#include <cdna3/runtime/model_loader.hpp>\n"
+        "int m(cdna3::runtime::KVCache& kv) { cdna3::runtime::ModelLoader l(\"/tmp/x\"); l.load();\n"
+        "  const auto& c = l.weights().cfg; kv.allocate(c.n_layers, c.n_kv_heads, 4096, c.head_dim);\n"
+        "  return kv.K_layer(1, 0) == l.weights().layers[0].Wq; }\n"
         "hipError_t h(const __half* q, const __half* k, const __half* v, __half* o) {\n"
         "  return fa_attn::launch(q, k, v, o, 256, 8, 2, 128) == hipSuccess\n"
         "       ? fa_decode::launch(q, k, v, o, fa_decode::DCfg{128, 256, 8, 2}, 4) : hipErrorInvalidValue;\n}\n"
@@ -98,6 +129,29 @@ def test_cpp_headers_compile_host_only(tmp_path):
         "       + (int)cdna3::attn::decode_dme(q, k, v, o, dd);\n}\n")
     r = subprocess.run([CLANG, "-std=c++17", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
                         f"-I{ROOT}/include", str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_reference_kernel_launches_compile_in_hip_source(tmp_path):
+    # The reference's layer loop launches the runtime kernels itself (session.hpp:168-177,
+    # :193-207, :246-249); the same statements compile against <cdna3/runtime/forward.hpp>.
+    src = tmp_path / "loop.hip"
+    src.write_text(
+        "#include <cdna3/runtime/forward.hpp>\n#include <cdna3/runtime/kv_cache.hpp>\n"
+        "namespace cdna3 { namespace runtime {\n"
+        "static dim3 grid1d(size_t n, int tpb = 256) { return dim3((unsigned)((n + tpb - 1) / tpb)); }\n"
+        "void step(float* d_hidden, const __half* w, float* d_norm, __half* d_q, __half* d_k, const float* d_cos,\n"
+        "          const float* d_sin, KVCache& kv_, __half* d_qh, int T, int H, int nH, int nKV, int D, int pos0, int max_seq_) {\n"
+        "  hipLaunchKernelGGL(rmsnorm_f32_kernel, dim3(T), dim3(256), 0, 0, d_hidden, w, d_norm, T, H, 1e-6f);\n"
+        "  hipLaunchKernelGGL(rope_kernel, grid1d((size_t)T * nH * D), dim3(256), 0, 0, d_q, d_cos, d_sin, T, nH, D);\n"
+        "  hipLaunchKernelGGL(repack_kernel, grid1d((size_t)T * nH * D), dim3(256), 0, 0, d_q, d_qh, T, nH, D, 0);\n"
+        "  hipLaunchKernelGGL(scatter_kv_kernel, grid1d((size_t)T * nKV * D), dim3(256), 0, 0, d_k, kv_.K_layer(0, 0),\n"
+        "                     T, nKV, D, pos0, max_seq_);\n"
+        "  hipLaunchKernelGGL(pack_kv_kernel, grid1d((size_t)nKV * T * D), dim3(256), 0, 0, kv_.K_layer(0, 0), d_qh,\n"
+        "                     nKV, T, D, max_seq_);\n"
+        "}\n}}\n")
+    r = subprocess.run([HIPCC, "--offload-arch=gfx950", "-std=c++17", "-fsyntax-only", f"-I{ROOT}/include", str(src)],
+                       capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
 
 
@@ -128,6 +182,20 @@ def test_wave_primitives_use_no_lds_and_no_readlane(tmp_path):
         assert not re.search(r"v_pk_(add|mul|fma)_f32", body), name
 
 
+def test_header_runtime_kernels_use_no_lds(tmp_path):
+    # rmsnorm_f32_kernel forms the row's scale in every wave with the DPP/permlane butterfly: no
+    # LDS and no barrier (the reference's used a 256-entry LDS tree with a barrier per level).
+    asm = _device_asm(os.path.join(ROOT, "tests", "native", "wave_hooks.hip"), tmp_path)
+    funcs = {k: v for k, v in _functions(asm).items()
+             if any(n in k for n in ("rmsnorm_f32_kernel", "rope_kernel", "repack_kernel", "scatter_kv_kernel",
+                                     "pack_kv_kernel"))}
+    assert len(funcs) == 5, sorted(funcs)
+    for name, body in funcs.items():
+        assert not re.search(r"^\s+ds_", body, re.M), name
+        assert "s_barrier" not in body, name
+        assert not re.search(r"v_pk_(add|mul|fma)_f32", body), name
+
+
 def test_library_kernels_avoid_lds_where_designed_to(tmp_path):
     # Reductions, scans, norms, KV-cache and runtime kernels and the decode merge are LDS-free by design; prefill and the
     # decode kernels (split partials and the short-cache workgroup variant) stage K/V in LDS, and the residual GEMV
@@ -143,6 +211,20 @@ def test_library_kernels_avoid_lds_where_designed_to(tmp_path):
                 assert len(ds) <= 4, (src, name, ds)
                 continue
             assert not ds, (src, name)
+
+
+def test_scan_tiles_keep_values_in_vgprs(tmp_path):
+    # The shipped scan tiles (32 vectors per lane) fit the architectural VGPRs: no accumulator
+    # registers and no scratch. (A 48-vector build of an earlier kernel structure needed 504
+    # registers, the upper 248 as accumulator registers, and took a memory-aperture fault.)
+    asm = _device_asm(os.path.join(ROOT, "amd-incstinct-labs_amd", "csrc", "reduce_scan.hip"), tmp_path)
+    kernels = re.findall(r"\.amdhsa_kernel (\S*scan_tiles\S*)(.*?)\.end_amdhsa_kernel", asm, re.S)
+    assert len(kernels) == 36    # 6 dtypes x 3 ops x aligned / misaligned
+    for name, meta in kernels:
+        field = lambda k: int(re.search(r"\.amdhsa_" + k + r"\s+(\d+)", meta).group(1))
+        assert field("next_free_vgpr") <= 256, name
+        assert field("accum_offset") >= field("next_free_vgpr"), name   # no accumulator registers
+        assert field("private_segment_fixed_size") == 0, name
 
 
 def test_decode_kernel_streams_kv_through_lds_onto_matrix_cores(tmp_path):

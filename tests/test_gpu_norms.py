@@ -52,3 +52,71 @@ def test_rope_table_and_rope(seq, heads, D, pos0):
     want = oracle.widen(oracle.rope(bits, c_ref, s_ref, seq, heads, D), oracle.F16)
     # Same fp32 formula and RNE; only FMA contraction may move a result by one fp16 ulp.
     np.testing.assert_allclose(got, want, rtol=2.0 ** -10, atol=2.0 ** -24)
+
+
+# ---- the reference's __global__ kernels from <cdna3/runtime/forward.hpp>, launched as its layer
+# loop launches them (hipLaunchKernelGGL, session.hpp:168-177, :193-207, :246-249) -------------
+
+def _rt(which, a, b, c=None, d=None, ints=(0, 0, 0, 0, 0), f=0.0):
+    from gpu_util import hooks, ptr, stream
+    import ctypes
+    p = lambda t: ctypes.c_void_p(0 if t is None else t.data_ptr())
+    rc = hooks().hook_runtime_kernels(which, p(a), p(b), p(c), p(d), *ints, f, stream())
+    torch.cuda.synchronize()
+    assert rc == 0
+
+
+@pytest.mark.parametrize("M,H,block", [(1, 768, 256), (512, 768, 256), (37, 64, 256), (5, 1000, 256), (3, 5000, 256),
+                                       (2, 3, 256), (64, 768, 64), (16, 4096, 1024)])
+def test_rmsnorm_f32_kernel_as_launched_by_the_reference(M, H, block):
+    X = oracle.normal(M * 3 + H, M * H, 0.0, 2.0).reshape(M, H)
+    _, wb = oracle.round16(oracle.normal(H + 1, H, 1.0, 0.1), oracle.F16)
+    Xt = torch.from_numpy(X).to(DEV)
+    Wt = torch.from_numpy(wb.view(np.int16)).view(torch.float16).to(DEV)
+    Y = torch.full_like(Xt, float("nan"))
+    _rt(0, Xt, Y, Wt, None, (M, H, block, 0, 0), 1e-6)
+    np.testing.assert_allclose(Y.cpu().numpy(), oracle.rmsnorm(X, wb, 1e-6), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("seq,heads,D", [(512, 12, 64), (1, 12, 64), (33, 8, 128), (5, 2, 10)])
+def test_rope_kernel_as_launched_by_the_reference(seq, heads, D):
+    c_ref, s_ref = oracle.rope_table(7, seq, D, 10000.0)
+    _, bits = oracle.round16(oracle.normal(seq * D + heads, seq * heads * D), oracle.F16)
+    T = torch.from_numpy(bits.view(np.int16)).view(torch.float16).to(DEV)
+    _rt(1, None, T, torch.from_numpy(c_ref).to(DEV), torch.from_numpy(s_ref).to(DEV), (seq, heads, D, 0, 0))
+    got = oracle.widen(T.view(torch.int16).cpu().numpy().view(np.uint16), oracle.F16)
+    want = oracle.widen(oracle.rope(bits, c_ref, s_ref, seq, heads, D), oracle.F16)
+    np.testing.assert_allclose(got, want, rtol=2.0 ** -10, atol=2.0 ** -24)
+
+
+@pytest.mark.parametrize("seq,heads,D", [(77, 12, 64), (5, 2, 128)])
+def test_repack_and_pack_kv_kernels(seq, heads, D):
+    bits = (oracle.integers(seq, seq * heads * D, 0, 65535).astype(np.uint16) & 0x7bff)
+    src = torch.from_numpy(bits.view(np.int16)).to(DEV)
+    for direction in (0, 1):
+        dst = torch.zeros_like(src)
+        _rt(2, src, dst, ints=(seq, heads, D, direction, 0))
+        assert np.array_equal(dst.cpu().numpy().view(np.uint16), oracle.repack(bits, seq, heads, D, direction))
+    # pack_kv_kernel: the first N rows of each head of a [heads][max_seq][D] cache, packed.
+    max_seq, N = seq + 9, seq - 3
+    cache = oracle.integers(seq + 1, heads * max_seq * D, 0, 30000).astype(np.uint16)
+    tc = torch.from_numpy(cache.view(np.int16)).to(DEV)
+    packed = torch.zeros(heads * N * D, dtype=torch.int16, device=DEV)
+    _rt(4, tc, packed, ints=(heads, N, D, max_seq, 0))
+    want = cache.reshape(heads, max_seq, D)[:, :N].reshape(-1)
+    assert np.array_equal(packed.cpu().numpy().view(np.uint16), want)
+
+
+@pytest.mark.parametrize("T,pos0,max_seq", [(16, 0, 64), (1, 63, 64), (10, 60, 64)])
+def test_scatter_kv_kernel(T, pos0, max_seq):
+    heads, D = 4, 64
+    src = oracle.integers(T + pos0, T * heads * D, 0, 30000).astype(np.uint16)
+    cache = oracle.integers(7, heads * max_seq * D, 0, 30000).astype(np.uint16)
+    ts = torch.from_numpy(src.view(np.int16)).to(DEV)
+    tc = torch.from_numpy(cache.view(np.int16)).to(DEV)
+    _rt(3, ts, tc, ints=(T, heads, D, pos0, max_seq))
+    # Rows at or past max_seq are skipped (the reference wrote past the slot): compare with the
+    # oracle's scatter of the rows that fit.
+    fit = max(0, min(T, max_seq - pos0))
+    want = oracle.scatter_kv(src.reshape(T, heads, D)[:fit].reshape(-1), cache, fit, heads, D, pos0, max_seq)
+    assert np.array_equal(tc.cpu().numpy().view(np.uint16), want)

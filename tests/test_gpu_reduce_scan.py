@@ -124,3 +124,22 @@ def test_full_sweep_2_26(dtype):
     # Checksum of checksums: the last prefix equals the total.
     if dtype in (oracle.I32, oracle.I64):
         assert int(got[-1].item()) == int(cdna4.reduce(t, "sum").item())
+
+
+def test_scan_timeout_is_reported_not_silent(monkeypatch):
+    # Force the look-back's bounded wait to give up at once (CDNA4_SCAN_SPIN_LIMIT=0): tiles whose
+    # predecessors have not published yet stop waiting, every kernel still finishes, and the
+    # workspace status word reports the invalid result, so the Python scan raises instead of
+    # returning it. With the normal bound the same call is valid.
+    n = 1 << 24
+    h, t = make(oracle.I32, n, 11)
+    ws = torch.empty(cdna4.scan_workspace_size(n, cdna4.I32), dtype=torch.uint8, device=DEV)
+    monkeypatch.setenv("CDNA4_SCAN_SPIN_LIMIT", "0")
+    with pytest.raises(cdna4.CDNA4Error):
+        for _ in range(8):   # some tile must find its predecessor unpublished
+            cdna4.scan_inclusive(t, "sum", workspace=ws)
+    assert cdna4.scan_status(ws) != 0
+    monkeypatch.delenv("CDNA4_SCAN_SPIN_LIMIT")
+    got = cdna4.scan_inclusive(t, "sum", workspace=ws)
+    assert cdna4.scan_status(ws) == 0
+    assert np.array_equal(got.cpu().numpy(), oracle.scan_inclusive(oracle.SUM, oracle.I32, h))

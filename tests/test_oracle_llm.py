@@ -134,7 +134,40 @@ def test_oracle_closed_form_without_layer_contributions(tmp_path):
     x = t["embed_tokens"].astype(np.float64)[ids]
     y = x / np.sqrt((x * x).mean(1, keepdims=True) + 1e-6) * t["final_norm"].astype(np.float64)
     ref = y @ t["lm_head"].astype(np.float64).T
-    assert np.abs(got - ref).max() < 1e-4
+    # the logits are stored as fp16 (gemm_f32in_f16out_kernel): representable in fp16, and within
+    # half an fp16 ulp (plus fp32 accumulation error) of the exact value
+    assert np.array_equal(got, got.astype(np.float16).astype(np.float32))
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -11 + 1e-5)
+
+
+def _bitrev8(x):
+    return int(f"{x:08b}"[::-1], 2)
+
+
+def test_reference_argmax_tie_break():
+    # argmax_kernel (forward.hpp:244-262), restated step by step in oracle.reference_argmax:
+    # thread t keeps the first maximum of indices t, t + 256, ...; the tree then merges thread
+    # t + s into t for s = 128, 64, ..., 1 and keeps t on ties. Thread t therefore beats every
+    # tied thread whose index, bit-reversed over 8 bits, is larger: the winner among equal maxima
+    # has the smallest bitrev8(i % 256), then the smallest i.
+    x = np.zeros(1000, np.float32)
+    x[[5, 256]] = 3.0
+    assert oracle.reference_argmax(x) == 256          # thread 0 beats thread 5
+    x[:] = 0
+    x[[44, 300]] = 3.0
+    assert oracle.reference_argmax(x) == 44           # same thread: its first maximum
+    assert oracle.reference_argmax(np.zeros(1000, np.float32)) == 0
+    assert oracle.reference_argmax(np.array([1.0, 7.0, 7.0], np.float32)) == 2   # thread 2 merges into 0 first
+    x[:] = 0
+    x[[1, 128]] = 1.0
+    assert oracle.reference_argmax(x) == 128          # bitrev8(128) = 1 < bitrev8(1) = 128
+    rng = np.random.default_rng(0)
+    for n in (3, 255, 256, 257, 1000, 32000):
+        for _ in range(20):
+            v = rng.integers(0, 4, n).astype(np.float32)     # many ties
+            best = np.flatnonzero(v == v.max())
+            want = min(best, key=lambda i: (_bitrev8(i % 256), i))
+            assert oracle.reference_argmax(v) == want
 
 
 def test_model_format_round_trip_and_validation(tmp_path):
