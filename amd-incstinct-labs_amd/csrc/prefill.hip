@@ -40,6 +40,21 @@ using wave::xlane::Sum;
 using namespace tile;
 constexpr int kBc = 64;       // keys per K/V tile
 
+// (batch * head, q block) of a workgroup in a grid of exactly nbh * nqb workgroups. Workgroups are
+// dispatched round-robin over the 8 XCDs (XCD = blockIdx % 8); with xcd_map (nbh % 8 == 0) the q
+// blocks of (batch, head) bh all run on XCD bh % 8, so that head's K and V are fetched into one
+// XCD's L2 instead of into all eight. Otherwise q blocks of one head are consecutive.
+__device__ __forceinline__ void block_item(int item, int nqb, int xcd_map, int& bh, int& qblk) {
+    if (xcd_map) {
+        const int xcd = item & 7, slot = item >> 3;
+        bh = (slot / nqb) * 8 + xcd;
+        qblk = slot % nqb;
+    } else {
+        bh = item / nqb;
+        qblk = item % nqb;
+    }
+}
+
 struct PrefillArgs {
     const uint16_t* Q; const uint16_t* K; const uint16_t* V; uint16_t* O;
     // Element strides (batch, head, row) of Q, of K and V, and of O; the contiguous layout is
@@ -332,14 +347,15 @@ __device__ __forceinline__ void f32_chunk_load(const float* __restrict__ Kh, con
 template <int D>
 __global__ __launch_bounds__(64 * kF32Waves) void fa_f32(const float* __restrict__ Q, const float* __restrict__ K,
                                                          const float* __restrict__ V, float* __restrict__ O, int seqQ,
-                                                         int seqK, int nQH, int nKVH, int causal, int nqb, float sc) {
+                                                         int seqK, int nQH, int nKVH, int causal, int nqb, int xcd_map,
+                                                         float sc) {
     constexpr int DS = D / 4, NB = D / 16;
     __shared__ __attribute__((aligned(16))) float o_s[kF32Waves][kF32Br][D];
     __shared__ float m_s[kF32Waves][kF32Br], l_s[kF32Waves][kF32Br];
     const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
     const int r = lane & 15, g = lane >> 4;
-    const int qb = blockIdx.x % nqb;
-    const int bh = blockIdx.x / nqb;
+    int bh, qb;
+    block_item(blockIdx.x, nqb, xcd_map, bh, qb);
     const int b = bh / nQH, h = bh % nQH;
     const int kvh = h / (nQH / nKVH);
     const int q0 = qb * kF32Br;
@@ -453,8 +469,8 @@ __global__ __launch_bounds__(64 * W) void fa_small(PrefillArgs a) {
     const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
     const int li = lane & 15, g = lane >> 4;
     const int nqb = (a.seqQ + 15) / 16;
-    const int qblk = blockIdx.x % nqb;
-    const int bh = blockIdx.x / nqb;
+    int bh, qblk;
+    block_item(blockIdx.x, nqb, a.xcd_map, bh, qblk);
     const int b = bh / a.nQH, h = bh % a.nQH;
     const int kvh = h / (a.nQH / a.nKVH);
     const int q0 = qblk * 16;
@@ -571,6 +587,7 @@ int dispatch_mfma(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& st, c
             fa_mfma<D, 4, 1, kBf16><<<(unsigned)p.grid, 64 * 4, 0, s>>>(a);
             break;
         default:
+            a.xcd_map = (nbh % 8 == 0) ? 1 : 0;
             if (p.waves == small_waves<D>(true))
                 fa_small<D, kBf16, small_waves<D>(true)><<<(unsigned)p.grid, 64 * small_waves<D>(true), 0, s>>>(a);
             else
@@ -620,14 +637,15 @@ extern "C" int cdna3_attn_prefill(const void* Q, const void* K, const void* V, v
         const long long blocks = (long long)c.batch * c.nQHeads * nqb;
         if (blocks > 0x7fffffffLL) return CDNA4_ERR_INVALID_VALUE;
         const float sc = kLog2e / sqrtf((float)c.D);
+        const int xcd = ((long long)c.batch * c.nQHeads % 8 == 0) ? 1 : 0;
         if (c.D == 128)
             fa_f32<128><<<(unsigned)blocks, 64 * kF32Waves, 0, s>>>((const float*)Q, (const float*)K, (const float*)V,
                                                                     (float*)O, c.seqQ, c.seqK, c.nQHeads, c.nKVHeads,
-                                                                    c.causal ? 1 : 0, nqb, sc);
+                                                                    c.causal ? 1 : 0, nqb, xcd, sc);
         else
             fa_f32<64><<<(unsigned)blocks, 64 * kF32Waves, 0, s>>>((const float*)Q, (const float*)K, (const float*)V,
                                                                    (float*)O, c.seqQ, c.seqK, c.nQHeads, c.nKVHeads,
-                                                                   c.causal ? 1 : 0, nqb, sc);
+                                                                   c.causal ? 1 : 0, nqb, xcd, sc);
         return launch_status();
     }
     const cdna3_prefill_strides st = contiguous_strides(c);
