@@ -98,6 +98,15 @@ def load_traffic(name):
         return json.load(f).get(name, {}).get("bytes_per_launch")
 
 
+def load_traffic_llm():
+    """HBM bytes read per decode step of config 5 recorded in profiles/traffic.json (None when absent)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("llm", {}).get("read_bytes_per_token")
+
+
 def cpu_baseline_prefill():
     """Reference cpu_prefill (oracle/_ref) on one (batch, head) of config 3, one thread."""
     import numpy as np
@@ -461,7 +470,10 @@ def bench_llm(steps):
                       "heads": nH, "head_dim": H // nH, "mlp": F, "vocab": V, "prompt": prompt, "new_tokens": new,
                       "norm": meta.get("norm"), "dtype": "fp16"},
            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                        "frac": gbs / PEAK_HBM_GBS, "traffic": None,
+                        "frac": gbs / PEAK_HBM_GBS, "traffic": load_traffic_llm(),
+                        "traffic_source": ("profiles/traffic.json: HBM reads per decode step from an earlier "
+                                           "rocprofv3 --pmc FETCH_SIZE run of this workload (calibrated on a 1 GiB "
+                                           "copy); writes, ~0.4 MB per token, not included; not measured in this run"),
                         "bytes_per_token": 2 * params + kv_bytes}}
     if cpu:
         out["cpu_baseline"] = cpu
