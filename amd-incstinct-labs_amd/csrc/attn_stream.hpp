@@ -33,8 +33,9 @@ __device__ __forceinline__ void wait_copies_younger(int y) {
 }
 
 // Copy keys [k0, k0 + kDecT) of one head (row stride rs elements; rows past N re-read key N-1,
-// they are masked) into a ring stage, 16-byte chunks of a row XOR-swizzled as the tile reads expect.
-template <int D>
+// they are masked) into a ring stage, 16-byte chunks of a row XOR-swizzled as the tile reads expect
+// (the K swizzle when kIsK, else the V swizzle).
+template <int D, bool kIsK>
 __device__ __forceinline__ void load_stage(const uint16_t* __restrict__ head, long long rs, int k0, int N,
                                            uint16_t* stage, int lane) {
     constexpr int CPR = D / 8;
@@ -43,7 +44,7 @@ __device__ __forceinline__ void load_stage(const uint16_t* __restrict__ head, lo
     for (int j = 0; j < NI; ++j) {
         const int p = j * 64 + lane;
         const int r = p / CPR;
-        const int lc = (p % CPR) ^ tile::swz<D>(r);
+        const int lc = (p % CPR) ^ tile::swz<D, kIsK>(r);
         const int key = min(k0 + r, N - 1);
         dma16(head + key * rs + lc * 8, stage + j * 64 * 8);
     }
@@ -77,16 +78,16 @@ __device__ __forceinline__ void stream_keys(const uint16_t* Kh, const uint16_t* 
 #pragma unroll
     for (int i = 0; i < NS - 1; ++i)
         if (i < nch) {
-            load_stage<D>(Kh, rs, kbeg + i * kDecT, N, k_lds + i * kStage, lane);
-            load_stage<D>(Vh, rs, kbeg + i * kDecT, N, v_lds + i * kStage, lane);
+            load_stage<D, true>(Kh, rs, kbeg + i * kDecT, N, k_lds + i * kStage, lane);
+            load_stage<D, false>(Vh, rs, kbeg + i * kDecT, N, v_lds + i * kStage, lane);
         }
     int st = 0;   // stage of chunk ch
     for (int ch = 0; ch < nch; ++ch) {
         const int ahead = ch + NS - 1;
         if (ahead < nch) {
             const int sa = (st == 0) ? NS - 1 : st - 1;   // stage of chunk ch - 1, already consumed
-            load_stage<D>(Kh, rs, kbeg + ahead * kDecT, N, k_lds + sa * kStage, lane);
-            load_stage<D>(Vh, rs, kbeg + ahead * kDecT, N, v_lds + sa * kStage, lane);
+            load_stage<D, true>(Kh, rs, kbeg + ahead * kDecT, N, k_lds + sa * kStage, lane);
+            load_stage<D, false>(Vh, rs, kbeg + ahead * kDecT, N, v_lds + sa * kStage, lane);
         }
         wait_copies_younger<kCopies>(min(NS - 1, nch - 1 - ch));
         const char* Kt = (const char*)(k_lds + st * kStage);

@@ -6,7 +6,8 @@
 // accumulator into the B operand of the P.V MFMA without data movement: the rows of each K
 // operand tile are permuted (key = 8*(m/4) + 4*u + m%4 for A-row m of sub-tile u) so that the
 // 8 keys a lane holds are the 8 consecutive keys its B operand needs. K rows come from LDS with
-// ds_read_b128, V^T rows with ds_read_b64_tr_b16, both conflict-free under the swizzle swz<D>.
+// ds_read_b128 under the swizzle swz_k<D>, V^T rows with ds_read_b64_tr_b16 under swz_v<D>,
+// both free of bank conflicts.
 // Softmax runs in base 2 (scores prescaled by log2(e) / sqrt(D)) against a lazily refreshed
 // reference maximum m (see kTau).
 #pragma once
@@ -52,21 +53,40 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
 }
 
-// XOR swizzle of the 16-byte chunks of key row r inside a K/V tile. Requirements:
-//   * K operand reads (ds_read_b128): the 16 rows one lane group reads, r = 8*(m/4) + 4u + m%4
-//     (bits 0, 1, 3, 4 vary), land on 16 different chunk positions;
-//   * V^T operand reads (ds_read_b64_tr_b16): a lane group reads rows 8g + x (x = 0..3) at two
-//     adjacent chunks; the 4 rows must land on distinct chunk pairs, and lane groups g, g+1 (one
-//     32-lane LDS pass) on different 128-byte halves.
-// D = 128 (16 chunks per 256-byte row): bit 0 <- r4, bits 1-2 <- r0-r1, bit 3 <- r3.
-// D = 64 (8 chunks per 128-byte row, two rows per 256-byte bank window): bit 0 <- r4,
-// bit 1 <- r1, bit 2 <- r3.
+// XOR swizzles of the 16-byte chunks of key row r inside a K tile (swz_k) and a V tile (swz_v).
+// The LDS has 64 four-byte banks (256 bytes per clock). Both swizzles depend on row bits 0, 1,
+// 3 and 4 only (see LdsOffsets).
+//   * K operand reads (ds_read_b128, 4 clocks per wave): lane (li, g) reads row
+//     r = 8*(li/4) + li%4 (+ 4u + 32kc) at chunk g + 4c. Which 16 lanes share a clock is not
+//     documented; measured on gfx950, a swizzle that spreads every 16 consecutive lanes over the
+//     16 chunk positions still leaves a 2-way conflict (8 clocks per read), and one that is
+//     conflict-free under every pairing of 8-lane blocks consistent with that measurement runs
+//     at 4 clocks with no conflict cycles (SQ_LDS_BANK_CONFLICT = 0). That is swz_k:
+//     D = 128 (16 chunks per 256-byte row): bits 0-1 <- r0-r1, bits 2-3 <- r3-r4;
+//     D = 64 (8 chunks per 128-byte row, two rows per 256-byte window): bits 0-2 <- r1, r3, r4.
+//   * V^T operand reads (ds_read_b64_tr_b16, 2 clocks): a lane group reads rows 8g + x
+//     (x = 0..3) at two adjacent chunks; the 4 rows must land on distinct chunk pairs, and lane
+//     groups g, g+1 (one 32-lane pass) on different 128-byte halves. swz_v:
+//     D = 128: bit 0 <- r4, bits 1-2 <- r0-r1, bit 3 <- r3;
+//     D = 64: bit 0 <- r4, bit 1 <- r1, bit 2 <- r3 (measured conflict-free as well).
 template <int D>
-__device__ __forceinline__ int swz(int r) {
+__device__ __forceinline__ int swz_k(int r) {
+    if constexpr (D == 128)
+        return (r & 3) | (((r >> 3) & 3) << 2);
+    else
+        return ((r >> 1) & 1) | (((r >> 3) & 1) << 1) | (((r >> 4) & 1) << 2);
+}
+template <int D>
+__device__ __forceinline__ int swz_v(int r) {
     if constexpr (D == 128)
         return ((r >> 4) & 1) | ((r & 3) << 1) | (((r >> 3) & 1) << 3);
     else
         return ((r >> 4) & 1) | (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
+}
+// Swizzle of a tile that holds K rows (kIsK) or V rows.
+template <int D, bool kIsK>
+__device__ __forceinline__ int swz(int r) {
+    return kIsK ? swz_k<D>(r) : swz_v<D>(r);
 }
 
 // Softmax reference maxima are refreshed only when a new maximum exceeds them by more than
@@ -95,9 +115,9 @@ template <int D>
 __device__ __forceinline__ LdsOffsets lds_offsets(int li, int g) {
     LdsOffsets off;
     const int rk = (li >> 2) * 8 + (li & 3);                 // K row of A-row li, sub-tile 0
-    off.k = (uint32_t)(rk * D + ((g ^ swz<D>(rk)) * 8)) * 2u;
+    off.k = (uint32_t)(rk * D + ((g ^ swz_k<D>(rk)) * 8)) * 2u;
     const int rv = g * 8 + (li >> 2);                        // V row of the first transpose read
-    off.v = (uint32_t)(rv * D + ((((li & 3) >> 1) ^ swz<D>(rv)) * 8) + (li & 1) * 4) * 2u;
+    off.v = (uint32_t)(rv * D + ((((li & 3) >> 1) ^ swz_v<D>(rv)) * 8) + (li & 1) * 4) * 2u;
     return off;
 }
 

@@ -122,16 +122,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void de
 #pragma unroll
     for (int i = 0; i < NS - 1; ++i)
         if (i < nch) {
-            load_stage<D>(Kh, D, kbeg + i * kDecT, N, k_lds + i * kStage, lane);
-            load_stage<D>(Vh, D, kbeg + i * kDecT, N, v_lds + i * kStage, lane);
+            load_stage<D, true>(Kh, D, kbeg + i * kDecT, N, k_lds + i * kStage, lane);
+            load_stage<D, false>(Vh, D, kbeg + i * kDecT, N, v_lds + i * kStage, lane);
         }
     int st = 0;   // stage of chunk ch
     for (int ch = 0; ch < nch; ++ch) {
         const int ahead = ch + NS - 1;
         if (ahead < nch) {
             const int sa = (st == 0) ? NS - 1 : st - 1;   // stage of chunk ch - 1, already consumed
-            load_stage<D>(Kh, D, kbeg + ahead * kDecT, N, k_lds + sa * kStage, lane);
-            load_stage<D>(Vh, D, kbeg + ahead * kDecT, N, v_lds + sa * kStage, lane);
+            load_stage<D, true>(Kh, D, kbeg + ahead * kDecT, N, k_lds + sa * kStage, lane);
+            load_stage<D, false>(Vh, D, kbeg + ahead * kDecT, N, v_lds + sa * kStage, lane);
         }
         wait_copies_younger<kCopies>(min(NS - 1, nch - 1 - ch));
         const char* Kt = (const char*)(k_lds + st * kStage);

@@ -66,8 +66,9 @@ struct PrefillArgs {
     float sc;         // log2(e) / sqrt(D)
 };
 
-// Issue the asynchronous copy of keys [k0, k0 + kBc) of one head into an LDS tile.
-template <int D, int W>
+// Issue the asynchronous copy of keys [k0, k0 + kBc) of one head into an LDS tile, chunks
+// placed by the K (kIsK) or the V swizzle.
+template <int D, int W, bool kIsK>
 __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ head, long long row_stride, int k0, int seqK,
                                           uint16_t* tile, int wave, int lane) {
     constexpr int CPR = D / 8;                       // 16-byte chunks per key row
@@ -78,7 +79,7 @@ __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ head, lon
         const int p0 = (j * W + wave) * 64;
         const int p = p0 + lane;
         const int r = p / CPR;
-        const int lc = (p % CPR) ^ swz<D>(r);
+        const int lc = (p % CPR) ^ swz<D, kIsK>(r);
         const int key = min(k0 + r, seqK - 1);   // rows past the end re-read the last key (masked)
         __builtin_amdgcn_global_load_lds((const void*)(head + key * row_stride + lc * 8),
                                          (LDS_AS void*)(tile + p0 * 8), 16, 0, 0);
@@ -197,8 +198,8 @@ __device__ __forceinline__ void tile_step(const uint16_t* __restrict__ kt, const
                                           f32x4 (&o)[QT][D / 16], float (&m)[QT], f32x4 (&lacc)[QT], int qw0,
                                           int wave, int lane, int li, int g) {
     if (load_next) {
-        load_tile<D, W>(Kh, a.k_rs, k0 + kBc, a.seqK, kn, wave, lane);
-        load_tile<D, W>(Vh, a.k_rs, k0 + kBc, a.seqK, vn, wave, lane);
+        load_tile<D, W, true>(Kh, a.k_rs, k0 + kBc, a.seqK, kn, wave, lane);
+        load_tile<D, W, false>(Vh, a.k_rs, k0 + kBc, a.seqK, vn, wave, lane);
     }
     if (!(a.causal && k0 > wave_qmax)) {
         const bool need_mask = (a.causal && k0 + kBc - 1 > qw0) || (k0 + kBc > a.seqK);
@@ -277,8 +278,8 @@ __global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
         if (a.causal) ntiles = min(ntiles, (min(q0 + BM, a.seqQ) - 1) / kBc + 1);
         const int wave_qmax = min(qw0 + QT * 16, a.seqQ) - 1;   // last real query of this wave
 
-        load_tile<D, W>(Kh, a.k_rs, 0, a.seqK, lds[0][0], wave, lane);
-        load_tile<D, W>(Vh, a.k_rs, 0, a.seqK, lds[0][1], wave, lane);
+        load_tile<D, W, true>(Kh, a.k_rs, 0, a.seqK, lds[0][0], wave, lane);
+        load_tile<D, W, false>(Vh, a.k_rs, 0, a.seqK, lds[0][1], wave, lane);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
 
