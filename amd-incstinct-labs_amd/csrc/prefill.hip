@@ -5,7 +5,7 @@
 // sqrt(D)) V per (batch, query head), query head h reads kv head h / (nQH / nKVH), causal
 // mask "key > query -> excluded", fp32 softmax and accumulation, O / l with an l > 0 guard.
 //
-// MI355X design of the f16 / bf16 kernel (fa_mfma):
+// MI355X design of the f16 / bf16 kernels (fa_pipe for large problems, fa_mfma for mid-size):
 //   * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_{f16,bf16}. In that orientation
 //     the S^T accumulator of a lane holds one query column (q = lane % 16) and 4 keys, so
 //     the softmax state (m, l) and the O^T accumulator of a query live in the same lanes:
@@ -14,18 +14,22 @@
 //     rows of each K operand tile are permuted (key = 8*(m/4) + 4*t + m%4 for A-row m of
 //     sub-tile t) so that the 8 keys a lane holds are the 8 consecutive keys its B operand
 //     needs.
-//   * The row max over a query's 64 keys spans the lane's own registers and the three
-//     other lanes that hold the same query (lanes q, q+16, q+32, q+48): two permlane swaps.
+//   * The row max over a query's keys spans the lane's own registers and the three other
+//     lanes that hold the same query (lanes q, q+16, q+32, q+48): two permlane swaps, only
+//     when some score exceeds the lazily kept reference maximum by more than kTau.
 //   * K and V tiles go HBM -> LDS with global_load_lds_dwordx4 (asynchronous, no VGPRs),
-//     double-buffered so tile i+1 streams in while tile i is on the matrix cores. The
-//     16-byte chunks of a key row are XOR-swizzled so the K operand reads (ds_read_b128,
-//     16 rows per lane group) and the V^T operand reads (ds_read_b64_tr_b16, 4 rows x 32
-//     bytes per lane group) are both free of bank conflicts.
+//     a tile or two ahead of their use (fa_mfma: two buffers; fa_pipe: a ring of three). The
+//     16-byte chunks of a key row are XOR-swizzled so the K operand reads (ds_read_b128) and
+//     the V^T operand reads (ds_read_b64_tr_b16) are both free of bank conflicts.
+//   * fa_pipe software-pipelines the key loop: the exponentials of one 32-key chunk are
+//     interleaved with the S^T MFMAs of the next, so VALU and matrix-core work overlap.
 //   * Q stays in VGPRs as B operands for the whole kernel; softmax is base-2 with a
 //     log2(e)-prescaled scale; causal blocks are issued heaviest first, with all q blocks
 //     of a (batch, head) on the same XCD so its K/V stay in that XCD's L2.
 // The fp32 kernel (fa_f32) serves the fp32 arm of the reference configuration (fp32 in and
 // out, accuracy 1e-4) on the fp32 matrix-core instruction (v_mfma_f32_16x16x4_f32).
+#include <type_traits>
+
 #include "attn_tile.hpp"
 #include "attn_stream.hpp"
 
@@ -311,6 +315,304 @@ __global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
     }
 }
 
+// ---- the 8-wave kernel: software-pipelined key loop (fa_pipe) -------------------------------
+// A wave walks its keys in 32-key chunks. Region j of the loop does, in one straight block:
+//   P_j = 2^(S_j sc - m) from s (S^T of chunk j, already masked and max-checked), packed into
+//   the P.V B operands, with the exponentials placed between the S^T MFMAs of chunk j + 1 (its
+//   K operand reads two ahead), so that the VALU work issues under matrix-core work instead of
+//   after it; then l += rowsum(P_j) and O^T += V^T P_j^T (V^T operand reads two ahead); then the
+//   max check of chunk j + 1 and, rarely, the rescale of O and l.
+// K/V tiles (64 keys) stream HBM -> LDS in a ring of three buffers, one workgroup barrier per
+// tile: region 2t reads tile t (S of chunk 2t + 1, P.V of chunk 2t); the barrier before region
+// 2t + 1 makes tile t + 1 visible and frees tile t - 1's buffer (last read by region 2t - 1),
+// which then receives the copy of tile t + 2; region 2t + 1 reads tiles t + 1 (S of chunk 2t + 2)
+// and t (P.V of chunk 2t + 1). The copies are inline assembly, so the compiler neither tracks nor
+// waits for them; the kernel waits with vmcnt before each barrier.
+// Tiles whose regions need no mask for any wave of the workgroup (keys below its first query,
+// and a full chunk ahead) run in a main loop unrolled over the three buffers (LDS offsets become
+// immediates); the remaining diagonal / ragged tiles run in a tail loop that masks every chunk
+// and lets each wave skip the chunks past its last query. Keeping the two loops apart keeps each
+// region one block: variants joined inside the loop made the register allocator copy the O
+// accumulators at every join.
+constexpr int kPipeBufs = 3;
+
+// Masks chunk scores s whose first key is kb: key >= seqK or (causal) key > query -> -inf.
+template <int QT>
+__device__ __forceinline__ void mask_chunk(f32x4 (&s)[QT][2], int kb, int qw0, int seqK, int causal, int li, int g) {
+#pragma unroll
+    for (int t = 0; t < QT; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int key = kb + g * 8 + u * 4 + e;
+                const int q = qw0 + t * 16 + li;
+                if (key >= seqK || (causal && key > q)) s[t][u][e] = -INFINITY;
+            }
+}
+
+// Region j (see above). Kn (K tile of chunk j + 1, half kcn) always points into the LDS ring;
+// when chunk j + 1 does not exist for this wave (has_next false, tail only) the scores formed
+// from it are ignored. Vc / kcc: V tile and half of chunk j. kTail: mask chunk j + 1.
+template <int D, int QT, bool kBf16, bool kTail>
+__device__ __forceinline__ void pipe_region(const char* Kn, int kcn, const char* Vc, int kcc, const LdsOffsets& off,
+                                           const u32x4 (&qb)[QT][D / 32], f32x4 (&s)[QT][2], f32x4 (&o)[QT][D / 16],
+                                           float (&m)[QT], f32x4 (&lacc)[QT], bool has_next, int kbn, int qw0,
+                                           int seqK, int causal, float sc, int li, int g) {
+    constexpr int NK = (D / 32) * 2;   // K operand reads (ds_read_b128) of chunk j + 1, i = 2c + u
+    constexpr int NV = D / 16;         // V^T operands of chunk j (two transpose reads each)
+    constexpr int NP = QT * 8;         // P_j values per lane
+    constexpr int SL = NP / NK;        // P values per interleave slot
+    constexpr int kAhead = 2;          // LDS operand reads issued ahead of their MFMAs
+    static_assert(NP % NK == 0 && SL % 2 == 0, "softmax slices must pair up for the packing");
+    float p[QT][8];
+    u32x4 pb[QT];
+    f32x4 sn[QT][2];
+    u32x4 ka[NK];
+    auto kread = [&](int i) {
+        ka[i] = *(const u32x4*)(Kn + off.kc(i >> 1) + (kcn * 32 + (i & 1) * 4) * D * 2);
+    };
+    auto soft = [&](int v) {   // P value v (query tile v / 8, element v % 8)
+        const int t = v >> 3, x = v & 7;
+        p[t][x] = __builtin_amdgcn_exp2f(fmaf(s[t][x >> 2][x & 3], sc, -m[t]));
+        if (x & 1) pb[t][x >> 1] = pack2<kBf16>(p[t][x - 1], p[t][x]);
+    };
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) kread(i);
+#pragma unroll
+    for (int t = 0; t < QT; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) sn[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // S^T of chunk j + 1, one K operand (QT MFMAs) per slot, SL values of P_j per slot. The
+    // scheduling barriers keep the slots in this order.
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < QT; ++t) sn[t][i & 1] = mfma<kBf16>(ka[i], qb[t][i >> 1], sn[t][i & 1]);
+        if (i + kAhead < NK) kread(i + kAhead);
+#pragma unroll
+        for (int v = 0; v < SL; ++v) soft(i * SL + v);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 va[NV];
+    auto vread = [&](int dt) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS s16x4*)(Vc + off.vd(dt) + (kcc * 32) * D * 2));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS s16x4*)(Vc + off.vd(dt) + (kcc * 32 + 4) * D * 2));
+        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+        va[dt] = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
+    };
+#pragma unroll
+    for (int dt = 0; dt < kAhead; ++dt) vread(dt);
+    // l += row sums of exactly the rounded weights the product uses (all-ones A operand)
+    const uint32_t one2 = kBf16 ? 0x3F803F80u : 0x3C003C00u;
+#pragma unroll
+    for (int t = 0; t < QT; ++t) lacc[t] = mfma<kBf16>(u32x4{one2, one2, one2, one2}, pb[t], lacc[t]);
+#pragma unroll
+    for (int dt = 0; dt < NV; ++dt) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < QT; ++t) o[t][dt] = mfma<kBf16>(va[dt], pb[t], o[t][dt]);
+        if (dt + kAhead < NV) vread(dt + kAhead);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kTail) mask_chunk<QT>(sn, kbn, qw0, seqK, causal, li, g);
+    float lm[QT];
+    bool need = check_chunk<QT, false>(sn, m, lm, kbn, qw0, seqK, causal, sc, li, g);
+    if constexpr (kTail) need = need && has_next;
+#pragma unroll
+    for (int t = 0; t < QT; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) s[t][u] = sn[t][u];
+    if (__builtin_amdgcn_ballot_w64(need)) rescale_rows<D, QT>(lm, m, o, lacc, sc);
+}
+
+// Asynchronous copy of keys [k0, k0 + kBc) of one head into an LDS tile (inline assembly, see
+// stream::dma16), chunks placed by the K (kIsK) or the V swizzle.
+template <int D, int W, bool kIsK>
+__device__ __forceinline__ void copy_tile(const uint16_t* __restrict__ head, long long row_stride, int k0, int seqK,
+                                          uint16_t* tile, int wave, int lane) {
+    constexpr int CPR = D / 8;
+    constexpr int NI = kBc * CPR / (64 * W);
+    static_assert(NI >= 1 && NI * 64 * W == kBc * CPR, "tile copy must split evenly over the waves");
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        const int p0 = (j * W + wave) * 64;
+        const int p = p0 + lane;
+        const int r = p / CPR;
+        const int lc = (p % CPR) ^ swz<D, kIsK>(r);
+        const int key = min(k0 + r, seqK - 1);   // rows past the end re-read the last key (masked)
+        stream::dma16(head + key * row_stride + lc * 8, tile + p0 * 8);
+    }
+}
+
+// Work item of a persistent workgroup: item = round * gridDim.x + position. With xcd_map (grid
+// and batch * heads multiples of 8) the XCD of position p is p % 8 and it owns heads x, x + 8, ...;
+// the G = grid / 8 workgroups of an XCD take, in round r, G consecutive entries of that XCD's
+// head-major, heaviest-first item list (so they share one or a few heads' K/V in the XCD's L2),
+// and take them in reverse order on odd rounds, so that a workgroup that drew a heavy causal q
+// block in one round draws a light one in the next whatever the ratio of q blocks per head to G.
+// Without xcd_map: heads vary fastest, q blocks heaviest first.
+__device__ __forceinline__ void persistent_item(int item, int nqb, int nbh, int xcd_map, int& bh, int& qrev) {
+    if (xcd_map) {
+        const int grid = (int)gridDim.x;
+        const int r = item / grid, p = item - r * grid;
+        const int xcd = p & 7, sp = p >> 3, G = grid >> 3;
+        const int K = min(G, ((nbh * nqb) >> 3) - r * G);   // this round's entries per XCD
+        const int idx = r * G + ((r & 1) ? K - 1 - sp : sp);
+        bh = (idx / nqb) * 8 + xcd;
+        qrev = idx % nqb;
+    } else {
+        bh = item % nbh;
+        qrev = item / nbh;
+    }
+}
+
+template <int D, int W, int QT, bool kBf16>
+__global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
+    constexpr int ND = D / 32;
+    constexpr int NDT = D / 16;
+    constexpr int BM = W * QT * 16;
+    constexpr int NB = kPipeBufs;
+    constexpr int kTile = kBc * D;                              // elements of one K (or V) tile
+    constexpr int kCopies = 2 * (kBc * (D / 8) / (64 * W));     // copy instructions per tile per wave
+    __shared__ __attribute__((aligned(16))) uint16_t lds[NB * 2 * kTile];   // [buffer][K|V][tile]
+
+    const int lane = (int)(threadIdx.x & 63u);
+    // wave-uniform as far as the compiler knows too, so that branches on it stay scalar
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int li = lane & 15, g = lane >> 4;
+
+    const int nbh = a.batch * a.nQH;
+    const int nitems = nbh * a.nqb;
+    for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+        int bh, qrev;
+        persistent_item(item, a.nqb, nbh, a.xcd_map, bh, qrev);
+        const int qblk = a.causal ? (a.nqb - 1 - qrev) : qrev;
+        const int b = bh / a.nQH, h = bh % a.nQH;
+        const int kvh = h / (a.nQH / a.nKVH);
+        const int q0 = qblk * BM;
+        const int qw0 = q0 + wave * QT * 16;   // first query row of this wave
+
+        const uint16_t* Kh = a.K + b * a.k_bs + kvh * a.k_hs;
+        const uint16_t* Vh = a.V + b * a.k_bs + kvh * a.k_hs;
+        const uint16_t* Qh = a.Q + b * a.q_bs + h * a.q_hs;
+
+        // Q as B operands: lane holds Q[q = qw0 + t*16 + li][32*c + 8*g .. +8].
+        u32x4 qb[QT][ND];
+#pragma unroll
+        for (int t = 0; t < QT; ++t) {
+            const int q = min(qw0 + t * 16 + li, a.seqQ - 1);
+#pragma unroll
+            for (int c = 0; c < ND; ++c) qb[t][c] = *(const u32x4*)(Qh + q * a.q_rs + c * 32 + g * 8);
+        }
+        f32x4 o[QT][NDT], lacc[QT];
+        float m[QT];
+#pragma unroll
+        for (int t = 0; t < QT; ++t) {
+            m[t] = kInitM;
+            lacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int d = 0; d < NDT; ++d) o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+
+        int ntiles = (a.seqK + kBc - 1) / kBc;
+        if (a.causal) ntiles = min(ntiles, (min(q0 + BM, a.seqQ) - 1) / kBc + 1);
+        // Main tiles t < t_main: for every wave, chunks 2t + 1 and 2t + 2 (whose scores tile t's
+        // regions form) lie below the workgroup's first query and a full chunk inside seqK.
+        int t_main = a.seqK >= 96 ? (a.seqK - 96) / 64 + 1 : 0;
+        if (a.causal) t_main = min(t_main, q0 >= 95 ? (q0 - 95) / 64 + 1 : 0);
+        t_main = min(t_main, ntiles);
+        const int wave_qmax = min(qw0 + QT * 16, a.seqQ) - 1;   // last real query of this wave
+        const int kend = a.causal ? min(a.seqK, wave_qmax + 1) : a.seqK;
+        const int nch = (kend + 31) / 32;                        // this wave's chunks (>= 1)
+
+        // tiles 0 .. NB - 2 in flight; issued after the Q loads, so vmcnt counts them last
+#pragma unroll
+        for (int i = 0; i < NB - 1; ++i)
+            if (i < ntiles) {
+                copy_tile<D, W, true>(Kh, a.k_rs, i * kBc, a.seqK, lds + i * 2 * kTile, wave, lane);
+                copy_tile<D, W, false>(Vh, a.k_rs, i * kBc, a.seqK, lds + i * 2 * kTile + kTile, wave, lane);
+            }
+        if (ntiles > 1) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(kCopies) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+        __syncthreads();
+        const LdsOffsets off = lds_offsets<D>(li, g);
+
+        // S^T of chunk 0, its mask and max check (the first check always sets m)
+        f32x4 s[QT][2];
+        qk_chunk<D, QT, kBf16>((const char*)lds, off, qb, s, 0);
+        {
+            float lm[QT];
+            if (32 > a.seqK || (a.causal && 31 > qw0)) mask_chunk<QT>(s, 0, qw0, a.seqK, a.causal, li, g);
+            if (__builtin_amdgcn_ballot_w64(check_chunk<QT, false>(s, m, lm, 0, qw0, a.seqK, a.causal, a.sc, li, g)))
+                rescale_rows<D, QT>(lm, m, o, lacc, a.sc);
+        }
+
+        // tile t sits in buffer bc = t % NB (a literal in the unrolled main loop)
+        auto tile_iter = [&](int t, auto tail, int bc) {
+            constexpr bool kTail = decltype(tail)::value;
+            const int bn = bc == NB - 1 ? 0 : bc + 1;   // buffer of tile t + 1
+            const char* Kt = (const char*)(lds + bc * 2 * kTile);
+            const char* Vt = (const char*)(lds + bc * 2 * kTile + kTile);
+            const char* Kn = (const char*)(lds + bn * 2 * kTile);
+            // region 2t: P of chunk 2t, S of chunk 2t + 1 (this tile, keys 32..63), P.V of chunk 2t
+            const int j0 = 2 * t;
+            if (!kTail)
+                pipe_region<D, QT, kBf16, false>(Kt, 1, Vt, 0, off, qb, s, o, m, lacc, true, (j0 + 1) * 32, qw0, a.seqK,
+                                                 a.causal, a.sc, li, g);
+            else if (j0 < nch)
+                pipe_region<D, QT, kBf16, true>(Kt, 1, Vt, 0, off, qb, s, o, m, lacc, j0 + 1 < nch, (j0 + 1) * 32, qw0,
+                                                a.seqK, a.causal, a.sc, li, g);
+            if (!kTail || t + 1 < ntiles) {
+                // tile t + 1 landed and is visible; every wave is past region 2t - 1, the last reader
+                // of tile t - 1's buffer, which now receives tile t + 2
+                asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+                __syncthreads();
+                if (t + 2 < ntiles) {
+                    const int bf = bc == 0 ? NB - 1 : bc - 1;
+                    copy_tile<D, W, true>(Kh, a.k_rs, (t + 2) * kBc, a.seqK, lds + bf * 2 * kTile, wave, lane);
+                    copy_tile<D, W, false>(Vh, a.k_rs, (t + 2) * kBc, a.seqK, lds + bf * 2 * kTile + kTile, wave, lane);
+                }
+            }
+            // region 2t + 1: P of chunk 2t + 1, S of chunk 2t + 2 (tile t + 1, keys 0..31), P.V of
+            // chunk 2t + 1; past the last tile Kn is a stale buffer whose scores are ignored
+            const int j1 = 2 * t + 1;
+            if (!kTail)
+                pipe_region<D, QT, kBf16, false>(Kn, 0, Vt, 1, off, qb, s, o, m, lacc, true, (j1 + 1) * 32, qw0, a.seqK,
+                                                 a.causal, a.sc, li, g);
+            else if (j1 < nch)
+                pipe_region<D, QT, kBf16, true>(Kn, 0, Vt, 1, off, qb, s, o, m, lacc, j1 + 1 < nch, (j1 + 1) * 32, qw0,
+                                                a.seqK, a.causal, a.sc, li, g);
+        };
+        int t = 0;
+        for (; t + NB <= t_main; t += NB) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) tile_iter(t + i, std::false_type{}, i);
+        }
+        for (; t < t_main; ++t) tile_iter(t, std::false_type{}, t % NB);
+        for (; t < ntiles; ++t) tile_iter(t, std::true_type{}, t % NB);
+
+        // ---- O = O^T / l: lane holds d = 16dt + 4g + e of query li, and its query's full l.
+        uint16_t* Oh = a.O + b * a.o_bs + h * a.o_hs;
+#pragma unroll
+        for (int t = 0; t < QT; ++t) {
+            const float lt = lacc[t][0];
+            const float inv = (lt > 0.f) ? 1.f / lt : 1.f;
+            const int q = qw0 + t * 16 + li;
+            if (q < a.seqQ) {
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const u32x2 w = u32x2{pack2<kBf16>(o[t][dt][0] * inv, o[t][dt][1] * inv),
+                                          pack2<kBf16>(o[t][dt][2] * inv, o[t][dt][3] * inv)};
+                    *(u32x2*)(Oh + q * a.o_rs + dt * 16 + g * 4) = w;
+                }
+            }
+        }
+        __syncthreads();   // every wave is done with the LDS ring before the next item's copies
+    }
+}
+
 // ---- fp32 arm on the matrix cores -------------------------------------------------------
 // v_mfma_f32_16x16x4_f32 multiplies and accumulates in fp32. Lane L holds A[L % 16][L / 16],
 // B[L / 16][L % 16] and C[4 (L / 16) + i][L % 16], i < 4 (cdna4::mfma::*_16x16x4f32 and its exact
@@ -581,7 +883,7 @@ int dispatch_mfma(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& st, c
     switch (p.kernel) {
         case CDNA4_KERNEL_PREFILL_MFMA_8W:
             a.xcd_map = (nbh % 8 == 0) ? 1 : 0;
-            fa_mfma<D, 8, 2, kBf16><<<(unsigned)p.grid, 64 * 8, 0, s>>>(a);
+            fa_pipe<D, 8, 2, kBf16><<<(unsigned)p.grid, 64 * 8, 0, s>>>(a);
             break;
         case CDNA4_KERNEL_PREFILL_MFMA_4W:
             a.xcd_map = (nbh % 8 == 0) ? 1 : 0;

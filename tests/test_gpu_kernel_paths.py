@@ -70,7 +70,7 @@ def check_prefill(D, SQ, SK, HQ, HK, B, causal, dtype, kernel, seed=0, heads=Non
     assert worst <= tolerance(dtype)
 
 
-# ---- fa_mfma<D, 8, 2>: batch * heads * ceil(seqQ / 256) >= 512 --------------------------------
+# ---- fa_pipe<D, 8, 2> (plan name fa_mfma_8w): batch * heads * ceil(seqQ / 256) >= 512 ----------
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_fa_mfma_8w_d128_causal_mha(dtype):
@@ -106,6 +106,20 @@ def test_fa_mfma_8w_ragged_cross_attention():
     # the item mapping without the XCD grouping).
     check_prefill(64, 4096 + 37, 3001, 36, 9, 1, 0, torch.float16, "fa_mfma_8w", seed=6,
                   heads=[(0, 0), (0, 4), (0, 20), (0, 35)])
+
+
+def test_fa_pipe_partial_odd_round():
+    # 4 x 32 heads x 7 q blocks = 896 items: with 256 CUs each XCD holds 112 = 3 x 32 + 16 of them,
+    # so the persistent grid's last round is partial and odd (taken in reverse over 16 entries).
+    check_prefill(128, 1700, 1700, 32, 32, 4, 1, torch.bfloat16, "fa_mfma_8w", seed=11,
+                  heads=[(0, 0), (1, 9), (2, 18), (3, 31)])
+
+
+@pytest.mark.parametrize("SK", [1, 50, 95, 96, 97])
+def test_fa_pipe_short_keys(SK):
+    # Fewer keys than the pipelined main loop needs (t_main = 0 below 96): every tile in the tail.
+    check_prefill(128, 4096, SK, 32, 32, 1, 0, torch.float16, "fa_mfma_8w", seed=12 + SK,
+                  heads=[(0, 0), (0, 13), (0, 31)])
 
 
 # ---- fa_mfma<D, 4, 1>: mid-size problems --------------------------------------------------------
