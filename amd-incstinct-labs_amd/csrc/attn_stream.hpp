@@ -21,6 +21,13 @@ __device__ __forceinline__ void dma16(const void* gsrc, const void* lds_dst) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "{m0}"(base) : "memory");
 }
 
+// The same copy from a wave-uniform base (SGPR pair) plus a 32-bit per-lane byte offset: no
+// per-copy 64-bit address arithmetic in the vector ALU.
+__device__ __forceinline__ void dma16_s(const void* sbase, uint32_t voff, const void* lds_dst) {
+    const uint32_t base = (uint32_t)(uintptr_t)(const tile::LDS_AS_T*)lds_dst;
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(base) : "memory");
+}
+
 // Wait until at most Y of this wave's newest copy groups (kCopies copies each) are in flight.
 template <int kCopies>
 __device__ __forceinline__ void wait_copies_younger(int y) {

@@ -67,6 +67,7 @@ struct PrefillArgs {
     int seqQ, seqK, nQH, nKVH, batch, causal;
     int nqb;          // q blocks per (batch, head)
     int xcd_map;      // 1: all q blocks of a (batch, head) on one XCD, heads in sequence
+    int copy32;       // 1: a K/V tile's rows span < 4 GiB (32-bit per-lane copy offsets)
     float sc;         // log2(e) / sqrt(D)
 };
 
@@ -385,6 +386,9 @@ __device__ __forceinline__ void pipe_region(const char* Kn, int kcn, const char*
         for (int u = 0; u < 2; ++u) sn[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
     // S^T of chunk j + 1, one K operand (QT MFMAs) per slot, SL values of P_j per slot. The
     // scheduling barriers keep the slots in this order.
+    // Wave priority 2 here, 1 for the P.V part, 0 for the check and the copies between regions:
+    // measured +1.7 to +2.7 % on the causal B4 H32 S8192 D128 prefill over equal priorities.
+    __builtin_amdgcn_s_setprio(2);
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
         __builtin_amdgcn_sched_barrier(0);
@@ -404,6 +408,7 @@ __device__ __forceinline__ void pipe_region(const char* Kn, int kcn, const char*
     };
 #pragma unroll
     for (int dt = 0; dt < kAhead; ++dt) vread(dt);
+    __builtin_amdgcn_s_setprio(1);
     // l += row sums of exactly the rounded weights the product uses (all-ones A operand)
     const uint32_t one2 = kBf16 ? 0x3F803F80u : 0x3C003C00u;
 #pragma unroll
@@ -416,6 +421,7 @@ __device__ __forceinline__ void pipe_region(const char* Kn, int kcn, const char*
         if (dt + kAhead < NV) vread(dt + kAhead);
     }
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
     if constexpr (kTail) mask_chunk<QT>(sn, kbn, qw0, seqK, causal, li, g);
     float lm[QT];
     bool need = check_chunk<QT, false>(sn, m, lm, kbn, qw0, seqK, causal, sc, li, g);
@@ -444,6 +450,34 @@ __device__ __forceinline__ void copy_tile(const uint16_t* __restrict__ head, lon
         const int key = min(k0 + r, seqK - 1);   // rows past the end re-read the last key (masked)
         stream::dma16(head + key * row_stride + lc * 8, tile + p0 * 8);
     }
+}
+
+// Per-lane byte offsets of the copy of a full tile (row r, swizzled 16-byte chunk lc), the same for
+// every tile of a head, so formed once per work item: a full tile's copies then need only a
+// wave-uniform base (stream::dma16_s).
+template <int D, int W, bool kIsK>
+__device__ __forceinline__ void copy_offsets(long long row_stride, int wave, int lane,
+                                             uint32_t (&voff)[kBc * (D / 8) / (64 * W)]) {
+    constexpr int CPR = D / 8;
+    constexpr int NI = kBc * CPR / (64 * W);
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        const int p = (j * W + wave) * 64 + lane;
+        const int r = p / CPR;
+        const int lc = (p % CPR) ^ swz<D, kIsK>(r);
+        voff[j] = (uint32_t)(((long long)r * row_stride + lc * 8) * 2);
+    }
+}
+
+// Copy of keys [k0, k0 + kBc), all inside the sequence, with the offsets above.
+template <int D, int W>
+__device__ __forceinline__ void copy_tile_full(const uint16_t* head, long long row_stride, int k0,
+                                               const uint32_t (&voff)[kBc * (D / 8) / (64 * W)], uint16_t* tile,
+                                               int wave) {
+    constexpr int NI = kBc * (D / 8) / (64 * W);
+    const uint16_t* base = head + (long long)k0 * row_stride;
+#pragma unroll
+    for (int j = 0; j < NI; ++j) stream::dma16_s(base, voff[j], tile + (j * W + wave) * 64 * 8);
 }
 
 // Work item of a persistent workgroup: item = round * gridDim.x + position. With xcd_map (grid
@@ -527,13 +561,24 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
         const int kend = a.causal ? min(a.seqK, wave_qmax + 1) : a.seqK;
         const int nch = (kend + 31) / 32;                        // this wave's chunks (>= 1)
 
+        constexpr int NI = kBc * (D / 8) / (64 * W);
+        uint32_t koff[NI], voff[NI];
+        copy_offsets<D, W, true>(a.k_rs, wave, lane, koff);
+        copy_offsets<D, W, false>(a.k_rs, wave, lane, voff);
+        auto copy = [&](int tt, int buf) {   // K and V of tile tt into LDS buffer buf
+            uint16_t* kd = lds + buf * 2 * kTile;
+            if (a.copy32 && (tt + 1) * kBc <= a.seqK) {
+                copy_tile_full<D, W>(Kh, a.k_rs, tt * kBc, koff, kd, wave);
+                copy_tile_full<D, W>(Vh, a.k_rs, tt * kBc, voff, kd + kTile, wave);
+            } else {
+                copy_tile<D, W, true>(Kh, a.k_rs, tt * kBc, a.seqK, kd, wave, lane);
+                copy_tile<D, W, false>(Vh, a.k_rs, tt * kBc, a.seqK, kd + kTile, wave, lane);
+            }
+        };
         // tiles 0 .. NB - 2 in flight; issued after the Q loads, so vmcnt counts them last
 #pragma unroll
         for (int i = 0; i < NB - 1; ++i)
-            if (i < ntiles) {
-                copy_tile<D, W, true>(Kh, a.k_rs, i * kBc, a.seqK, lds + i * 2 * kTile, wave, lane);
-                copy_tile<D, W, false>(Vh, a.k_rs, i * kBc, a.seqK, lds + i * 2 * kTile + kTile, wave, lane);
-            }
+            if (i < ntiles) copy(i, i);
         if (ntiles > 1) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(kCopies) : "memory");
         else asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
         __syncthreads();
@@ -569,11 +614,7 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
                 // of tile t - 1's buffer, which now receives tile t + 2
                 asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
                 __syncthreads();
-                if (t + 2 < ntiles) {
-                    const int bf = bc == 0 ? NB - 1 : bc - 1;
-                    copy_tile<D, W, true>(Kh, a.k_rs, (t + 2) * kBc, a.seqK, lds + bf * 2 * kTile, wave, lane);
-                    copy_tile<D, W, false>(Vh, a.k_rs, (t + 2) * kBc, a.seqK, lds + bf * 2 * kTile + kTile, wave, lane);
-                }
+                if (t + 2 < ntiles) copy(t + 2, bc == 0 ? NB - 1 : bc - 1);
             }
             // region 2t + 1: P of chunk 2t + 1, S of chunk 2t + 2 (tile t + 1, keys 0..31), P.V of
             // chunk 2t + 1; past the last tile Kn is a stale buffer whose scores are ignored
@@ -869,6 +910,7 @@ PrefillArgs make_args(const cdna3_prefill_cfg& c, const cdna3_prefill_strides& s
     a.causal = c.causal ? 1 : 0;
     a.nqb = (c.seqQ + rows - 1) / rows;
     a.xcd_map = 0;
+    a.copy32 = (long long)kBc * st.kv_row * 2 < (1LL << 32) ? 1 : 0;
     a.sc = kLog2e / sqrtf((float)c.D);
     return a;
 }
