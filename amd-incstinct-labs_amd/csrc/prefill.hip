@@ -352,14 +352,43 @@ __device__ __forceinline__ void mask_chunk(f32x4 (&s)[QT][2], int kb, int qw0, i
             }
 }
 
+// Per-lane raw maxima lm of a chunk and whether one exceeds its query's threshold thr = (m + kTau)
+// / sc, i.e. whether a scaled score exceeds the reference maximum by more than kTau (the
+// threshold is kept in raw score units so that the check per chunk needs no multiply).
+template <int QT>
+__device__ __forceinline__ bool check_raw(const f32x4 (&s)[QT][2], const float (&thr)[QT], float (&lm)[QT]) {
+    bool need = false;
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+        float v = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v = fmaxf(v, s[t][u][e]);
+        lm[t] = v;
+        need |= v > thr[t];
+    }
+    return need;
+}
+
+// rescale_rows, then the thresholds of the new reference maxima.
+template <int D, int QT>
+__device__ __forceinline__ void rescale_pipe(const float (&lm)[QT], float (&m)[QT], float (&thr)[QT],
+                                             f32x4 (&o)[QT][D / 16], f32x4 (&lacc)[QT], float sc, float inv_sc) {
+    rescale_rows<D, QT>(lm, m, o, lacc, sc);
+#pragma unroll
+    for (int t = 0; t < QT; ++t) thr[t] = (m[t] + kTau) * inv_sc;
+}
+
 // Region j (see above). Kn (K tile of chunk j + 1, half kcn) always points into the LDS ring;
 // when chunk j + 1 does not exist for this wave (has_next false, tail only) the scores formed
 // from it are ignored. Vc / kcc: V tile and half of chunk j. kTail: mask chunk j + 1.
 template <int D, int QT, bool kBf16, bool kTail>
 __device__ __forceinline__ void pipe_region(const char* Kn, int kcn, const char* Vc, int kcc, const LdsOffsets& off,
                                            const u32x4 (&qb)[QT][D / 32], f32x4 (&s)[QT][2], f32x4 (&o)[QT][D / 16],
-                                           float (&m)[QT], f32x4 (&lacc)[QT], bool has_next, int kbn, int qw0,
-                                           int seqK, int causal, float sc, int li, int g) {
+                                           float (&m)[QT], float (&thr)[QT], f32x4 (&lacc)[QT], const u32x4& ones,
+                                           bool has_next, int kbn, int qw0, int seqK, int causal, float sc,
+                                           float inv_sc, int li, int g) {
     constexpr int NK = (D / 32) * 2;   // K operand reads (ds_read_b128) of chunk j + 1, i = 2c + u
     constexpr int NV = D / 16;         // V^T operands of chunk j (two transpose reads each)
     constexpr int NP = QT * 8;         // P_j values per lane
@@ -410,9 +439,8 @@ __device__ __forceinline__ void pipe_region(const char* Kn, int kcn, const char*
     for (int dt = 0; dt < kAhead; ++dt) vread(dt);
     __builtin_amdgcn_s_setprio(1);
     // l += row sums of exactly the rounded weights the product uses (all-ones A operand)
-    const uint32_t one2 = kBf16 ? 0x3F803F80u : 0x3C003C00u;
 #pragma unroll
-    for (int t = 0; t < QT; ++t) lacc[t] = mfma<kBf16>(u32x4{one2, one2, one2, one2}, pb[t], lacc[t]);
+    for (int t = 0; t < QT; ++t) lacc[t] = mfma<kBf16>(ones, pb[t], lacc[t]);
 #pragma unroll
     for (int dt = 0; dt < NV; ++dt) {
         __builtin_amdgcn_sched_barrier(0);
@@ -424,13 +452,13 @@ __device__ __forceinline__ void pipe_region(const char* Kn, int kcn, const char*
     __builtin_amdgcn_s_setprio(0);
     if constexpr (kTail) mask_chunk<QT>(sn, kbn, qw0, seqK, causal, li, g);
     float lm[QT];
-    bool need = check_chunk<QT, false>(sn, m, lm, kbn, qw0, seqK, causal, sc, li, g);
+    bool need = check_raw<QT>(sn, thr, lm);
     if constexpr (kTail) need = need && has_next;
 #pragma unroll
     for (int t = 0; t < QT; ++t)
 #pragma unroll
         for (int u = 0; u < 2; ++u) s[t][u] = sn[t][u];
-    if (__builtin_amdgcn_ballot_w64(need)) rescale_rows<D, QT>(lm, m, o, lacc, sc);
+    if (__builtin_amdgcn_ballot_w64(need)) rescale_pipe<D, QT>(lm, m, thr, o, lacc, sc, inv_sc);
 }
 
 // Asynchronous copy of keys [k0, k0 + kBc) of one head into an LDS tile (inline assembly, see
@@ -541,10 +569,12 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
             for (int c = 0; c < ND; ++c) qb[t][c] = *(const u32x4*)(Qh + q * a.q_rs + c * 32 + g * 8);
         }
         f32x4 o[QT][NDT], lacc[QT];
-        float m[QT];
+        float m[QT], thr[QT];
+        const float inv_sc = 1.f / a.sc;
 #pragma unroll
         for (int t = 0; t < QT; ++t) {
             m[t] = kInitM;
+            thr[t] = (kInitM + kTau) * inv_sc;
             lacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int d = 0; d < NDT; ++d) o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -590,8 +620,15 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
         {
             float lm[QT];
             if (32 > a.seqK || (a.causal && 31 > qw0)) mask_chunk<QT>(s, 0, qw0, a.seqK, a.causal, li, g);
-            if (__builtin_amdgcn_ballot_w64(check_chunk<QT, false>(s, m, lm, 0, qw0, a.seqK, a.causal, a.sc, li, g)))
-                rescale_rows<D, QT>(lm, m, o, lacc, a.sc);
+            if (__builtin_amdgcn_ballot_w64(check_raw<QT>(s, thr, lm)))
+                rescale_pipe<D, QT>(lm, m, thr, o, lacc, a.sc, inv_sc);
+        }
+        // the all-ones A operand of the row-sum MFMA, held in registers for the whole item
+        u32x4 ones;
+        {
+            const uint32_t one2 = kBf16 ? 0x3F803F80u : 0x3C003C00u;
+            ones = u32x4{one2, one2, one2, one2};
+            asm volatile("" : "+v"(ones));
         }
 
         // tile t sits in buffer bc = t % NB (a literal in the unrolled main loop)
@@ -604,11 +641,11 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
             // region 2t: P of chunk 2t, S of chunk 2t + 1 (this tile, keys 32..63), P.V of chunk 2t
             const int j0 = 2 * t;
             if (!kTail)
-                pipe_region<D, QT, kBf16, false>(Kt, 1, Vt, 0, off, qb, s, o, m, lacc, true, (j0 + 1) * 32, qw0, a.seqK,
-                                                 a.causal, a.sc, li, g);
+                pipe_region<D, QT, kBf16, false>(Kt, 1, Vt, 0, off, qb, s, o, m, thr, lacc, ones, true, (j0 + 1) * 32, qw0,
+                                                 a.seqK, a.causal, a.sc, inv_sc, li, g);
             else if (j0 < nch)
-                pipe_region<D, QT, kBf16, true>(Kt, 1, Vt, 0, off, qb, s, o, m, lacc, j0 + 1 < nch, (j0 + 1) * 32, qw0,
-                                                a.seqK, a.causal, a.sc, li, g);
+                pipe_region<D, QT, kBf16, true>(Kt, 1, Vt, 0, off, qb, s, o, m, thr, lacc, ones, j0 + 1 < nch, (j0 + 1) * 32,
+                                                qw0, a.seqK, a.causal, a.sc, inv_sc, li, g);
             if (!kTail || t + 1 < ntiles) {
                 // tile t + 1 landed and is visible; every wave is past region 2t - 1, the last reader
                 // of tile t - 1's buffer, which now receives tile t + 2
@@ -620,11 +657,11 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
             // chunk 2t + 1; past the last tile Kn is a stale buffer whose scores are ignored
             const int j1 = 2 * t + 1;
             if (!kTail)
-                pipe_region<D, QT, kBf16, false>(Kn, 0, Vt, 1, off, qb, s, o, m, lacc, true, (j1 + 1) * 32, qw0, a.seqK,
-                                                 a.causal, a.sc, li, g);
+                pipe_region<D, QT, kBf16, false>(Kn, 0, Vt, 1, off, qb, s, o, m, thr, lacc, ones, true, (j1 + 1) * 32, qw0,
+                                                 a.seqK, a.causal, a.sc, inv_sc, li, g);
             else if (j1 < nch)
-                pipe_region<D, QT, kBf16, true>(Kn, 0, Vt, 1, off, qb, s, o, m, lacc, j1 + 1 < nch, (j1 + 1) * 32, qw0,
-                                                a.seqK, a.causal, a.sc, li, g);
+                pipe_region<D, QT, kBf16, true>(Kn, 0, Vt, 1, off, qb, s, o, m, thr, lacc, ones, j1 + 1 < nch, (j1 + 1) * 32,
+                                                qw0, a.seqK, a.causal, a.sc, inv_sc, li, g);
         };
         int t = 0;
         for (; t + NB <= t_main; t += NB) {
