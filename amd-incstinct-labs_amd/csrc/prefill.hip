@@ -380,15 +380,30 @@ __device__ __forceinline__ void rescale_pipe(const float (&lm)[QT], float (&m)[Q
     for (int t = 0; t < QT; ++t) thr[t] = (m[t] + kTau) * inv_sc;
 }
 
+// The copy of one full K/V tile a region issues between its MFMAs (kCopy): global bases of the
+// tile's K and V rows, their LDS buffers, and the per-lane offsets of copy_offsets.
+template <int NI>
+struct TileCopy {
+    const uint16_t* kg; const uint16_t* vg;
+    uint16_t* kd; uint16_t* vd;
+    const uint32_t* koff; const uint32_t* voff;
+    int wave, W;
+    __device__ __forceinline__ void issue(int c) const {   // copy c of 2 NI: K parts, then V parts
+        const int j = c % NI;
+        if (c < NI) stream::dma16_s(kg, koff[j], kd + (j * W + wave) * 64 * 8);
+        else stream::dma16_s(vg, voff[j], vd + (j * W + wave) * 64 * 8);
+    }
+};
+
 // Region j (see above). Kn (K tile of chunk j + 1, half kcn) always points into the LDS ring;
 // when chunk j + 1 does not exist for this wave (has_next false, tail only) the scores formed
 // from it are ignored. Vc / kcc: V tile and half of chunk j. kTail: mask chunk j + 1.
-template <int D, int QT, bool kBf16, bool kTail>
+template <int D, int QT, bool kBf16, bool kTail, bool kCopy, int NI>
 __device__ __forceinline__ void pipe_region(const char* Kn, int kcn, const char* Vc, int kcc, const LdsOffsets& off,
                                            const u32x4 (&qb)[QT][D / 32], f32x4 (&s)[QT][2], f32x4 (&o)[QT][D / 16],
                                            float (&m)[QT], float (&thr)[QT], f32x4 (&lacc)[QT], const u32x4& ones,
                                            bool has_next, int kbn, int qw0, int seqK, int causal, float sc,
-                                           float inv_sc, int li, int g) {
+                                           float inv_sc, int li, int g, const TileCopy<NI>& cp) {
     constexpr int NK = (D / 32) * 2;   // K operand reads (ds_read_b128) of chunk j + 1, i = 2c + u
     constexpr int NV = D / 16;         // V^T operands of chunk j (two transpose reads each)
     constexpr int NP = QT * 8;         // P_j values per lane
@@ -424,6 +439,12 @@ __device__ __forceinline__ void pipe_region(const char* Kn, int kcn, const char*
 #pragma unroll
         for (int t = 0; t < QT; ++t) sn[t][i & 1] = mfma<kBf16>(ka[i], qb[t][i >> 1], sn[t][i & 1]);
         if (i + kAhead < NK) kread(i + kAhead);
+        // one copy of the next-but-one tile per odd slot (NK / 2 = 2 NI slots): the waves' copies
+        // then reach the texture unit spread over the region instead of all after the barrier
+        if constexpr (kCopy) {
+            static_assert(NK / 2 == 2 * NI, "one copy per odd slot");
+            if (i & 1) cp.issue(i >> 1);
+        }
 #pragma unroll
         for (int v = 0; v < SL; ++v) soft(i * SL + v);
     }
@@ -587,6 +608,10 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
         int t_main = a.seqK >= 96 ? (a.seqK - 96) / 64 + 1 : 0;
         if (a.causal) t_main = min(t_main, q0 >= 95 ? (q0 - 95) / 64 + 1 : 0);
         t_main = min(t_main, ntiles);
+        // the main loop's second regions copy tile t + 2 between their MFMAs, so it runs only while
+        // that tile exists and is full (and the 32-bit lane offsets apply)
+        t_main = a.copy32 ? min(t_main, min(ntiles - 2, a.seqK / kBc - 2)) : 0;
+        t_main = max(t_main, 0);
         const int wave_qmax = min(qw0 + QT * 16, a.seqQ) - 1;   // last real query of this wave
         const int kend = a.causal ? min(a.seqK, wave_qmax + 1) : a.seqK;
         const int nch = (kend + 31) / 32;                        // this wave's chunks (>= 1)
@@ -640,28 +665,32 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
             const char* Kn = (const char*)(lds + bn * 2 * kTile);
             // region 2t: P of chunk 2t, S of chunk 2t + 1 (this tile, keys 32..63), P.V of chunk 2t
             const int j0 = 2 * t;
+            const int bf = bc == 0 ? NB - 1 : bc - 1;   // tile t - 1's buffer, refilled with tile t + 2
+            TileCopy<NI> cp{Kh + (long long)(t + 2) * kBc * a.k_rs, Vh + (long long)(t + 2) * kBc * a.k_rs,
+                            lds + bf * 2 * kTile, lds + bf * 2 * kTile + kTile, koff, voff, wave, W};
             if (!kTail)
-                pipe_region<D, QT, kBf16, false>(Kt, 1, Vt, 0, off, qb, s, o, m, thr, lacc, ones, true, (j0 + 1) * 32, qw0,
-                                                 a.seqK, a.causal, a.sc, inv_sc, li, g);
+                pipe_region<D, QT, kBf16, false, false, NI>(Kt, 1, Vt, 0, off, qb, s, o, m, thr, lacc, ones, true,
+                                                            (j0 + 1) * 32, qw0, a.seqK, a.causal, a.sc, inv_sc, li, g, cp);
             else if (j0 < nch)
-                pipe_region<D, QT, kBf16, true>(Kt, 1, Vt, 0, off, qb, s, o, m, thr, lacc, ones, j0 + 1 < nch, (j0 + 1) * 32,
-                                                qw0, a.seqK, a.causal, a.sc, inv_sc, li, g);
+                pipe_region<D, QT, kBf16, true, false, NI>(Kt, 1, Vt, 0, off, qb, s, o, m, thr, lacc, ones, j0 + 1 < nch,
+                                                           (j0 + 1) * 32, qw0, a.seqK, a.causal, a.sc, inv_sc, li, g, cp);
             if (!kTail || t + 1 < ntiles) {
                 // tile t + 1 landed and is visible; every wave is past region 2t - 1, the last reader
-                // of tile t - 1's buffer, which now receives tile t + 2
+                // of tile t - 1's buffer, which now receives tile t + 2 (in the tail here, in the main
+                // loop during region 2t + 1)
                 asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
                 __syncthreads();
-                if (t + 2 < ntiles) copy(t + 2, bc == 0 ? NB - 1 : bc - 1);
+                if (kTail && t + 2 < ntiles) copy(t + 2, bf);
             }
             // region 2t + 1: P of chunk 2t + 1, S of chunk 2t + 2 (tile t + 1, keys 0..31), P.V of
             // chunk 2t + 1; past the last tile Kn is a stale buffer whose scores are ignored
             const int j1 = 2 * t + 1;
             if (!kTail)
-                pipe_region<D, QT, kBf16, false>(Kn, 0, Vt, 1, off, qb, s, o, m, thr, lacc, ones, true, (j1 + 1) * 32, qw0,
-                                                 a.seqK, a.causal, a.sc, inv_sc, li, g);
+                pipe_region<D, QT, kBf16, false, true, NI>(Kn, 0, Vt, 1, off, qb, s, o, m, thr, lacc, ones, true,
+                                                           (j1 + 1) * 32, qw0, a.seqK, a.causal, a.sc, inv_sc, li, g, cp);
             else if (j1 < nch)
-                pipe_region<D, QT, kBf16, true>(Kn, 0, Vt, 1, off, qb, s, o, m, thr, lacc, ones, j1 + 1 < nch, (j1 + 1) * 32,
-                                                qw0, a.seqK, a.causal, a.sc, inv_sc, li, g);
+                pipe_region<D, QT, kBf16, true, false, NI>(Kn, 0, Vt, 1, off, qb, s, o, m, thr, lacc, ones, j1 + 1 < nch,
+                                                           (j1 + 1) * 32, qw0, a.seqK, a.causal, a.sc, inv_sc, li, g, cp);
         };
         int t = 0;
         for (; t + NB <= t_main; t += NB) {
