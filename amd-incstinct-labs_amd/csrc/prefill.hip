@@ -568,27 +568,46 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
 
     const int nbh = a.batch * a.nQH;
     const int nitems = nbh * a.nqb;
-    for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+    // Query block of this wave: waves w and w + W/2 share a SIMD, so the second half takes the
+    // blocks in reverse (on the causal diagonal each SIMD holds one early and one late block).
+    const int wblk = wave < W / 2 ? wave : W + W / 2 - 1 - wave;
+    struct Item { int b, h, q0, qw0; };
+    auto item_of = [&](int item) {
         int bh, qrev;
         persistent_item(item, a.nqb, nbh, a.xcd_map, bh, qrev);
         const int qblk = a.causal ? (a.nqb - 1 - qrev) : qrev;
-        const int b = bh / a.nQH, h = bh % a.nQH;
-        const int kvh = h / (a.nQH / a.nKVH);
-        const int q0 = qblk * BM;
-        const int qw0 = q0 + wave * QT * 16;   // first query row of this wave
-
-        const uint16_t* Kh = a.K + b * a.k_bs + kvh * a.k_hs;
-        const uint16_t* Vh = a.V + b * a.k_bs + kvh * a.k_hs;
-        const uint16_t* Qh = a.Q + b * a.q_bs + h * a.q_hs;
-
-        // Q as B operands: lane holds Q[q = qw0 + t*16 + li][32*c + 8*g .. +8].
-        u32x4 qb[QT][ND];
+        Item it;
+        it.b = bh / a.nQH;
+        it.h = bh % a.nQH;
+        it.q0 = qblk * BM;
+        it.qw0 = it.q0 + wblk * QT * 16;   // first query row of this wave
+        return it;
+    };
+    // Q as B operands: lane holds Q[q = qw0 + t*16 + li][32*c + 8*g .. +8]. An item's Q is loaded
+    // at the end of the previous item (into the registers its Q no longer needs), so the loads are
+    // in flight during that item's output stores and final barrier.
+    u32x4 qb[QT][ND];
+    auto load_q = [&](const Item& it) {
+        const uint16_t* Qh = a.Q + it.b * a.q_bs + it.h * a.q_hs;
 #pragma unroll
         for (int t = 0; t < QT; ++t) {
-            const int q = min(qw0 + t * 16 + li, a.seqQ - 1);
+            const int q = min(it.qw0 + t * 16 + li, a.seqQ - 1);
 #pragma unroll
             for (int c = 0; c < ND; ++c) qb[t][c] = *(const u32x4*)(Qh + q * a.q_rs + c * 32 + g * 8);
         }
+    };
+    // per-lane offsets of full-tile copies: the same for every item
+    constexpr int NI = kBc * (D / 8) / (64 * W);
+    uint32_t koff[NI], voff[NI];
+    copy_offsets<D, W, true>(a.k_rs, wave, lane, koff);
+    copy_offsets<D, W, false>(a.k_rs, wave, lane, voff);
+    if ((int)blockIdx.x < nitems) load_q(item_of(blockIdx.x));
+    for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+        const Item it = item_of(item);
+        const int b = it.b, h = it.h, q0 = it.q0, qw0 = it.qw0;
+        const int kvh = h / (a.nQH / a.nKVH);
+        const uint16_t* Kh = a.K + b * a.k_bs + kvh * a.k_hs;
+        const uint16_t* Vh = a.V + b * a.k_bs + kvh * a.k_hs;
         f32x4 o[QT][NDT], lacc[QT];
         float m[QT], thr[QT];
         const float inv_sc = 1.f / a.sc;
@@ -616,10 +635,6 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
         const int kend = a.causal ? min(a.seqK, wave_qmax + 1) : a.seqK;
         const int nch = (kend + 31) / 32;                        // this wave's chunks (>= 1)
 
-        constexpr int NI = kBc * (D / 8) / (64 * W);
-        uint32_t koff[NI], voff[NI];
-        copy_offsets<D, W, true>(a.k_rs, wave, lane, koff);
-        copy_offsets<D, W, false>(a.k_rs, wave, lane, voff);
         auto copy = [&](int tt, int buf) {   // K and V of tile tt into LDS buffer buf
             uint16_t* kd = lds + buf * 2 * kTile;
             if (a.copy32 && (tt + 1) * kBc <= a.seqK) {
@@ -699,6 +714,7 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
         }
         for (; t < t_main; ++t) tile_iter(t, std::false_type{}, t % NB);
         for (; t < ntiles; ++t) tile_iter(t, std::true_type{}, t % NB);
+        if (item + (int)gridDim.x < nitems) load_q(item_of(item + (int)gridDim.x));
 
         // ---- O = O^T / l: lane holds d = 16dt + 4g + e of query li, and its query's full l.
         uint16_t* Oh = a.O + b * a.o_bs + h * a.o_hs;
