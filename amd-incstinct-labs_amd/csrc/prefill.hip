@@ -951,10 +951,14 @@ __global__ __launch_bounds__(64 * W) void fa_small(PrefillArgs a) {
     }
 }
 
-// Kernel choice for the 16-bit path: 8 waves x 32 queries (two waves per SIMD) when that gives
-// >= 2 workgroups per CU; 4 waves x 16 queries for mid-size problems; for problems whose 64-query
-// blocks would not fill the CUs twice over, 16 queries per workgroup with the keys split over its
-// waves (the large form when one round of workgroups covers the grid).
+// Kernel choice for the 16-bit path: the pipelined 8 waves x 32 queries (two waves per SIMD, one
+// workgroup per CU) once its 256-query blocks fill the CUs at least once (causal) or a quarter of
+// them (non-causal: every block has the same work, and one fast workgroup per block beat four-wave
+// workgroups of 64 queries at every size measured down to 64 blocks, e.g. B1 H8 S4096 622 -> 705
+// TFLOP/s; causal blocks below one round left the heaviest block on the critical path, e.g. B1 H12
+// S4096 603 -> 547); 4 waves x 16 queries for the remaining mid-size causal problems; for problems
+// whose 64-query blocks would not fill the CUs twice over, 16 queries per workgroup with the keys
+// split over its waves (the large form when one round of workgroups covers the grid).
 struct PrefillPlan { int kernel, waves, rows; long long grid; };
 
 template <int D>
@@ -962,9 +966,10 @@ PrefillPlan plan_mfma(const cdna3_prefill_cfg& c) {
     const long long heads = (long long)c.batch * c.nQHeads;
     const int cus = device_cus();
     PrefillPlan p;
-    if (heads * ((c.seqQ + 255) / 256) >= 512) {
+    const long long blocks8 = heads * ((c.seqQ + 255) / 256);
+    if (blocks8 >= (c.causal ? cus : cus / 4)) {
         p.kernel = CDNA4_KERNEL_PREFILL_MFMA_8W; p.waves = 8; p.rows = 256;
-        p.grid = heads * ((c.seqQ + 255) / 256);
+        p.grid = blocks8;
         // One resident workgroup per CU at W = 8 (LDS and VGPRs allow no second), so a grid of one
         // workgroup per CU (a multiple of 8, see the item mapping) runs every item without
         // relaunch gaps between workgroups.

@@ -95,11 +95,14 @@ def test_invalid_arguments_rejected_without_gpu():
 
 def test_kernel_plans_without_gpu():
     # The dispatch thresholds (for a 256-CU MI355X): 8 waves x 32 queries once batch * heads *
-    # ceil(seqQ / 256) >= 512, 4 waves x 16 queries for mid sizes, fa_small below; decode splits
-    # long caches only when given a workspace.
+    # ceil(seqQ / 256) >= 256 (causal) or >= 64 (non-causal), 4 waves x 16 queries for the other
+    # mid-size causal problems, fa_small below; decode splits long caches only when given a workspace.
     plan = lambda *c: cdna4.prefill_plan(cdna4.PrefillCfg(*c), cdna4.BF16)
     assert plan(128, 8192, 8192, 32, 32, 4, 1).name == "fa_mfma_8w"
+    assert plan(128, 4096, 4096, 16, 16, 1, 1).name == "fa_mfma_8w"
     assert plan(128, 4096, 4096, 8, 8, 1, 1).name == "fa_mfma_4w"
+    assert plan(128, 2048, 2048, 8, 8, 1, 0).name == "fa_mfma_8w"
+    assert plan(128, 2048, 2048, 4, 4, 1, 0).name == "fa_small"
     assert plan(64, 512, 512, 8, 8, 1, 0).name == "fa_small"
     assert cdna4.prefill_plan(cdna4.PrefillCfg(64, 512, 512, 8, 8, 1, 0), cdna4.F32).name == "fa_f32"
     d = cdna4.DecodeCfg(128, 8192, 32, 8, 1)

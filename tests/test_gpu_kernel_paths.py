@@ -70,7 +70,8 @@ def check_prefill(D, SQ, SK, HQ, HK, B, causal, dtype, kernel, seed=0, heads=Non
     assert worst <= tolerance(dtype)
 
 
-# ---- fa_pipe<D, 8, 2> (plan name fa_mfma_8w): batch * heads * ceil(seqQ / 256) >= 512 ----------
+# ---- fa_pipe<D, 8, 2> (plan name fa_mfma_8w): batch * heads * ceil(seqQ / 256) >= CUs (causal) --
+# ---- or >= CUs / 4 (non-causal) ---------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_fa_mfma_8w_d128_causal_mha(dtype):
@@ -130,16 +131,29 @@ def test_fa_mfma_4w_d128_causal(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_fa_mfma_4w_d64_gqa_noncausal(dtype):
-    check_prefill(64, 2048, 2048, 16, 4, 1, 0, dtype, "fa_mfma_4w", seed=8)
+def test_fa_mfma_4w_d64_gqa_causal(dtype):
+    check_prefill(64, 2048, 2048, 16, 4, 1, 1, dtype, "fa_mfma_4w", seed=8)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fa_pipe_mid_size_d64_gqa_noncausal(dtype):
+    # 16 heads x 8 blocks of 256 queries = 128 < one round: the non-causal 8-wave plan with a grid of
+    # 128 workgroups, one work item each.
+    check_prefill(64, 2048, 2048, 16, 4, 1, 0, dtype, "fa_mfma_8w", seed=8)
 
 
 def test_fa_mfma_4w_ragged_causal():
     check_prefill(128, 4093, 4093, 8, 2, 1, 1, torch.float16, "fa_mfma_4w", seed=9)
 
 
-def test_fa_mfma_4w_cross_attention():
-    check_prefill(64, 4096, 1003, 8, 8, 1, 0, torch.bfloat16, "fa_mfma_4w", seed=10)
+def test_fa_pipe_mid_size_cross_attention():
+    # non-causal, seqK 1003 (ragged last tile), 8 x 16 = 128 blocks
+    check_prefill(64, 4096, 1003, 8, 8, 1, 0, torch.bfloat16, "fa_mfma_8w", seed=10)
+
+
+def test_fa_pipe_quarter_round_noncausal():
+    # the smallest non-causal 8-wave plan: 64 blocks (one per XCD-aligned group), D 128
+    check_prefill(128, 2048, 2048, 8, 8, 1, 0, torch.bfloat16, "fa_mfma_8w", seed=13)
 
 
 # ---- fa_small: both workgroup forms -------------------------------------------------------------
