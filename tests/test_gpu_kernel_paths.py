@@ -198,6 +198,41 @@ def test_prefill_strided_against_oracle(D, S, HQ, HK, dtype, kernel):
     assert worst <= tolerance(dtype)
 
 
+def test_prefill_strided_rows_4gib_apart():
+    # K/V rows 2^25 elements apart: a 64-key tile spans 4 GiB, beyond the pipelined kernel's 32-bit
+    # per-lane copy offsets, so every tile takes the clamped copy with 64-bit addresses (the plan is
+    # still the 8-wave kernel). K and V share one ~4.5 GB allocation, heads interleaved in a row;
+    # only the rows used are written. seqK 70: one full and one partial tile.
+    D, SQ, SK, HQ, HK = 128, 2048, 70, 8, 2
+    rs = 1 << 25
+    cfg = cdna4.PrefillCfg(D, SQ, SK, HQ, HK, 1, 0)
+    assert cdna4.prefill_plan(cfg, torch.bfloat16).name == "fa_mfma_8w"
+    g = torch.Generator(device=DEV).manual_seed(77)
+    Q = _randn((HQ, SQ, D), torch.bfloat16, g)
+    Kd = _randn((HK, SK, D), torch.bfloat16, g)
+    Vd = _randn((HK, SK, D), torch.bfloat16, g)
+    big = torch.empty((SK - 1) * rs + 2 * HK * D, device=DEV, dtype=torch.bfloat16)
+    big.as_strided((HK, SK, D), (D, rs, 1), 0).copy_(Kd)
+    big.as_strided((HK, SK, D), (D, rs, 1), HK * D).copy_(Vd)
+    O = torch.full((HQ, SQ, D), float("nan"), device=DEV, dtype=torch.bfloat16)
+    st = cdna4.PrefillStrides(HQ * SQ * D, SQ * D, D, 0, D, rs, HQ * SQ * D, SQ * D, D)
+    cdna4.prefill_strided(Q, big, big[HK * D:], O, cfg, st)
+    torch.cuda.synchronize()
+    assert torch.isfinite(O.float()).all()
+    rows = _rows(SQ, 5)
+    q = Q.float().cpu().numpy()[None]
+    k = Kd.float().cpu().numpy()[None]
+    v = Vd.float().cpu().numpy()[None]
+    heads = [(0, h) for h in range(HQ)]
+    want = _oracle_heads(q, k, v, heads, rows, D, SQ, SK, HQ, HK, 0)
+    o = O.float().cpu().numpy()
+    worst = max(max_rel_err(o[h, rows], want[(0, h)]) for _, h in heads)
+    print(f"  max err {worst:.2e}", flush=True)
+    del big
+    torch.cuda.empty_cache()
+    assert worst <= tolerance(torch.bfloat16)
+
+
 # ---- BASELINE config 3 at full size: every head of batches 0 and 3 -------------------------------
 
 def test_prefill_config3_subsample_every_head_of_batches_0_and_3():
