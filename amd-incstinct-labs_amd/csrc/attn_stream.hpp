@@ -16,16 +16,24 @@ constexpr int kDecStages = 2;   // ring depth: one chunk in flight while the wav
 // One asynchronous copy, 16 bytes per lane: lane i's bytes at gsrc land at LDS lds_dst + 16 i
 // (lds_dst wave-uniform, in M0). Issued as inline assembly so that the compiler does not track
 // it (it would otherwise wait for every copy before any LDS read); the kernel waits itself.
+// The compiler's hazard recognizer does not look inside inline assembly, so the copies keep
+// their own wait states: an SALU write of M0 needs 1 before an LDS DMA (`s_nop 0`; the compiler
+// writes M0 for the "{m0}" operand with an SALU move).
 __device__ __forceinline__ void dma16(const void* gsrc, const void* lds_dst) {
     const uint32_t base = (uint32_t)(uintptr_t)(const tile::LDS_AS_T*)lds_dst;
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "{m0}"(base) : "memory");
 }
 
 // The same copy from a wave-uniform base (SGPR pair) plus a 32-bit per-lane byte offset: no
-// per-copy 64-bit address arithmetic in the vector ALU.
+// per-copy 64-bit address arithmetic in the vector ALU. A VALU write of an SGPR (v_readlane of a
+// spilled SGPR, v_readfirstlane) needs 5 wait states before a vector memory instruction reads that
+// SGPR, and the compiler does not know the copy reads it; so the base is first moved by the SALU
+// (which waits for VALU-written SGPRs by itself) into a fresh pair that only the copy reads.
 __device__ __forceinline__ void dma16_s(const void* sbase, uint32_t voff, const void* lds_dst) {
     const uint32_t base = (uint32_t)(uintptr_t)(const tile::LDS_AS_T*)lds_dst;
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(base) : "memory");
+    const void* b;
+    asm volatile("s_mov_b64 %0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %0"
+                 : "=&s"(b) : "v"(voff), "s"(sbase), "{m0}"(base) : "memory");
 }
 
 // Wait until at most Y of this wave's newest copy groups (kCopies copies each) are in flight.
