@@ -352,6 +352,23 @@ __device__ __forceinline__ void mask_chunk(f32x4 (&s)[QT][2], int kb, int qw0, i
             }
 }
 
+// Causal mask of the chunk whose first key is the wave's first query (kb == qw0, both multiples of
+// 32): key - query = 4u + e - (16t + li - 8g) for lane (li, g), so the pattern is the same for every
+// such chunk, 2 VALU per score instead of mask_chunk's general form. Chunks below qw0 need no
+// causal mask, and those above it lie past the wave's last query (never used).
+template <int QT>
+__device__ __forceinline__ void mask_diag(f32x4 (&s)[QT][2], int li, int g) {
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+        const int dq = 16 * t + li - 8 * g;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (4 * u + e > dq) s[t][u][e] = -INFINITY;
+    }
+}
+
 // Per-lane raw maxima lm of a chunk and whether one exceeds its query's threshold thr = (m + kTau)
 // / sc, i.e. whether a scaled score exceeds the reference maximum by more than kTau (the
 // threshold is kept in raw score units so that the check per chunk needs no multiply).
@@ -471,7 +488,10 @@ __device__ __forceinline__ void pipe_region(const char* Kn, int kcn, const char*
     }
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(0);
-    if constexpr (kTail) mask_chunk<QT>(sn, kbn, qw0, seqK, causal, li, g);
+    if constexpr (kTail) {   // wave-uniform branches: most tail chunks need neither mask
+        if (causal && kbn == qw0) mask_diag<QT>(sn, li, g);
+        if (kbn + 32 > seqK) mask_chunk<QT>(sn, kbn, qw0, seqK, causal, li, g);
+    }
     float lm[QT];
     bool need = check_raw<QT>(sn, thr, lm);
     if constexpr (kTail) need = need && has_next;
