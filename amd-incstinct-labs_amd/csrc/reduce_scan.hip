@@ -87,9 +87,12 @@ constexpr int kReduceThreads = 256;          // 4 waves, no LDS: each wave write
 constexpr int kReduceMaxBlocks = 2048;       // 8192 partials at most
 constexpr int kReduceUnroll = 4;             // 16-byte loads in flight per lane
 
+// kVec: in_ is 16-byte aligned and read as vectors; the nhead (< one vector) elements at head_
+// that precede it (a misaligned call's first elements) are folded in by the first threads.
 template <int DT, class Op, bool kVec>
 __global__ __launch_bounds__(kReduceThreads) void reduce_stage1(const void* __restrict__ in_, size_t n,
-                                                                 void* __restrict__ part_) {
+                                                                 void* __restrict__ part_,
+                                                                 const void* __restrict__ head_, int nhead) {
     using E = Elem<DT>;
     using Acc = typename E::Acc;
     const typename E::In* in = (const typename E::In*)in_;
@@ -126,6 +129,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_stage1(const void* __re
         scalar_from = nvec * E::VEC;
     }
     for (size_t i = scalar_from + tid; i < n; i += nthr) acc[1] = op(acc[1], E::load1(in + i));
+    if (tid < (size_t)nhead) acc[2] = op(acc[2], E::load1((const typename E::In*)head_ + tid));
     static_assert(kReduceUnroll == 4, "combine below assumes four accumulators");
     Acc a = op(op(acc[0], acc[1]), op(acc[2], acc[3]));
     a = allreduce(a, op);
@@ -173,12 +177,23 @@ unsigned reduce_blocks(size_t n, int vec) {
 template <int DT, class Op>
 int reduce_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
     using E = Elem<DT>;
-    const unsigned blocks = reduce_blocks(n, E::VEC);
-    const bool vec = ((uintptr_t)in % 16) == 0;
+    constexpr size_t kEsz = sizeof(typename E::In);
+    // A misaligned input (elements at their natural alignment) splits into the elements up to the
+    // first 16-byte boundary, folded in by the first threads, and an aligned vector body.
+    const uintptr_t addr = (uintptr_t)in;
+    size_t head = 0;
+    bool vec = addr % 16 == 0;
+    if (!vec && addr % kEsz == 0) {
+        head = (16 - addr % 16) / kEsz;
+        vec = head < n;
+        if (!vec) head = 0;
+    }
+    const unsigned blocks = reduce_blocks(n - head, E::VEC);
     if (vec)
-        reduce_stage1<DT, Op, true><<<blocks, kReduceThreads, 0, s>>>(in, n, ws);
+        reduce_stage1<DT, Op, true><<<blocks, kReduceThreads, 0, s>>>((const char*)in + head * kEsz, n - head, ws, in,
+                                                                       (int)head);
     else
-        reduce_stage1<DT, Op, false><<<blocks, kReduceThreads, 0, s>>>(in, n, ws);
+        reduce_stage1<DT, Op, false><<<blocks, kReduceThreads, 0, s>>>(in, n, ws, nullptr, 0);
     reduce_stage2<DT, Op><<<1, kReduce2Threads, 0, s>>>(ws, (int)(blocks * (kReduceThreads / 64)), out);
     return launch_status();
 }
