@@ -116,6 +116,16 @@ def test_fa_pipe_partial_odd_round():
                   heads=[(0, 0), (1, 9), (2, 18), (3, 31)])
 
 
+@pytest.mark.parametrize("D,S,H,dtype", [(128, 3000, 32, torch.bfloat16), (128, 2053, 32, torch.float16),
+                                         (64, 2085, 64, torch.float16)])
+def test_fa_pipe_causal_ragged_lengths(D, S, H, dtype):
+    # Causal (seqQ == seqK) at lengths that are not multiples of 32: the tail's fixed mask of the
+    # chunk at a wave's first query and the general mask of the ragged last chunk apply to the
+    # same chunk in some waves and to different chunks in others.
+    check_prefill(D, S, S, H, H, 1, 1, dtype, "fa_mfma_8w", seed=30 + S,
+                  heads=[(0, 0), (0, H // 2 - 1), (0, H - 1)])
+
+
 @pytest.mark.parametrize("SK", [1, 50, 95, 96, 97])
 def test_fa_pipe_short_keys(SK):
     # Fewer keys than the pipelined main loop needs (t_main = 0 below 96): every tile in the tail.
