@@ -13,7 +13,10 @@
 //     (the heads take the place of the 16 query columns), which leaves the VALU only the
 //     softmax: the kernel is bound by HBM, not by per-element dot products.
 //   * K/V chunks go HBM -> LDS by asynchronous global_load_lds copies into a ring of stages,
-//     three chunks per wave in flight.
+//     three chunks per wave in flight. The split-K kernel's copies carry the non-temporal policy
+//     (every K/V byte is read once): config 4 measured 5.8 -> 6.6 TB/s with it, with the
+//     Infinity Cache holding other data. The short-cache kernel keeps the default policy: the
+//     runtime's decode step, whose caches are small and just appended to, ran 3 % slower with it.
 //   * A second kernel merges the (m, l, O) partials of each query head, with the max and the
 //     denominator formed by the wave butterfly.
 #include "attn_tile.hpp"
@@ -122,16 +125,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void de
 #pragma unroll
     for (int i = 0; i < NS - 1; ++i)
         if (i < nch) {
-            load_stage<D, true>(Kh, D, kbeg + i * kDecT, N, k_lds + i * kStage, lane);
-            load_stage<D, false>(Vh, D, kbeg + i * kDecT, N, v_lds + i * kStage, lane);
+            load_stage<D, true, true>(Kh, D, kbeg + i * kDecT, N, k_lds + i * kStage, lane);
+            load_stage<D, false, true>(Vh, D, kbeg + i * kDecT, N, v_lds + i * kStage, lane);
         }
     int st = 0;   // stage of chunk ch
     for (int ch = 0; ch < nch; ++ch) {
         const int ahead = ch + NS - 1;
         if (ahead < nch) {
             const int sa = (st == 0) ? NS - 1 : st - 1;   // stage of chunk ch - 1, already consumed
-            load_stage<D, true>(Kh, D, kbeg + ahead * kDecT, N, k_lds + sa * kStage, lane);
-            load_stage<D, false>(Vh, D, kbeg + ahead * kDecT, N, v_lds + sa * kStage, lane);
+            load_stage<D, true, true>(Kh, D, kbeg + ahead * kDecT, N, k_lds + sa * kStage, lane);
+            load_stage<D, false, true>(Vh, D, kbeg + ahead * kDecT, N, v_lds + sa * kStage, lane);
         }
         wait_copies_younger<kCopies>(min(NS - 1, nch - 1 - ch));
         const char* Kt = (const char*)(k_lds + st * kStage);
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(64 * W) void decode_wg(DecodeArgs a, void* __restri
     load_q<D>(a, b, qh0, nrows, li, g, qb);
     f32x4 o[1][NDT], lacc[1];
     float m[1];
-    stream_keys<D, kBf16, kDecStages>((const uint16_t*)a.K + head_off, (const uint16_t*)a.V + head_off, D, N, kbeg,
+    stream_keys<D, kBf16, kDecStages, false>((const uint16_t*)a.K + head_off, (const uint16_t*)a.V + head_off, D, N, kbeg,
                                       kend, 0, 0, a.sc, qb, o, lacc, m, k_lds + wave * kRing, v_lds + wave * kRing,
                                       lane);
     merge_waves<D, kBf16, W>(o, lacc, m, (float*)k_lds, (float*)v_lds, nrows,

@@ -34,6 +34,7 @@ is timed instead when oracle/_ref is absent. `cpu_baseline_threads` is the same 
 their own one-thread CPU figures (reference cpu_decode, attn_cpu_ref; the oracle's reduce/scan).
 """
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -80,6 +81,22 @@ def time_launches(torch, fn, steps, warmup):
     torch.cuda.synchronize()
     total = t0.elapsed_time(t1)
     return total / steps, total
+
+
+def abi_launcher(torch, cdna4, name, arg_sets):
+    """fn(i) that calls C-ABI entry point `name` with the i-th (mod len) of arg_sets, tuples of
+    arguments already converted for ctypes, ending with the current stream. The few-microsecond
+    kernels (config 1, batch-1 decode, the norms) are timed this way: through the Python wrappers,
+    whose per-call argument checks take longer than such a kernel, the GPU would idle between
+    launches and the figure would time the host. Each leg calls the checked wrapper once first."""
+    f = getattr(cdna4.lib(), name)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def call(i=0):
+        r = f(*arg_sets[i % len(arg_sets)], stream)
+        if r != 0:
+            raise RuntimeError(f"{name} returned {r}")
+    return call
 
 
 TRAFFIC_SOURCE = ("profiles/traffic.json: HBM bytes per launch from an earlier rocprofv3 --pmc FETCH_SIZE / "
@@ -318,8 +335,11 @@ def bench_decode(torch, cdna4, steps, warmup):
             torch.randn(1, HK, N, D, device="cuda", dtype=torch.float16, generator=g)) for _ in range(32)]
     o1 = torch.empty_like(q1)
     ws1 = torch.empty(cdna4.decode_workspace_size(cfg1b), dtype=torch.uint8, device="cuda")
-    ms1, _ = time_launches(
-        torch, lambda i=0: cdna4.decode(q1, kv1[i % 32][0], kv1[i % 32][1], o1, cfg1b, workspace=ws1), steps, warmup)
+    cdna4.decode(q1, kv1[0][0], kv1[0][1], o1, cfg1b, workspace=ws1)
+    fn1 = abi_launcher(torch, cdna4, "cdna3_attn_decode",
+                       [(q1.data_ptr(), k.data_ptr(), v.data_ptr(), o1.data_ptr(), ctypes.byref(cfg1b), cdna4.F16,
+                         ws1.data_ptr(), ws1.numel()) for k, v in kv1])
+    ms1, _ = time_launches(torch, fn1, steps, warmup)
     nb1 = 2.0 * HK * N * D * 2 + 2.0 * HQ * D * 2
     batch1 = {"us": ms1 * 1e3, "GBs": nb1 / (ms1 * 1e-3) / 1e9, "reference_us_mi300x": 803.4,
               "config": {"batch": 1, "q_heads": HQ, "kv_heads": HK, "head_dim": D, "kv_len": N, "dtype": "fp16"}}
@@ -389,7 +409,11 @@ def bench_cfg1(torch, cdna4, steps, warmup):
         Q, K, V = ((torch.rand(B, H, S, D, device="cuda", generator=g) * 2 - 1).to(dt) for _ in range(3))
         O = torch.empty_like(Q)
         cfg = cdna4.PrefillCfg(D, S, S, H, H, B, 0)
-        ms, _ = time_launches(torch, lambda i=0: cdna4.prefill(Q, K, V, O, cfg), steps, warmup)
+        cdna4.prefill(Q, K, V, O, cfg)
+        fn = abi_launcher(torch, cdna4, "cdna3_attn_prefill",
+                          [(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), ctypes.byref(cfg),
+                            cdna4.F32 if dt == torch.float32 else cdna4.F16)])
+        ms, _ = time_launches(torch, fn, steps, warmup)
         tf = flop / (ms * 1e-3) / 1e12
         out[name] = {"us": round(ms * 1e3, 2), "TFLOPS": round(tf, 2), "frac": round(tf / peak, 4),
                      "peak": peak, "peak_unit": "TFLOP/s"}
@@ -429,8 +453,14 @@ def bench_norms(torch, cdna4, steps, warmup):
         w16 = (torch.rand(H, device="cuda", generator=g) + 0.5).half()
         nbytes = 2 * M * H * 4
         entry = {}
-        for name, fn in (("layernorm", lambda i=0: cdna4.layernorm_f32(xs[i % nb], gamma, beta, out=ys[i % nb])),
-                         ("rmsnorm", lambda i=0: cdna4.rmsnorm_f32(xs[i % nb], w16, out=ys[i % nb]))):
+        cdna4.layernorm_f32(xs[0], gamma, beta, out=ys[0])
+        cdna4.rmsnorm_f32(xs[0], w16, out=ys[0])
+        ln = abi_launcher(torch, cdna4, "cdna3_layernorm_f32",
+                          [(x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), y.data_ptr(), M, H, 1e-5)
+                           for x, y in zip(xs, ys)])
+        rms = abi_launcher(torch, cdna4, "cdna3_rmsnorm_f32",
+                           [(x.data_ptr(), w16.data_ptr(), y.data_ptr(), M, H, 1e-6) for x, y in zip(xs, ys)])
+        for name, fn in (("layernorm", ln), ("rmsnorm", rms)):
             ms, _ = time_launches(torch, fn, steps, warmup)
             gbs = nbytes / (ms * 1e-3) / 1e9
             entry[name] = {"us": round(ms * 1e3, 2), "GBs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
