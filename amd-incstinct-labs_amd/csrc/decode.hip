@@ -15,8 +15,12 @@
 //   * K/V chunks go HBM -> LDS by asynchronous global_load_lds copies into a ring of stages,
 //     three chunks per wave in flight. The split-K kernel's copies carry the non-temporal policy
 //     (every K/V byte is read once): config 4 measured 5.8 -> 6.6 TB/s with it, with the
-//     Infinity Cache holding other data. The short-cache kernel keeps the default policy: the
-//     runtime's decode step, whose caches are small and just appended to, ran 3 % slower with it.
+//     Infinity Cache holding other data. The one-launch kernel takes it for caches larger than
+//     the Infinity Cache only: the runtime's decode step, whose caches are small and just
+//     appended to, ran 3 % slower with it.
+//   * When batch x kv heads fills whole rounds of the CUs (config 4: 256 on 256), one workgroup
+//     per (batch, kv head) streams its whole cache and merges its waves in LDS: no split-K
+//     partials, no merge launch (159.8 us against 162.6 us for split + merge at config 4).
 //   * A second kernel merges the (m, l, O) partials of each query head, with the max and the
 //     denominator formed by the wave butterfly.
 #include "attn_tile.hpp"
@@ -177,7 +181,8 @@ constexpr int wg_ring_elems() { return W * kDecStages * kDecT * D; }
 // Keys per wave of the short-cache variant: N split into W ranges of whole 32-key chunks.
 __host__ __device__ constexpr int wg_keys_per_wave(int N, int W) { return ((N + W - 1) / W + kDecT - 1) / kDecT * kDecT; }
 
-template <int D, bool kBf16, int W>
+// kNT: the copies take the non-temporal policy (long caches; see plan_decode).
+template <int D, bool kBf16, int W, bool kNT>
 __global__ __launch_bounds__(64 * W) void decode_wg(DecodeArgs a, void* __restrict__ out) {
     constexpr int ND = D / 32, NDT = D / 16;
     constexpr int kStage = kDecT * D;
@@ -204,7 +209,7 @@ __global__ __launch_bounds__(64 * W) void decode_wg(DecodeArgs a, void* __restri
     load_q<D>(a, b, qh0, nrows, li, g, qb);
     f32x4 o[1][NDT], lacc[1];
     float m[1];
-    stream_keys<D, kBf16, kDecStages, false>((const uint16_t*)a.K + head_off, (const uint16_t*)a.V + head_off, D, N, kbeg,
+    stream_keys<D, kBf16, kDecStages, kNT>((const uint16_t*)a.K + head_off, (const uint16_t*)a.V + head_off, D, N, kbeg,
                                       kend, 0, 0, a.sc, qb, o, lacc, m, k_lds + wave * kRing, v_lds + wave * kRing,
                                       lane);
     merge_waves<D, kBf16, W>(o, lacc, m, (float*)k_lds, (float*)v_lds, nrows,
@@ -262,7 +267,7 @@ __global__ __launch_bounds__(64) void decode_merge(const float* __restrict__ par
     }
 }
 
-struct Plan { int G, HB, KPW, P; size_t ws_bytes; bool wg; };
+struct Plan { int G, HB, KPW, P; size_t ws_bytes; bool wg, nt; };
 
 // Waves per workgroup of the short-cache variant (its LDS holds W rings of two K and V stages)
 // and the longest cache it takes when a split-K workspace is available: at most kWgChunks 32-key
@@ -278,6 +283,16 @@ constexpr int kWgChunks = 8;
 // no memory beyond q, K, V and o: such a call never allocates and shares no buffer with any other
 // call, so it is re-entrant across streams and capturable. Long caches then stream through one
 // workgroup per (batch, kv head, head group) instead of a split-K grid.
+// With a workspace, long caches also take the one-launch variant when its grid is whole rounds of
+// one workgroup per CU (batch x kv heads x head groups a multiple of the CU count): every CU then
+// streams the same number of rows from start to end, as the split grid's workgroups do, and the
+// call skips the merge launch and the partials (config 4, 256 rows on 256 CUs: 159.8 us against
+// 162.6 us for split + merge, both with non-temporal copies).
+// nt: K/V larger than the 256 MB Infinity Cache are copied with the non-temporal policy (no call
+// can find them cached anyway); smaller caches, such as the runtime's per-layer caches, keep the
+// default policy (the runtime's decode step measured 3 % slower with non-temporal copies).
+constexpr double kStreamBytes = 256.0 * 1024 * 1024;
+
 bool plan_decode(const cdna3_decode_cfg& c, bool split_k, Plan& p) {
     if (c.D != 64 && c.D != 128) return false;
     if (c.N < 1 || c.nQHeads < 1 || c.nKVHeads < 1 || c.batch < 1) return false;
@@ -287,16 +302,18 @@ bool plan_decode(const cdna3_decode_cfg& c, bool split_k, Plan& p) {
     p.G = c.nQHeads / c.nKVHeads;
     p.HB = (p.G + 15) / 16;
     const int W = c.D == 64 ? wg_waves<64>() : wg_waves<128>();
-    p.wg = !split_k || c.N <= W * kWgChunks * kDecT;
+    const long long rows = (long long)c.batch * c.nKVHeads * p.HB;
+    const int cus = device_cus();
+    p.nt = 4.0 * c.batch * c.nKVHeads * (double)c.N * c.D > kStreamBytes;
+    p.wg = !split_k || c.N <= W * kWgChunks * kDecT || (cus > 0 && rows % cus == 0);
     if (p.wg) {   // one workgroup per (batch, kv head, head group); W contiguous key ranges
         p.KPW = wg_keys_per_wave(c.N, W);
         p.P = 1;
         p.ws_bytes = 0;
         return true;
     }
-    const double rows = (double)c.batch * c.nKVHeads * p.HB;
-    const double slots = (double)device_cus() * kDecPerCU;
-    long long kpw = (long long)ceil((double)c.N * rows / slots);
+    const double slots = (double)cus * kDecPerCU;
+    long long kpw = (long long)ceil((double)c.N * (double)rows / slots);
     if (kpw < 4 * kDecT) kpw = 4 * kDecT;
     kpw = (kpw + kDecT - 1) / kDecT * kDecT;
     if (kpw > c.N) kpw = ((long long)c.N + kDecT - 1) / kDecT * kDecT;
@@ -323,7 +340,8 @@ int launch_decode(const cdna3_decode_cfg& c, const Plan& p, const void* q, const
     if (gy > 65535 || c.batch > 65535) return CDNA4_ERR_INVALID_VALUE;
     dim3 grid((unsigned)p.P, (unsigned)gy, (unsigned)c.batch);
     if (p.wg) {
-        decode_wg<D, kBf16, wg_waves<D>()><<<grid, 64 * wg_waves<D>(), 0, s>>>(a, o);
+        if (p.nt) decode_wg<D, kBf16, wg_waves<D>(), true><<<grid, 64 * wg_waves<D>(), 0, s>>>(a, o);
+        else decode_wg<D, kBf16, wg_waves<D>(), false><<<grid, 64 * wg_waves<D>(), 0, s>>>(a, o);
         return launch_status();
     }
     if (!ws) return CDNA4_ERR_INVALID_VALUE;
@@ -387,7 +405,7 @@ int scratch_address(void** out) {
 long long attn_decode_plan_key(const cdna3_decode_cfg& c) {
     Plan p;
     if (!plan_decode(c, true, p)) return -1;
-    return p.wg ? 1 : ((long long)p.P << 32) | (long long)p.KPW;
+    return p.wg ? (p.nt ? 3 : 1) : ((long long)p.P << 32) | (long long)p.KPW;
 }
 
 // The launches of cdna3_attn_decode planned for cfg->N, but with the cache length read on the

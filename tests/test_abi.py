@@ -36,10 +36,12 @@ def test_version_and_error_strings():
 
 
 def test_workspace_sizes():
-    cfg = cdna4.DecodeCfg(128, 8192, 32, 8, 32, 0)
+    cfg = cdna4.DecodeCfg(128, 8192, 32, 8, 4, 0)   # 32 (batch, kv head) rows: the split-K plan
     ws = cdna4.decode_workspace_size(cfg)
     # partials: batch * nQH * P * (D + 2) floats, P = ceil(N / keys-per-wave) >= 1
-    assert ws >= 32 * 32 * (128 + 2) * 4
+    assert ws >= 4 * 32 * (128 + 2) * 4
+    # config 4 (256 rows, whole rounds of the 256 CUs) takes the one-launch plan: no partials
+    assert cdna4.decode_plan(cdna4.DecodeCfg(128, 8192, 32, 8, 32, 0), cdna4.F16, True).name == "decode_wg"
     assert cdna4.decode_workspace_size(cdna4.DecodeCfg(96, 128, 8, 8)) == 0       # D not supported
     assert cdna4.decode_workspace_size(cdna4.DecodeCfg(128, 128, 6, 4)) == 0      # nQH % nKVH != 0
     assert cdna4.decode_workspace_size(cdna4.DecodeCfg(128, 128, 8, 8, 1, 64)) == 0  # stride < N
@@ -80,7 +82,7 @@ def test_invalid_arguments_rejected_without_gpu():
     assert l.cdna3_rope_append_kv_f16(p, p, p, p, p, p, p, p, 4, 8, 2, 63, 0, 16, None) == 1  # odd D
     assert l.cdna3_rope_append_kv_f16(p, p, p, p, p, p, p, p, 4, 8, 2, 64, 14, 16, None) == 1  # past the cache
     assert l.cdna3_attn_decode_noalloc(p, p, p, p, ctypes.byref(dcfg), cdna4.F32, None) == 1       # dtype
-    big = cdna4.DecodeCfg(128, 4096, 64, 4, 1024)                                                   # 34 MB of partials
+    big = cdna4.DecodeCfg(128, 4096, 64, 4, 1001)   # 33 MB of partials (4,004 rows: the split-K plan)
     assert l.cdna3_attn_decode_noalloc(p, p, p, p, ctypes.byref(big), cdna4.F16, None) == 2
     info = cdna4.PlanInfo()
     assert l.cdna3_attn_prefill_plan(ctypes.byref(bad[0]), cdna4.BF16, ctypes.byref(info)) == 1

@@ -165,6 +165,8 @@ def test_decode_full_size_config_and_split_invariance():
             T[b] = t.reshape(shape)
             vals.append(x)
         hostv[b] = vals
+    plan = cdna4.decode_plan(cdna4.DecodeCfg(D, N, HQ, HK, B), torch.float16, with_workspace=True)
+    print(f"config-4 plan: {plan.name}", flush=True)   # the one-launch plan on a 256-CU part
     ws = torch.empty(cdna4.decode_workspace_size(cdna4.DecodeCfg(D, N, HQ, HK, B)), dtype=torch.uint8, device=DEV)
     o = torch.empty_like(q)
     cdna4.decode(q, K, V, o, cdna4.DecodeCfg(D, N, HQ, HK, B), workspace=ws)

@@ -322,6 +322,24 @@ def test_decode_split_more_than_64_partials():
     assert plan.partials > 64
 
 
+def _cus():
+    return torch.cuda.get_device_properties(0).multi_processor_count
+
+
+def test_decode_whole_rounds_one_launch_d64_streaming():
+    # batch x kv heads = the CU count: with a workspace the long cache still takes the one-launch
+    # plan (one workgroup per CU); 327 MB of K/V, beyond the Infinity Cache: non-temporal copies.
+    HK = 4
+    check_decode(64, 5000, 16, HK, _cus() // HK, torch.float16, "decode_wg", seed=11)
+
+
+def test_decode_whole_rounds_one_launch_d128_strided_cached():
+    # whole rounds, a cache longer than the short-cache bound (1,024 keys at D 128) but K/V below
+    # the Infinity Cache size (default copy policy), rows 2,048 apart
+    HK = 8
+    check_decode(128, 1500, 32, HK, _cus() // HK, torch.bfloat16, "decode_wg", stride=2048, seed=12)
+
+
 @pytest.mark.parametrize("N,HQ,HK,B", [(8192, 32, 8, 1), (3000, 40, 2, 2), (4097, 12, 12, 1)])
 def test_decode_without_workspace_one_launch(N, HQ, HK, B):
     # The reference launchers' contract: no workspace, one launch, any cache length.

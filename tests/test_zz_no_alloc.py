@@ -68,8 +68,9 @@ def test_noalloc_short_cache_one_launch():
 
 
 def test_noalloc_rejects_calls_beyond_the_scratch():
-    # 1024 sequences x 64 query heads: one partial per head is 1024 * 64 * 130 * 4 B = 34 MB.
-    cfg = cdna4.DecodeCfg(128, 4096, 64, 4, 1024)
+    # 1001 sequences x 64 query heads: one partial per head is 1001 * 64 * 130 * 4 B = 33 MB
+    # (4,004 (batch, kv head) rows, not whole rounds of the CUs: the split-K plan).
+    cfg = cdna4.DecodeCfg(128, 4096, 64, 4, 1001)
     assert cdna4.decode_workspace_size(cfg) > cdna4.decode_noalloc_max_bytes()
     small = torch.empty(4096, dtype=torch.float16, device=DEV)   # never read: rejected before launch
     rc = _noalloc_abi(small, small, small, small, cfg, torch.float16)
