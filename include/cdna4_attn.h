@@ -126,7 +126,10 @@ int cdna3_attn_prefill_strided(const void* Q, const void* K, const void* V, void
  * each head are read). dtype CDNA4_F16 or CDNA4_BF16 (q, K, V, o alike).
  * With a workspace (ws_bytes >= cdna3_attn_decode_workspace_size(cfg); the contents need no
  * initialisation), long caches are split over a grid of single-wave workgroups that leave
- * (m, l, O) partials in it, merged by a second kernel. With workspace == NULL the call takes
+ * (m, l, O) partials in it, merged by a second kernel, unless batch x nKVHeads x (groups of 16
+ * query heads) is a multiple of the device's CU count: then the one-launch plan below fills
+ * whole rounds of the CUs and is taken instead (the workspace is then not used). With
+ * workspace == NULL the call takes
  * the one-launch plan, which needs no memory beyond q, K, V and o: one workgroup per (batch,
  * kv head, group of 16 query heads) streams the whole cache, like the reference's launchers,
  * which take no workspace. Both forms are capturable and re-entrant across streams (a
@@ -140,8 +143,8 @@ int cdna3_attn_decode(const void* q, const void* K, const void* V, void* o,
 /*
  * cdna3_attn_decode_noalloc: no counterpart in the reference. For callers that cannot allocate
  * (code under HIP graph capture that must not call hipMalloc, tight serving loops, harnesses that
- * forbid allocation): the split-K computation of cdna3_attn_decode with a workspace, with its
- * partials in a static device array of the library (cdna3_attn_decode_noalloc_max_bytes(), 16 MiB
+ * forbid allocation): the computation of cdna3_attn_decode with a workspace, with its split-K
+ * partials (when its plan has any) in a static device array of the library (cdna3_attn_decode_noalloc_max_bytes(), 16 MiB
  * per GPU, held until the process ends) instead of a caller's workspace. The caller passes only
  * q, K, V and o; the call never allocates. Returns CDNA4_ERR_SCRATCH_TOO_SMALL when the plan's
  * partials (cdna3_attn_decode_workspace_size(cfg)) exceed the array. Every call on one GPU shares
