@@ -85,11 +85,12 @@ using OpMin = wave::xlane::Min;
 // ---- reduce -------------------------------------------------------------------------
 constexpr int kReduceThreads = 256;          // 4 waves, no LDS: each wave writes a partial
 constexpr int kReduceMaxBlocks = 2048;       // 8192 partials at most
-// 16-byte loads in flight per lane: eight for f16 inputs, four otherwise (A/B at 2^26 on the
-// MI355X, eight against four: f16 26.2 -> 23.9 us; bf16 26.0 -> 29.4; f32 49.4 -> 49.5; f64
-// 96.5 -> 110).
+// 16-byte loads in flight per lane. Each block reads kReduceThreads * 4 consecutive vectors per
+// step (its four loads per lane 4 KiB apart), the steps strided over the grid: at 2^26 on the
+// MI355X this ran f32 49.1 -> 42.8 us, f64 96.9 -> 81.0, bf16 26.0 -> 23.7 against four loads per
+// lane spread a whole grid apart (8 MiB); eight loads per lane were no faster in either layout.
 template <int DT>
-constexpr int reduce_unroll() { return DT == CDNA4_F16 ? 8 : 4; }
+constexpr int reduce_unroll() { return 4; }
 
 // kVec: in_ is 16-byte aligned and read as vectors; the nhead (< one vector) elements at head_
 // that precede it (a misaligned call's first elements) are folded in by the first threads.
@@ -112,11 +113,13 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_stage1(const void* __re
     if constexpr (kVec) {
         const u32x4* vin = (const u32x4*)in;
         const size_t nvec = n / E::VEC;
-        size_t i = tid;
-        for (; i + (kReduceUnroll - 1) * nthr < nvec; i += kReduceUnroll * nthr) {
+        constexpr size_t kGroup = (size_t)kReduceThreads * kReduceUnroll;   // vectors per block step
+        const size_t full = nvec / kGroup * kGroup;
+        for (size_t base = (size_t)blockIdx.x * kGroup; base < full; base += (size_t)gridDim.x * kGroup) {
             u32x4 v[kReduceUnroll];
 #pragma unroll
-            for (int u = 0; u < kReduceUnroll; ++u) v[u] = __builtin_nontemporal_load(vin + i + u * nthr);
+            for (int u = 0; u < kReduceUnroll; ++u)
+                v[u] = __builtin_nontemporal_load(vin + base + u * kReduceThreads + threadIdx.x);
 #pragma unroll
             for (int u = 0; u < kReduceUnroll; ++u) {
                 Acc x[E::VEC];
@@ -125,7 +128,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_stage1(const void* __re
                 for (int e = 0; e < E::VEC; ++e) acc[u] = op(acc[u], x[e]);
             }
         }
-        for (; i < nvec; i += nthr) {
+        for (size_t i = full + tid; i < nvec; i += nthr) {   // the last partial step
             Acc x[E::VEC];
             E::unpack(vin[i], x);
 #pragma unroll
