@@ -2,15 +2,16 @@
 //
 // The reference has these operations only at wave level (research/wave-primitives/
 // include/wave_primitives/wave_reduce_dpp.hpp:106-113, wave_scan_dpp.hpp:70-87). Here
-// they run over whole HBM arrays without a single LDS instruction:
+// they run over whole HBM arrays, the cross-lane work on the DPP/permlane path:
 //   reduce: stage 1 streams the input with 16-byte loads, each wave folds its share in
 //           registers and combines its 64 lanes with the DPP/permlane butterfly, then
-//           writes one partial; stage 2 (one wave) folds the partials.
-//   scan:   one pass with decoupled look-back. Each single-wave workgroup scans a tile
-//           held in registers (per-lane serial + wave scan per 64x16-byte chunk),
-//           publishes its aggregate, reads its predecessors' aggregates / prefixes 64 at
-//           a time (one per lane) and writes the output. A small fill kernel clears the
-//           tile flags first.
+//           writes one partial; stage 2 (one wave) folds the partials. No LDS.
+//   scan:   one pass with decoupled look-back. Each wave scans a tile held in registers
+//           (per-lane serial + wave scan per 64x16-byte chunk); the four waves of a
+//           workgroup meet their tile totals in LDS (one write and one read of four values
+//           per wave, the only LDS use), and the group publishes its aggregate, reads its
+//           predecessor groups' aggregates / prefixes 64 at a time (one per lane) and writes
+//           the output. A small fill kernel clears the group flags first.
 #include "common.hpp"
 #include <stdlib.h>
 #include "scan_layout.hpp"
@@ -207,7 +208,7 @@ int reduce_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) 
     return launch_status();
 }
 
-// ---- scan (decoupled look-back, single-wave workgroups) ------------------------------
+// ---- scan (decoupled look-back over groups of four single-wave tiles) ------------------
 // Scan layout per element type: 16-bit inputs load 8 bytes (4 values) per lane and vector, so
 // each lane's fp32 output vector leaves as one 16-byte store and every store instruction writes
 // 1 KiB of contiguous lines (16-byte loads of 8 values left each lane's 32-byte output as two
@@ -355,9 +356,17 @@ __device__ Acc look_back(const ScanState& st, size_t tile, Op op) {
     return acc;
 }
 
+// Wave w of workgroup g scans tile g * 4 + w (scan_layout::group_tile); the group runs one
+// look-back for its four tiles. With one tile per single-wave workgroup the look-back was the
+// bound: per-tile stamps showed a tile's loads arriving after 13 us and its look-back taking
+// another 17 us (median, ~2 us per round trip of the device-scope slot words behind the stream),
+// as prefixes trailed ~190 tiles behind the aggregates; four times fewer, larger look-back units
+// took the f32 scan at 2^26 from 125 to 102 us (16-bit inputs 112 -> 83 us, 64-bit 253 -> 202 us;
+// two or eight waves per group: 112 / 115 us).
 template <int DT, class Op, bool kVec>
-__global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, size_t n,
-                                                  void* __restrict__ out_, ScanState st) {
+__global__ __launch_bounds__(64 * scan_layout::kScanWaves) void scan_tiles(const void* __restrict__ in_, size_t n,
+                                                                           void* __restrict__ out_, ScanState st) {
+    constexpr int kWaves = scan_layout::kScanWaves;
     using E = ScanElem<DT>;
     using Acc = typename E::Acc;
     using Out = typename E::Out;
@@ -368,9 +377,14 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
     Out* out = (Out*)out_;
     Op op;
     const Acc id = Op::template identity<Acc>();
-    const unsigned lane = threadIdx.x;
-    const size_t tile = blockIdx.x;
-    const size_t base = scan_layout::tile_base(tile, TILE);
+    const unsigned lane = threadIdx.x & 63u;
+    const unsigned wave = threadIdx.x >> 6;
+    const size_t group = blockIdx.x;
+    const size_t tile = scan_layout::group_tile(group, wave);
+    const bool live = tile < (n + TILE - 1) / TILE;   // the last group's waves past the last tile: no memory access
+    const size_t base = live ? scan_layout::tile_base(tile, TILE) : 0;
+    __shared__ Acc s_tot[kWaves];   // the waves' tile totals
+    __shared__ Acc s_excl;          // the group's exclusive prefix
 
     // Aligned calls (kVec): n counts the elements of whole VEC-element vectors only (the host
     // scans the remaining n % VEC elements in scan_tail). Every tile but the last is full and
@@ -378,8 +392,8 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
     // before any arithmetic; the last tile guards each vector with a 32-bit tile-local index against the
     // uniform vector count. Misaligned calls go element by element.
     const typename E::In* tin = in + base;
-    const bool full = kVec && scan_layout::tile_full(base, TILE, n);
-    const uint32_t rem = scan_layout::tile_rem(base, TILE, n);  // elements
+    const bool full = live && kVec && scan_layout::tile_full(base, TILE, n);
+    const uint32_t rem = live ? scan_layout::tile_rem(base, TILE, n) : 0u;  // elements (0: none)
     Acc v[U][VEC];
     if constexpr (kVec) {
         const typename E::Load* src = (const typename E::Load*)tin + lane;
@@ -427,15 +441,31 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
     for (int j = 0; j < U; ++j)
 #pragma unroll
         for (int e = 0; e < VEC; ++e) asm volatile("" : "+v"(v[j][e]));
-    const Acc tile_total = run;
-    Acc excl = id;
-    if (tile == 0) {
-        publish(st.pre, tile, tile_total, kTagPre);
-    } else {
-        publish(st.agg, tile, tile_total, kTagAgg);
-        excl = look_back<Acc>(st, tile, op);
-        publish(st.pre, tile, op(excl, tile_total), kTagPre);
+    // Group combine: each wave's prefix within the group and the group total; wave 0 publishes
+    // and runs the look-back (publish and look_back take the lane from threadIdx.x: wave 0 only).
+    if (lane == 0) s_tot[wave] = run;
+    __syncthreads();
+    Acc wpre = id, gtot = id;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const Acc t = s_tot[w];
+        if (w < (int)wave) wpre = op(wpre, t);
+        gtot = op(gtot, t);
     }
+    if (wave == 0) {
+        Acc gex = id;
+        if (group == 0) {
+            publish(st.pre, group, gtot, kTagPre);
+        } else {
+            publish(st.agg, group, gtot, kTagAgg);
+            gex = look_back<Acc>(st, group, op);
+            publish(st.pre, group, op(gex, gtot), kTagPre);
+        }
+        if (lane == 0) s_excl = gex;
+    }
+    __syncthreads();
+    const Acc excl = op(s_excl, wpre);
+    if (!live) return;
     Out* tout = out + base;
     if constexpr (kVec) {
         constexpr int kWords = (int)(sizeof(Out) * VEC / 16);
@@ -466,10 +496,10 @@ __global__ __launch_bounds__(64) void scan_tiles(const void* __restrict__ in_, s
 }
 
 // The last n % VEC (< VEC) elements of an aligned call, after scan_tiles has published every
-// tile's inclusive prefix: lane 0 continues the running value from the last tile's prefix.
+// group's inclusive prefix: lane 0 continues the running value from the last group's prefix.
 template <int DT, class Op>
 __global__ __launch_bounds__(64) void scan_tail(const void* __restrict__ in_, size_t from, size_t n,
-                                                 void* __restrict__ out_, ScanState st, size_t ntiles) {
+                                                 void* __restrict__ out_, ScanState st, size_t ngroups) {
     using E = Elem<DT>;
     using Acc = typename E::Acc;
     using Out = typename E::Out;
@@ -478,7 +508,7 @@ __global__ __launch_bounds__(64) void scan_tail(const void* __restrict__ in_, si
     Op op;
     Acc acc = Op::template identity<Acc>();
     bool ok = true;
-    if (ntiles > 0) ok = read_slot<Acc>(st.pre, (long long)ntiles - 1, kTagPre, acc);
+    if (ngroups > 0) ok = read_slot<Acc>(st.pre, (long long)ngroups - 1, kTagPre, acc);
     if (threadIdx.x == 0) {
         if (!ok) __hip_atomic_store(st.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         for (size_t i = from; i < n; ++i) {
@@ -521,22 +551,24 @@ int scan_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
     const bool vec = ((uintptr_t)in % 16) == 0 && ((uintptr_t)out % 16) == 0;
     const size_t n_main = scan_layout::main_elems(n, vec, (int)VEC);
     const size_t ntiles = vec ? scan_tiles_for<DT, true>(n_main) : scan_tiles_for<DT, false>(n_main);
+    const size_t ngroups = scan_layout::groups_for(ntiles);   // look-back slots: one per group
     char* w = (char*)ws;
     ScanState st;
     st.error = (uint32_t*)w;
     st.spin_limit = scan_spin_limit();
     st.agg = (uint64_t*)(w + scan_layout::agg_offset());
-    st.pre = (uint64_t*)(w + scan_layout::pre_offset(ntiles));
+    st.pre = (uint64_t*)(w + scan_layout::pre_offset(ngroups));
     // Both slot arrays are cleared in one pass (the pre array directly follows the agg array).
-    const size_t nwords = scan_layout::clear_words(ntiles, Words<Acc>::NW);
+    const size_t nwords = scan_layout::clear_words(ngroups, Words<Acc>::NW);
     scan_clear<<<(unsigned)(nwords == 0 ? 1 : ceil_div(nwords, 256)), 256, 0, s>>>(st.agg, nwords, st.error);
-    if (ntiles > 0) {
+    constexpr unsigned kThreads = 64 * scan_layout::kScanWaves;
+    if (ngroups > 0) {
         if (vec)
-            scan_tiles<DT, Op, true><<<(unsigned)ntiles, 64, 0, s>>>(in, n_main, out, st);
+            scan_tiles<DT, Op, true><<<(unsigned)ngroups, kThreads, 0, s>>>(in, n_main, out, st);
         else
-            scan_tiles<DT, Op, false><<<(unsigned)ntiles, 64, 0, s>>>(in, n_main, out, st);
+            scan_tiles<DT, Op, false><<<(unsigned)ngroups, kThreads, 0, s>>>(in, n_main, out, st);
     }
-    if (n_main < n) scan_tail<DT, Op><<<1, 64, 0, s>>>(in, n_main, n, out, st, ntiles);
+    if (n_main < n) scan_tail<DT, Op><<<1, 64, 0, s>>>(in, n_main, n, out, st, ngroups);
     return launch_status();
 }
 

@@ -16,8 +16,10 @@ constexpr size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 constexpr size_t tile_elems(int vec, int u) { return (size_t)64 * vec * u; }
 constexpr size_t tiles_for(size_t n, int vec, int u) { return (n + tile_elems(vec, u) - 1) / tile_elems(vec, u); }
 
-// Workspace: [error word, padded to 256 B][agg slots: align256(ntiles * 16)][pre slots: ntiles * 16],
-// two 64-bit words per tile and array (one used by 32-bit values).
+// Workspace for `nslots` look-back slots (one per tile group): [error word, padded to 256 B]
+// [agg slots: align256(nslots * 16)][pre slots: nslots * 16], two 64-bit words per slot and array
+// (one used by 32-bit values). The library sizes it by the misaligned path's tile count, which
+// bounds the group count of either path.
 constexpr size_t ws_bytes(size_t ntiles) { return 256 + 2 * align256(ntiles * 16); }
 constexpr size_t agg_offset() { return 256; }
 constexpr size_t pre_offset(size_t ntiles) { return 256 + align256(ntiles * 16); }
@@ -44,7 +46,15 @@ constexpr bool vec_live(bool full, int j, unsigned lane, uint32_t rem, int VEC) 
 // Element e of vector j of a lane on the element-wise (misaligned) path, and its guard.
 constexpr uint32_t elem_in_tile(int j, unsigned lane, int e, int VEC) { return vec_in_tile(j, lane) * (uint32_t)VEC + e; }
 
-// 64-bit word w of tile t's slot (NW words per slot).
+// Tiles run in workgroups of kScanWaves waves, one tile per wave: wave w of workgroup g scans tile
+// g * kScanWaves + w (waves past the last tile load and store nothing). The waves' totals meet in
+// the workgroup, and the look-back state (a slot per published value) is per workgroup: a group
+// publishes the total of its tiles and then its inclusive prefix.
+constexpr int kScanWaves = 4;
+constexpr size_t groups_for(size_t ntiles) { return (ntiles + kScanWaves - 1) / kScanWaves; }
+constexpr size_t group_tile(size_t group, unsigned wave) { return group * kScanWaves + wave; }
+
+// 64-bit word w of group (slot) t's slot (NW words per slot).
 constexpr size_t slot_word(size_t tile, int nw, unsigned w) { return tile * (size_t)nw + w; }
 
 }  // namespace scan_layout

@@ -2,9 +2,10 @@
 //
 // Uses the same constexpr functions the kernels and their launcher use
 // (amd-incstinct-labs_amd/csrc/scan_layout.hpp) and walks, for each element type, tile size and
-// input size given, every vector / element load and store of every lane of every tile, every
-// tile-slot word a tile publishes or reads during its look-back, the clear kernel's range and the
-// tail's reads, checking each against the sizes of the input, output and workspace buffers (the
+// input size given, every vector / element load and store of every lane of every tile (tiles in
+// groups of kScanWaves waves, the last group's extra waves touching nothing), every slot word a
+// tile group publishes or reads during its look-back, the clear kernel's range and the tail's
+// reads, checking each against the sizes of the input, output and workspace buffers (the
 // workspace sized as cdna3_scan_workspace_size sizes it). Both the aligned (16-byte vector) and the
 // misaligned (element-wise, half-size tiles) paths are replayed.
 // Usage: scan_layout_check [--plant] U n [n ...]   (U = vectors per lane of the aligned path;
@@ -57,12 +58,19 @@ static void replay(const Type& T, int U, size_t n, size_t in_off) {
     const size_t TILE = sl::tile_elems(VEC, u);
     const size_t in_end = in_off + n * (size_t)T.in_bytes;   // bytes of the input buffer from its 16-byte base
     const size_t out_end = n * (size_t)T.out_bytes;
-    const size_t slot_bytes = ntiles * (size_t)T.NW * 8;
-    CHECK(ntiles <= ws_tiles, "%s U%d n%zu: %zu tiles, workspace sized for %zu", T.name, U, n, ntiles, ws_tiles);
-    CHECK(sl::agg_offset() >= 4 && sl::agg_offset() + slot_bytes <= sl::pre_offset(ntiles), "%s n%zu agg", T.name, n);
-    CHECK(sl::pre_offset(ntiles) + slot_bytes <= ws, "%s n%zu pre", T.name, n);
-    const size_t clear_end = sl::agg_offset() + sl::clear_words(ntiles, T.NW) * 8;
-    CHECK(clear_end <= ws && clear_end >= sl::pre_offset(ntiles) + slot_bytes, "%s n%zu clear", T.name, n);
+    const size_t ngroups = sl::groups_for(ntiles);
+    const size_t slot_bytes = ngroups * (size_t)T.NW * 8;
+    CHECK(ngroups <= ws_tiles, "%s U%d n%zu: %zu groups, workspace sized for %zu", T.name, U, n, ngroups, ws_tiles);
+    CHECK(sl::agg_offset() >= 4 && sl::agg_offset() + slot_bytes <= sl::pre_offset(ngroups), "%s n%zu agg", T.name, n);
+    CHECK(sl::pre_offset(ngroups) + slot_bytes <= ws, "%s n%zu pre", T.name, n);
+    const size_t clear_end = sl::agg_offset() + sl::clear_words(ngroups, T.NW) * 8;
+    CHECK(clear_end <= ws && clear_end >= sl::pre_offset(ngroups) + slot_bytes, "%s n%zu clear", T.name, n);
+    // every wave of every group maps to one tile; exactly the tiles below ntiles are live
+    size_t live_tiles = 0;
+    for (size_t g = 0; g < ngroups; ++g)
+        for (unsigned wv = 0; wv < (unsigned)sl::kScanWaves; ++wv)
+            if (sl::group_tile(g, wv) < ntiles) ++live_tiles;
+    CHECK(live_tiles == ntiles, "%s n%zu: groups cover %zu of %zu tiles", T.name, n, live_tiles, ntiles);
     for (size_t t = 0; t < ntiles; ++t) {
         const size_t base = sl::tile_base(t, TILE);
         CHECK(base < n_main, "%s n%zu tile %zu base %zu", T.name, n, t, base);
@@ -93,24 +101,26 @@ static void replay(const Type& T, int U, size_t n, size_t in_off) {
                 }
             }
         }
-        // publish: lanes 0 .. NW-1 write the words of tile t's slot in both arrays
+    }
+    for (size_t t = 0; t < ngroups; ++t) {
+        // publish: lanes 0 .. NW-1 of wave 0 write the words of group t's slot in both arrays
         for (unsigned w = 0; w < (unsigned)T.NW; ++w)
-            CHECK((sl::slot_word(t, T.NW, w) + 1) * 8 <= slot_bytes, "%s n%zu publish tile %zu", T.name, n, t);
-        // look-back: window positions pos = t - 1, t - 65, ...; lane l reads tile pos - l when >= 0
+            CHECK((sl::slot_word(t, T.NW, w) + 1) * 8 <= slot_bytes, "%s n%zu publish group %zu", T.name, n, t);
+        // look-back: window positions pos = t - 1, t - 65, ...; lane l reads group pos - l when >= 0
         for (long long pos = (long long)t - 1; pos >= 0; pos -= 64)
             for (unsigned lane = 0; lane < 64; ++lane) {
                 const long long r = pos - (long long)lane;
                 if (r < 0) continue;
-                CHECK(r < (long long)t, "%s look-back reads a later tile", T.name);
+                CHECK(r < (long long)t, "%s look-back reads a later group", T.name);
                 for (unsigned w = 0; w < (unsigned)T.NW; ++w)
-                    CHECK((sl::slot_word((size_t)r, T.NW, w) + 1) * 8 <= slot_bytes, "%s n%zu read tile %lld", T.name,
+                    CHECK((sl::slot_word((size_t)r, T.NW, w) + 1) * 8 <= slot_bytes, "%s n%zu read group %lld", T.name,
                           n, r);
             }
     }
     // the one-wave tail of an aligned call: the last tile's prefix, then elements n_main .. n-1
     if (n_main < n) {
         CHECK(vec, "%s tail on the misaligned path", T.name);
-        if (ntiles > 0) CHECK((sl::slot_word(ntiles - 1, T.NW, T.NW - 1) + 1) * 8 <= slot_bytes, "%s tail slot", T.name);
+        if (ngroups > 0) CHECK((sl::slot_word(ngroups - 1, T.NW, T.NW - 1) + 1) * 8 <= slot_bytes, "%s tail slot", T.name);
         CHECK(n - n_main < (size_t)VEC, "%s tail longer than a vector", T.name);
         CHECK(in_off + n * T.in_bytes <= in_end && n * T.out_bytes <= out_end, "%s tail", T.name);
     }
