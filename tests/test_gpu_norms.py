@@ -36,6 +36,24 @@ def test_layernorm(M, H):
         np.testing.assert_allclose(y.var(1), 1.0, atol=1e-2)
 
 
+@pytest.mark.parametrize("M,H", [(65536, 512), (262144, 64)])
+def test_norms_streaming_policy_sizes(M, H):
+    # Tensors of 64 MiB or more take the kernels with non-temporal loads and stores (the row-cached
+    # form at 512 columns, the four-rows-per-wave form at 64); checked on a sample of rows.
+    g = torch.Generator(device=DEV).manual_seed(M + H)
+    Xt = torch.randn(M, H, device=DEV, generator=g) * 2.0
+    rows = np.unique(np.concatenate([np.arange(8), np.arange(M - 8, M), oracle.integers(M + H, 200, 0, M - 1)]))
+    X = Xt[torch.from_numpy(rows).to(DEV)].cpu().numpy()
+    wv, wb = oracle.round16(oracle.normal(H, H, 1.0, 0.1), oracle.F16)
+    Wt = torch.from_numpy(wb.view(np.int16)).view(torch.float16).to(DEV)
+    got = cdna4.rmsnorm_f32(Xt, Wt, 1e-6)[torch.from_numpy(rows).to(DEV)].cpu().numpy()
+    np.testing.assert_allclose(got, oracle.rmsnorm(X, wb, 1e-6), rtol=1e-5, atol=1e-5)
+    gm, bt = oracle.uniform(1, H, 0.5, 1.5), oracle.uniform(2, H)
+    got = cdna4.layernorm_f32(Xt, torch.from_numpy(gm).to(DEV), torch.from_numpy(bt).to(DEV),
+                              1e-5)[torch.from_numpy(rows).to(DEV)].cpu().numpy()
+    np.testing.assert_allclose(got, oracle.layernorm(X, gm, bt, 1e-5), rtol=1e-4, atol=2e-5)
+
+
 @pytest.mark.parametrize("seq,heads,D,pos0", [(512, 12, 64, 0), (1, 12, 64, 511), (33, 8, 128, 1000), (4, 2, 10, 3)])
 def test_rope_table_and_rope(seq, heads, D, pos0):
     cos, sin = cdna4.rope_table_f32(pos0, seq, D, 10000.0)
