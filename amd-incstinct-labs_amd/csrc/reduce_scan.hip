@@ -2,16 +2,16 @@
 //
 // The reference has these operations only at wave level (research/wave-primitives/
 // include/wave_primitives/wave_reduce_dpp.hpp:106-113, wave_scan_dpp.hpp:70-87). Here
-// they run over whole HBM arrays, the cross-lane work on the DPP/permlane path:
+// they run over whole HBM arrays without a single LDS instruction:
 //   reduce: stage 1 streams the input with 16-byte loads, each wave folds its share in
 //           registers and combines its 64 lanes with the DPP/permlane butterfly, then
-//           writes one partial; stage 2 (one wave) folds the partials. No LDS.
+//           writes one partial; stage 2 (one wave) folds the partials.
 //   scan:   one pass with decoupled look-back. Each wave scans a tile held in registers
 //           (per-lane serial + wave scan per 64x16-byte chunk); the four waves of a
-//           workgroup meet their tile totals in LDS (one write and one read of four values
-//           per wave, the only LDS use), and the group publishes its aggregate, reads its
-//           predecessor groups' aggregates / prefixes 64 at a time (one per lane) and writes
-//           the output. A small fill kernel clears the group flags first.
+//           workgroup meet their tile totals in a line of the workspace, and the group
+//           publishes its aggregate, reads its predecessor groups' aggregates / prefixes 64
+//           at a time (one per lane) and writes the output. A small fill kernel clears the
+//           group flags first. No LDS in either.
 #include "common.hpp"
 #include <stdlib.h>
 #include "scan_layout.hpp"
@@ -248,6 +248,7 @@ struct ScanState {
     uint64_t* pre;    // per tile: NW words
     uint32_t* error;  // set when a look-back wait exceeds its bound
     uint32_t spin_limit;   // sleeps a look-back waits for a predecessor before it gives up
+    unsigned char* xchg;   // per group a 128-byte line: its waves' tile totals, then its prefix
 };
 
 constexpr uint32_t kSpinLimit = 1u << 22;
@@ -383,8 +384,12 @@ __global__ __launch_bounds__(64 * scan_layout::kScanWaves) void scan_tiles(const
     const size_t tile = scan_layout::group_tile(group, wave);
     const bool live = tile < (n + TILE - 1) / TILE;   // the last group's waves past the last tile: no memory access
     const size_t base = live ? scan_layout::tile_base(tile, TILE) : 0;
-    __shared__ Acc s_tot[kWaves];   // the waves' tile totals
-    __shared__ Acc s_excl;          // the group's exclusive prefix
+    // The group's exchange line in the workspace (global memory, no LDS): the waves' tile totals,
+    // then the group's exclusive prefix. Written before and read after a workgroup barrier, as
+    // reduce_stage2 meets its waves; each group owns a whole 128-byte line. In LDS the same
+    // exchange measured no faster (102.5 against 103.2 us at f32 2^26).
+    Acc* s_tot = (Acc*)(st.xchg + group * scan_layout::kXchgStride);
+    Acc* s_excl = s_tot + kWaves;
 
     // Aligned calls (kVec): n counts the elements of whole VEC-element vectors only (the host
     // scans the remaining n % VEC elements in scan_tail). Every tile but the last is full and
@@ -443,6 +448,7 @@ __global__ __launch_bounds__(64 * scan_layout::kScanWaves) void scan_tiles(const
         for (int e = 0; e < VEC; ++e) asm volatile("" : "+v"(v[j][e]));
     // Group combine: each wave's prefix within the group and the group total; wave 0 publishes
     // and runs the look-back (publish and look_back take the lane from threadIdx.x: wave 0 only).
+    // The barriers order the exchange line's writes before its reads within the workgroup.
     if (lane == 0) s_tot[wave] = run;
     __syncthreads();
     Acc wpre = id, gtot = id;
@@ -461,10 +467,10 @@ __global__ __launch_bounds__(64 * scan_layout::kScanWaves) void scan_tiles(const
             gex = look_back<Acc>(st, group, op);
             publish(st.pre, group, op(gex, gtot), kTagPre);
         }
-        if (lane == 0) s_excl = gex;
+        if (lane == 0) *s_excl = gex;
     }
     __syncthreads();
-    const Acc excl = op(s_excl, wpre);
+    const Acc excl = op(*s_excl, wpre);
     if (!live) return;
     Out* tout = out + base;
     if constexpr (kVec) {
@@ -558,6 +564,7 @@ int scan_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
     st.spin_limit = scan_spin_limit();
     st.agg = (uint64_t*)(w + scan_layout::agg_offset());
     st.pre = (uint64_t*)(w + scan_layout::pre_offset(ngroups));
+    st.xchg = (unsigned char*)w + scan_layout::xchg_offset(ngroups);
     // Both slot arrays are cleared in one pass (the pre array directly follows the agg array).
     const size_t nwords = scan_layout::clear_words(ngroups, Words<Acc>::NW);
     scan_clear<<<(unsigned)(nwords == 0 ? 1 : ceil_div(nwords, 256)), 256, 0, s>>>(st.agg, nwords, st.error);

@@ -17,12 +17,16 @@ constexpr size_t tile_elems(int vec, int u) { return (size_t)64 * vec * u; }
 constexpr size_t tiles_for(size_t n, int vec, int u) { return (n + tile_elems(vec, u) - 1) / tile_elems(vec, u); }
 
 // Workspace for `nslots` look-back slots (one per tile group): [error word, padded to 256 B]
-// [agg slots: align256(nslots * 16)][pre slots: nslots * 16], two 64-bit words per slot and array
-// (one used by 32-bit values). The library sizes it by the misaligned path's tile count, which
-// bounds the group count of either path.
-constexpr size_t ws_bytes(size_t ntiles) { return 256 + 2 * align256(ntiles * 16); }
+// [agg slots: align256(nslots * 16)][pre slots: align256(nslots * 16)][exchange lines:
+// nslots * kXchgStride], two 64-bit words per slot and array (one used by 32-bit values), and per
+// group one 128-byte line in which its waves leave their tile totals and wave 0 the group's prefix
+// (kScanWaves + 1 values of at most 8 bytes). The library sizes it by the misaligned path's tile
+// count, which bounds the group count of either path.
+constexpr size_t kXchgStride = 128;
+constexpr size_t ws_bytes(size_t ntiles) { return 256 + 2 * align256(ntiles * 16) + align256(ntiles * kXchgStride); }
 constexpr size_t agg_offset() { return 256; }
 constexpr size_t pre_offset(size_t ntiles) { return 256 + align256(ntiles * 16); }
+constexpr size_t xchg_offset(size_t ntiles) { return pre_offset(ntiles) + align256(ntiles * 16); }
 // 64-bit words the clear kernel zeroes from the start of the agg array: the whole agg array and
 // the used part of the pre array that follows it.
 constexpr size_t clear_words(size_t ntiles, int nw) { return (align256(ntiles * 16) + ntiles * (size_t)nw * 8) / 8; }
@@ -51,6 +55,7 @@ constexpr uint32_t elem_in_tile(int j, unsigned lane, int e, int VEC) { return v
 // the workgroup, and the look-back state (a slot per published value) is per workgroup: a group
 // publishes the total of its tiles and then its inclusive prefix.
 constexpr int kScanWaves = 4;
+static_assert((kScanWaves + 1) * 8 <= (int)kXchgStride, "a group's exchange values fit its line");
 constexpr size_t groups_for(size_t ntiles) { return (ntiles + kScanWaves - 1) / kScanWaves; }
 constexpr size_t group_tile(size_t group, unsigned wave) { return group * kScanWaves + wave; }
 

@@ -103,6 +103,10 @@ static void replay(const Type& T, int U, size_t n, size_t in_off) {
         }
     }
     for (size_t t = 0; t < ngroups; ++t) {
+        // the group's exchange line: kScanWaves tile totals and the group prefix, 8 bytes each at most
+        const size_t x0 = sl::xchg_offset(ngroups) + t * sl::kXchgStride;
+        CHECK(x0 >= sl::pre_offset(ngroups) + slot_bytes && x0 % 128 == 0, "%s n%zu exchange line %zu", T.name, n, t);
+        CHECK(x0 + (size_t)(sl::kScanWaves + 1) * 8 <= ws, "%s n%zu exchange line %zu past the workspace", T.name, n, t);
         // publish: lanes 0 .. NW-1 of wave 0 write the words of group t's slot in both arrays
         for (unsigned w = 0; w < (unsigned)T.NW; ++w)
             CHECK((sl::slot_word(t, T.NW, w) + 1) * 8 <= slot_bytes, "%s n%zu publish group %zu", T.name, n, t);
