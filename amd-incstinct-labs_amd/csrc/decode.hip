@@ -267,6 +267,49 @@ __global__ __launch_bounds__(64) void decode_merge(const float* __restrict__ par
     }
 }
 
+// The merge for P <= NR partials: every load (each partial's (m, l) on lane p, and all NR rows)
+// issued before any arithmetic, so the merge costs one memory round trip instead of one for the
+// (m, l) values and one per sixteen rows. Same arithmetic and order as decode_merge (bit-identical).
+template <int D, bool kBf16, int NR>
+__global__ __launch_bounds__(64) void decode_merge_short(const float* __restrict__ part_ml,
+                                                         const float* __restrict__ part_o, void* __restrict__ out,
+                                                         int P) {
+    constexpr int EPL = D / 64;
+    static_assert(NR <= 64, "one partial per lane");
+    const unsigned lane = threadIdx.x;
+    const size_t bh = blockIdx.x;
+    const float* ml = part_ml + bh * P * 2;
+    const float* pi = part_o + bh * P * D + lane * EPL;
+    const bool has = (int)lane < P;
+    const float mi = has ? ml[2 * lane] : -INFINITY;
+    const float li = has ? ml[2 * lane + 1] : 0.f;
+    float v[NR][EPL];   // rows past P re-read row P - 1 and are weighted 0
+#pragma unroll
+    for (int j = 0; j < NR; ++j)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[j][e] = pi[(size_t)min(j, P - 1) * D + e];
+    const float M = allreduce(mi, Max{});
+    const float Mref = (M == -INFINITY) ? 0.f : M;
+    const float wl = has ? exp2f(mi - Mref) : 0.f;
+    const float L = allreduce(has ? li * exp2f(mi - Mref) : 0.f, Sum{});
+    float acc[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+        const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), j));
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] = fmaf(w, v[j][e], acc[e]);
+    }
+    const float inv = (L > 0.f) ? 1.f / L : 1.f;
+    uint16_t* o = (uint16_t*)out + bh * D + lane * EPL;
+    if constexpr (EPL == 2) {
+        *(uint32_t*)o = pack2<kBf16>(acc[0] * inv, acc[1] * inv);
+    } else {
+        o[0] = (uint16_t)(kBf16 ? f32_to_bf16_bits(acc[0] * inv) : f32_to_f16_bits(acc[0] * inv));
+    }
+}
+
 struct Plan { int G, HB, KPW, P; size_t ws_bytes; bool wg, nt; };
 
 // Waves per workgroup of the short-cache variant (its LDS holds W rings of two K and V stages)
@@ -346,7 +389,10 @@ int launch_decode(const cdna3_decode_cfg& c, const Plan& p, const void* q, const
     }
     if (!ws) return CDNA4_ERR_INVALID_VALUE;
     decode_mfma<D, kBf16, kDecStages><<<grid, 64, 0, s>>>(a);
-    decode_merge<D, kBf16><<<(unsigned)((size_t)c.batch * c.nQHeads), 64, 0, s>>>(a.part_ml, a.part_o, o, p.P);
+    const unsigned nbh = (unsigned)((size_t)c.batch * c.nQHeads);
+    if (p.P <= 16) decode_merge_short<D, kBf16, 16><<<nbh, 64, 0, s>>>(a.part_ml, a.part_o, o, p.P);
+    else if (p.P <= 64) decode_merge_short<D, kBf16, 64><<<nbh, 64, 0, s>>>(a.part_ml, a.part_o, o, p.P);
+    else decode_merge<D, kBf16><<<nbh, 64, 0, s>>>(a.part_ml, a.part_o, o, p.P);
     return launch_status();
 }
 

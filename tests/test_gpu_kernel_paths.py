@@ -316,6 +316,12 @@ def test_decode_split_n8191():
     check_decode(128, 8191, 32, 8, 1, torch.bfloat16, "decode_split")
 
 
+def test_decode_split_few_partials():
+    # 64 (batch, kv head) rows: 16 partials per head, the sixteen-row form of the one-round-trip merge
+    plan = check_decode(128, 4096, 32, 8, 8, torch.float16, "decode_split", seed=5)
+    assert plan.partials <= 16
+
+
 def test_decode_split_more_than_64_partials():
     # batch 1 with one kv head: P > 64, so the merge runs several 64-partial passes.
     plan = check_decode(128, 65536, 4, 1, 1, torch.float16, "decode_split", seed=3)
