@@ -146,9 +146,9 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_stage1(const void* __re
     if ((threadIdx.x & 63u) == 0) ((Acc*)part_)[blockIdx.x * (kReduceThreads / 64) + threadIdx.x / 64] = a;
 }
 
-// Stage 2: 16 waves fold the partials with independent loads in flight (one memory round trip
-// instead of a dependent chain), each wave writes one value after the partials, and after the
-// workgroup barrier wave 0 folds those 16. Deterministic order, no LDS.
+// Stage 2: 16 waves fold the partials (at most eight per thread, all eight loads issued before
+// the first is used: one memory round trip), each wave writes one value after the partials, and
+// after the workgroup barrier wave 0 folds those 16. Deterministic order, no LDS.
 constexpr int kReduce2Threads = 1024;
 
 template <int DT, class Op>
@@ -158,14 +158,15 @@ __global__ __launch_bounds__(kReduce2Threads) void reduce_stage2(void* __restric
     Acc* part = (Acc*)part_;
     Op op;
     const Acc id = Op::template identity<Acc>();
-    Acc acc[4] = {id, id, id, id};
-    int i = threadIdx.x;
-    for (; i + 3 * kReduce2Threads < count; i += 4 * kReduce2Threads) {
+    static_assert(kReduceMaxBlocks * (kReduceThreads / 64) <= 8 * kReduce2Threads, "eight partials per thread");
+    Acc v[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[u] = op(acc[u], part[i + u * kReduce2Threads]);
+    for (int u = 0; u < 8; ++u) {
+        const int i = (int)threadIdx.x + u * kReduce2Threads;
+        v[u] = i < count ? part[i] : id;
     }
-    for (; i < count; i += kReduce2Threads) acc[0] = op(acc[0], part[i]);
-    Acc a = allreduce(op(op(acc[0], acc[1]), op(acc[2], acc[3])), op);
+    Acc a = op(op(op(v[0], v[1]), op(v[2], v[3])), op(op(v[4], v[5]), op(v[6], v[7])));
+    a = allreduce(a, op);
     Acc* wave_vals = part + count;   // kReduce2Threads / 64 slots after the partials
     if ((threadIdx.x & 63u) == 0) wave_vals[threadIdx.x >> 6] = a;
     __syncthreads();
