@@ -82,26 +82,42 @@ __global__ __launch_bounds__(256) void rmsnorm_vec(const float* __restrict__ X, 
 }
 
 // H <= 64 (H % 4 == 0): one 16-lane DPP row per norm row, four rows per wave, one float4 per lane,
-// so short rows keep all 64 lanes busy. Lanes of rows past M run on zeros (the row reductions need
-// every lane of the row) and store nothing.
-constexpr int kRows16 = 16;   // rows per 256-thread block
+// so short rows keep all 64 lanes busy; each 16-lane row takes kRowsPerLane norm rows kRows16
+// apart (a block's r-th loads are one contiguous run), all of its loads issued before any
+// arithmetic. Lanes of rows past M run on zeros (the row reductions need every lane of the row)
+// and store nothing.
+constexpr int kRows16 = 16;      // rows per 256-thread block and load
+// Norm rows per 16-lane row: at 65536 x 64 (f32, inputs from HBM) 1 / 2 / 4 / 8 took LayerNorm
+// 7.83 / 7.35 / 7.95 / 8.67 us and RMSNorm 7.66 / 7.25 / 7.24 / 7.77 us.
+constexpr int kRowsPerLane = 2;
 template <bool kNT>
 __global__ __launch_bounds__(256) void rmsnorm_row16(const float* __restrict__ X, const uint16_t* __restrict__ W,
                                                      float* __restrict__ Y, int M, int H, float eps) {
     const int c = (int)(threadIdx.x & 15u) * 4;
-    const int row = blockIdx.x * kRows16 + (int)(threadIdx.x >> 4);
-    const bool in = row < M && c < H;
-    const float4 v = in ? ld4<kNT>(X + (size_t)row * H + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float ss = row_allreduce((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w), Sum{});
-    const float inv = rsqrtf(ss / (float)H + eps);
-    if (in) {
-        const uint2 wb = *(const uint2*)(W + c);
-        float4 o;
-        o.x = v.x * inv * f16_bits_to_f32(wb.x & 0xffffu);
-        o.y = v.y * inv * f16_bits_to_f32(wb.x >> 16);
-        o.z = v.z * inv * f16_bits_to_f32(wb.y & 0xffffu);
-        o.w = v.w * inv * f16_bits_to_f32(wb.y >> 16);
-        st4<kNT>(Y + (size_t)row * H + c, o);
+    const int row0 = blockIdx.x * (kRows16 * kRowsPerLane) + (int)(threadIdx.x >> 4);
+    float4 v[kRowsPerLane];
+#pragma unroll
+    for (int r = 0; r < kRowsPerLane; ++r) {
+        const int row = row0 + r * kRows16;
+        v[r] = row < M && c < H ? ld4<kNT>(X + (size_t)row * H + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const uint2 wb = c < H ? *(const uint2*)(W + c) : make_uint2(0u, 0u);
+    const float w0 = f16_bits_to_f32(wb.x & 0xffffu), w1 = f16_bits_to_f32(wb.x >> 16);
+    const float w2 = f16_bits_to_f32(wb.y & 0xffffu), w3 = f16_bits_to_f32(wb.y >> 16);
+#pragma unroll
+    for (int r = 0; r < kRowsPerLane; ++r) {
+        const int row = row0 + r * kRows16;
+        const float ss =
+            row_allreduce((v[r].x * v[r].x + v[r].y * v[r].y) + (v[r].z * v[r].z + v[r].w * v[r].w), Sum{});
+        const float inv = rsqrtf(ss / (float)H + eps);
+        if (row < M && c < H) {
+            float4 o;
+            o.x = v[r].x * inv * w0;
+            o.y = v[r].y * inv * w1;
+            o.z = v[r].z * inv * w2;
+            o.w = v[r].w * inv * w3;
+            st4<kNT>(Y + (size_t)row * H + c, o);
+        }
     }
 }
 
@@ -166,25 +182,34 @@ __global__ __launch_bounds__(256) void layernorm_row16(const float* __restrict__
                                                        const float* __restrict__ B, float* __restrict__ Y, int M,
                                                        int H, float eps) {
     const int c = (int)(threadIdx.x & 15u) * 4;
-    const int row = blockIdx.x * kRows16 + (int)(threadIdx.x >> 4);
-    const bool in = row < M && c < H;
-    const float4 v = in ? ld4<kNT>(X + (size_t)row * H + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float mean = row_allreduce((v.x + v.y) + (v.z + v.w), Sum{}) / (float)H;
-    // Second pass over the register-cached deviations (padding lanes contribute 0).
-    float q = 0.f;
-    if (c < H) {
-        const float a = v.x - mean, b = v.y - mean, d = v.z - mean, e = v.w - mean;
-        q = (a * a + b * b) + (d * d + e * e);
+    const int row0 = blockIdx.x * (kRows16 * kRowsPerLane) + (int)(threadIdx.x >> 4);
+    float4 v[kRowsPerLane];
+#pragma unroll
+    for (int r = 0; r < kRowsPerLane; ++r) {
+        const int row = row0 + r * kRows16;
+        v[r] = row < M && c < H ? ld4<kNT>(X + (size_t)row * H + c) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    const float inv = rsqrtf(row_allreduce(q, Sum{}) / (float)H + eps);
-    if (in) {
-        const float4 g = *(const float4*)(G + c), bb = *(const float4*)(B + c);
-        float4 o;
-        o.x = (v.x - mean) * inv * g.x + bb.x;
-        o.y = (v.y - mean) * inv * g.y + bb.y;
-        o.z = (v.z - mean) * inv * g.z + bb.z;
-        o.w = (v.w - mean) * inv * g.w + bb.w;
-        st4<kNT>(Y + (size_t)row * H + c, o);
+    const float4 g = c < H ? *(const float4*)(G + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 bb = c < H ? *(const float4*)(B + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < kRowsPerLane; ++r) {
+        const int row = row0 + r * kRows16;
+        const float mean = row_allreduce((v[r].x + v[r].y) + (v[r].z + v[r].w), Sum{}) / (float)H;
+        // Second pass over the register-cached deviations (padding lanes contribute 0).
+        float q = 0.f;
+        if (c < H) {
+            const float a = v[r].x - mean, b = v[r].y - mean, d = v[r].z - mean, e = v[r].w - mean;
+            q = (a * a + b * b) + (d * d + e * e);
+        }
+        const float inv = rsqrtf(row_allreduce(q, Sum{}) / (float)H + eps);
+        if (row < M && c < H) {
+            float4 o;
+            o.x = (v[r].x - mean) * inv * g.x + bb.x;
+            o.y = (v[r].y - mean) * inv * g.y + bb.y;
+            o.z = (v[r].z - mean) * inv * g.z + bb.z;
+            o.w = (v[r].w - mean) * inv * g.w + bb.w;
+            st4<kNT>(Y + (size_t)row * H + c, o);
+        }
     }
 }
 
@@ -273,8 +298,8 @@ extern "C" int cdna3_rmsnorm_f32(const float* X, const void* W, float* Y, int M,
     }
     const bool nt = (size_t)M * (size_t)H * sizeof(float) >= kStreamBytes;
     if (H <= 64) {
-        if (nt) rmsnorm_row16<true><<<ceil_div((size_t)M, kRows16), 256, 0, s>>>(X, w, Y, M, H, eps);
-        else rmsnorm_row16<false><<<ceil_div((size_t)M, kRows16), 256, 0, s>>>(X, w, Y, M, H, eps);
+        if (nt) rmsnorm_row16<true><<<ceil_div((size_t)M, kRows16 * kRowsPerLane), 256, 0, s>>>(X, w, Y, M, H, eps);
+        else rmsnorm_row16<false><<<ceil_div((size_t)M, kRows16 * kRowsPerLane), 256, 0, s>>>(X, w, Y, M, H, eps);
         return launch_status();
     }
     return dispatch_nv(H, [&](auto nv) {
@@ -298,8 +323,8 @@ extern "C" int cdna3_layernorm_f32(const float* X, const float* gamma, const flo
     }
     const bool nt = (size_t)M * (size_t)H * sizeof(float) >= kStreamBytes;
     if (H <= 64) {
-        if (nt) layernorm_row16<true><<<ceil_div((size_t)M, kRows16), 256, 0, s>>>(X, gamma, beta, Y, M, H, eps);
-        else layernorm_row16<false><<<ceil_div((size_t)M, kRows16), 256, 0, s>>>(X, gamma, beta, Y, M, H, eps);
+        if (nt) layernorm_row16<true><<<ceil_div((size_t)M, kRows16 * kRowsPerLane), 256, 0, s>>>(X, gamma, beta, Y, M, H, eps);
+        else layernorm_row16<false><<<ceil_div((size_t)M, kRows16 * kRowsPerLane), 256, 0, s>>>(X, gamma, beta, Y, M, H, eps);
         return launch_status();
     }
     return dispatch_nv(H, [&](auto nv) {

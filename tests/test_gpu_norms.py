@@ -10,7 +10,7 @@ from gpu_util import DEV
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("M,H", [(1, 768), (512, 768), (65536 // 64, 64), (37, 64), (5, 32), (1, 4), (300, 512), (7, 4096), (5, 1000), (3, 5000), (2, 3)])
+@pytest.mark.parametrize("M,H", [(1, 768), (512, 768), (65536 // 64, 64), (37, 64), (17, 64), (16, 60), (5, 32), (1, 4), (300, 512), (7, 4096), (5, 1000), (3, 5000), (2, 3)])
 def test_rmsnorm(M, H):
     X = oracle.normal(M * 7 + H, M * H, 0.0, 2.0).reshape(M, H)
     wv, wb = oracle.round16(oracle.normal(H, H, 1.0, 0.1), oracle.F16)
@@ -20,7 +20,7 @@ def test_rmsnorm(M, H):
     np.testing.assert_allclose(got, oracle.rmsnorm(X, wb, 1e-6), rtol=1e-5, atol=1e-5)
 
 
-@pytest.mark.parametrize("M,H", [(65536 // 32, 64), (37, 64), (21, 48), (3, 8), (2048, 512), (512, 768), (4, 4096), (3, 6000), (5, 100), (9, 1)])
+@pytest.mark.parametrize("M,H", [(65536 // 32, 64), (37, 64), (33, 64), (17, 16), (21, 48), (3, 8), (2048, 512), (512, 768), (4, 4096), (3, 6000), (5, 100), (9, 1)])
 def test_layernorm(M, H):
     # The reference's input generator for its LayerNorm benchmark (bench_layernorm.hip:131).
     i = np.arange(M * H, dtype=np.uint64)
