@@ -148,6 +148,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "cdna3_scan_inclusive": (c_int, [c_int, c_int, vp, c_size, vp, vp, c_size, vp]),
         "cdna3_rmsnorm_f32": (c_int, [vp, vp, vp, c_int, c_int, c_float, vp]),
         "cdna3_layernorm_f32": (c_int, [vp, vp, vp, vp, c_int, c_int, c_float, vp]),
+        "cdna4_gemm_f16_nt": (c_int, [vp, vp, vp, c_int, c_int, c_int, c_int, c_int, c_int, vp]),
         "cdna3_rope_f16": (c_int, [vp, vp, vp, c_int, c_int, c_int, vp]),
         "cdna3_rope_table_f32": (c_int, [vp, vp, c_int, c_int, c_int, c_float, vp]),
         "cdna3_scatter_kv_f16": (c_int, [vp, vp] + [c_int] * 5 + [vp]),
@@ -414,6 +415,24 @@ def layernorm_f32(X: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps:
     out = torch.empty_like(X) if out is None else out
     _check(lib().cdna3_layernorm_f32(_ptr(X), _ptr(gamma), _ptr(beta), _ptr(out), M, H, eps, _stream(stream)),
            "cdna3_layernorm_f32")
+    return out
+
+
+def gemm_f16_nt(X: torch.Tensor, W: torch.Tensor, out: Optional[torch.Tensor] = None, accum: bool = False,
+                out_dtype=torch.float32, stream=None) -> torch.Tensor:
+    """Y = X W^T (+ Y when accum): X fp16 [M][K], W fp16 [N][K], Y fp32 or fp16 [M][N] (the
+    runtime's prompt GEMM; raises for the shapes it does not take)."""
+    _dev(X, W)
+    M, K = X.shape
+    N = W.shape[0]
+    if W.shape[1] != K or X.dtype != torch.float16 or W.dtype != torch.float16:
+        raise ValueError("gemm_f16_nt: X [M][K] and W [N][K] fp16")
+    if out is None:
+        out = (torch.zeros if accum else torch.empty)(M, N, device=X.device, dtype=out_dtype)
+    if out.dtype not in (torch.float32, torch.float16) or out.shape[0] != M or out.shape[1] != N or out.stride(1) != 1:
+        raise ValueError("gemm_f16_nt: out fp32 or fp16 [M][N], rows contiguous")
+    _check(lib().cdna4_gemm_f16_nt(_ptr(X.contiguous()), _ptr(W.contiguous()), _ptr(out), int(out.dtype == torch.float32),
+                                   int(accum), M, N, K, out.stride(0), _stream(stream)), "cdna4_gemm_f16_nt")
     return out
 
 

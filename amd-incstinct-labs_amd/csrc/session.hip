@@ -24,6 +24,8 @@
 //     index live in a device step state that the kernels read and the argmax advances, so one
 //     graph serves every step with the same attention plan (re-captured when the plan changes
 //     with the cache length). CDNA4_SESSION_GRAPH=0 launches the same kernels one by one.
+//   * The prompt's Q|K|V GEMM runs on the library's own MFMA GEMM (gemm.hip) when its shape
+//     allows, the other prompt GEMMs on rocBLAS; CDNA4_SESSION_ROCBLAS=1 sends all to rocBLAS.
 #include "common.hpp"
 #include <rocblas/rocblas.h>
 #include <math.h>
@@ -57,6 +59,8 @@ long long attn_decode_plan_key(const cdna3_decode_cfg& c);
 int attn_decode_replayable(const void* q, const void* K, const void* V, void* o, const cdna3_decode_cfg& c, int dtype,
                            void* ws, size_t ws_bytes, const int* len_pos, hipStream_t s);
 int llm_silu_mul(const float* gu, void* act, int T, int F, hipStream_t s);
+int llm_gemm_f16(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, bool accum, int M, int N, int K, int ldy,
+                 hipStream_t s);
 int llm_bias_add_f16(void* Y, const void* b, int T, int N, hipStream_t s);
 int kv_rope_append(const void* q, const void* k, const void* v, long long ldq, long long ldk, long long ldv,
                    void* q_out, void* K_cache, void* V_cache, const float* cos_tab, const float* sin_tab, int T,
@@ -149,6 +153,7 @@ struct Session {
     // positions and the token index live in the device step state dstate = {pos, step}.
     int* dstate = nullptr;
     bool use_graph = true;
+    bool rocblas_only = false;   // CDNA4_SESSION_ROCBLAS=1: prompt GEMMs through rocBLAS only
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
     long long gkey = -1;
@@ -307,9 +312,16 @@ int Session::reserve(int T) {
 // accumulation, fp32 or fp16 Y. rocBLAS is column-major: row-major Y is column-major Y^T [N][M],
 // and Y^T = W X^T, where the row-major W [N][K] read column-major is W^T (so op(A) = transpose,
 // lda = K) and the row-major X [M][K] read column-major is X^T (op(B) = none, ldb = K). The
-// reference derives the same call (rocblas_gemm.hpp:8-20).
+// reference derives the same call (rocblas_gemm.hpp:8-20). The library's MFMA GEMM takes the
+// fp16-output product (Q|K|V) when its shape allows: at the cfg5 prompt (T 512) it ran 13.5 us
+// against rocBLAS's 16.8; on the fp32-output products (O, gate|up, down) rocBLAS was faster
+// (gate|up 14.9 against 17.7-23.5 us, down 11.6 against 20.7), so those stay on rocBLAS.
 int Session::gemm(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, float beta, int M, int N, int K,
                   int ldy) {
+    if (!rocblas_only && !y_f32 && beta == 0.f) {
+        const int e = llm_gemm_f16(X, W, Y, false, false, M, N, K, ldy, stream);
+        if (e != -1) return e;   // -1: a shape the kernel does not take
+    }
     const float alpha = 1.f;
     const rocblas_datatype yt = y_f32 ? rocblas_datatype_f32_r : rocblas_datatype_f16_r;
     const rocblas_status st = rocblas_gemm_ex(blas, rocblas_operation_transpose, rocblas_operation_none, N, M, K,
@@ -451,6 +463,8 @@ extern "C" int cdna3_session_create(const char* model_dir, int max_seq, cdna3_se
         s->impl.max_seq = max_seq;
         const char* g = getenv("CDNA4_SESSION_GRAPH");   // "0": separate launches per decode step
         s->impl.use_graph = !(g && g[0] == '0' && g[1] == 0);
+        const char* rb = getenv("CDNA4_SESSION_ROCBLAS");
+        s->impl.rocblas_only = rb && rb[0] == '1' && rb[1] == 0;
         e = s->impl.read_config(model_dir);
         if (e == 0) e = check_device();
         if (e == 0) e = (int)hipStreamCreateWithFlags(&s->impl.stream, hipStreamNonBlocking);

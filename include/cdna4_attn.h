@@ -231,6 +231,18 @@ int cdna3_rope_table_f32(float* cos_tab, float* sin_tab, int pos0, int T, int D,
                          float theta, cdna4_stream_t stream);
 
 /*
+ * The runtime's prompt GEMM: Y[M][N] = X[M][K] W[N][K]^T (+ Y when accum = 1), X and W fp16
+ * row-major, fp32 accumulation, Y fp32 (y_f32 = 1) or fp16 with leading dimension ldy. It
+ * replaces, for the shapes it takes, the rocBLAS gemm_ex call of the reference's runtime
+ * (cdna3-prims/include/cdna3/runtime/rocblas_gemm.hpp:8-20, forward.hpp:70-131; beta 0 or 1).
+ * Returns CDNA4_ERR_INVALID_VALUE, launching nothing, when K is not a multiple of 64, N or ldy
+ * not a multiple of 4, ldy < N, X or W not 16-byte aligned or Y not 16- (fp32) or 8-byte (fp16)
+ * aligned (the session then calls rocBLAS).
+ */
+int cdna4_gemm_f16_nt(const void* X, const void* W, void* Y, int y_f32, int accum, int M, int N,
+                      int K, int ldy, cdna4_stream_t stream);
+
+/*
  * KV cache and layout kernels of the runtime layer loop (all fp16, device pointers).
  * cdna3_scatter_kv_f16 replaces scatter_kv_kernel (cdna3-prims/include/cdna3/runtime/
  * forward.hpp:209-220, launched by Session::append_kv, session.hpp:240-250):
