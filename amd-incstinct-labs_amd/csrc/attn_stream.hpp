@@ -127,6 +127,12 @@ __device__ __forceinline__ void stream_keys(const uint16_t* Kh, const uint16_t* 
         u32x4 pb[1];
         tile::softmax_chunk<1, kBf16>(s, m, pb, sc);
         tile::pv_chunk<D, 1, kBf16>(Vt, off, pb, o, lacc, 0);
+        if constexpr (kBf16) {
+            if (kb < tile::kLoKeys) {   // the first keys: the weights' second bf16 term
+                tile::softmax_lo_chunk<1>(s, m, pb, sc);
+                tile::pv_chunk<D, 1, true>(Vt, off, pb, o, lacc, 0);
+            }
+        }
         st = (st == NS - 1) ? 0 : st + 1;
     }
 }

@@ -197,6 +197,34 @@ __device__ __forceinline__ void softmax_chunk(const f32x4 (&s)[QT][2], const flo
     }
 }
 
+// Keys below kLoKeys enter the bf16 P.V product with a second weight term. A weight rounded to
+// bf16 carries 8 significant bits, and the output moves by up to 2^-9 sum_i w_i |v_i - O| (w_i
+// the normalised weights): a query that sees only a few keys (the first rows of a causal
+// sequence, a short cache) can be off by ~3e-3 for N(0,1) values. Sent as hi = bf16(p) plus
+// lo = bf16(p - hi) (p - hi is exact in fp32), a weight carries ~16 bits, and the two-term chunk
+// costs one more set of P.V and row-sum MFMAs. A query that sees more than kLoKeys keys spreads
+// its weight so that the rounding of the later keys averages out (its error falls as one over the
+// square root of the number of keys weighted alike), so only the first keys of a stream need it.
+constexpr int kLoKeys = 64;
+
+// The second term: lo = bf16(p - bf16(p)) for the weights softmax_chunk forms from the same s and
+// m (bit-identical p), packed like its B operands. fp16 weights (11 bits) need no second term.
+template <int QT>
+__device__ __forceinline__ void softmax_lo_chunk(const f32x4 (&s)[QT][2], const float (&m)[QT], u32x4 (&pl)[QT],
+                                                 float sc) {
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[t][x >> 1][(x & 1) * 2], sc, -m[t]));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[t][x >> 1][(x & 1) * 2 + 1], sc, -m[t]));
+            const uint32_t hi = pack2<true>(p0, p1);
+            const float h0 = __builtin_bit_cast(float, hi << 16), h1 = __builtin_bit_cast(float, hi & 0xFFFF0000u);
+            pl[t][x] = pack2<true>(p0 - h0, p1 - h1);
+        }
+    }
+}
+
 // O^T += V^T P^T for chunk kc of tile Vt, and l += row sums of P (ones-operand MFMA).
 template <int D, int QT, bool kBf16>
 __device__ __forceinline__ void pv_chunk(const char* Vt, const LdsOffsets& off, const u32x4 (&pb)[QT],

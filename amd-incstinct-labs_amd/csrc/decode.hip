@@ -154,6 +154,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void de
         u32x4 pb[1];
         tile::softmax_chunk<1, kBf16>(s, m, pb, a.sc);
         tile::pv_chunk<D, 1, kBf16>(Vt, off, pb, o, lacc, 0);
+        if constexpr (kBf16) {
+            if (kb < tile::kLoKeys) {   // the first keys of the cache: the weights' second bf16 term
+                tile::softmax_lo_chunk<1>(s, m, pb, a.sc);
+                tile::pv_chunk<D, 1, true>(Vt, off, pb, o, lacc, 0);
+            }
+        }
         st = (st == NS - 1) ? 0 : st + 1;
     }
 

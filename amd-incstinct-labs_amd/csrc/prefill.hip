@@ -92,7 +92,7 @@ __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ head, lon
 }
 
 // One 32-key half (kc) of a K/V tile: S^T MFMAs, masking, lazy rescale, P, P.V MFMAs.
-template <int D, int QT, bool kBf16, bool kMask>
+template <int D, int QT, bool kBf16, bool kMask, bool kTwo = false>
 __device__ __forceinline__ void chunk_body(const char* Kt, const char* Vt, const LdsOffsets& off,
                                            const u32x4 (&qb)[QT][D / 32],
                                            f32x4 (&o)[QT][D / 16], float (&m)[QT], f32x4 (&lacc)[QT], int kc,
@@ -180,16 +180,22 @@ __device__ __forceinline__ void chunk_body(const char* Kt, const char* Vt, const
 #pragma unroll
         for (int t = 0; t < QT; ++t) o[t][dt] = mfma<kBf16>(va, pb[t], o[t][dt]);
     }
+    // ---- kTwo (bf16, the tile of keys 0..63): the weights' second bf16 term, so that rows with
+    // few keys keep fp32-level weights (see kLoKeys).
+    if constexpr (kTwo) {
+        softmax_lo_chunk<QT>(s, m, pb, sc);
+        pv_chunk<D, QT, true>(Vt, off, pb, o, lacc, kc);
+    }
 }
 
-template <int D, int QT, bool kBf16, bool kMask>
+template <int D, int QT, bool kBf16, bool kMask, bool kTwo = false>
 __device__ __forceinline__ void tile_body(const char* Kt, const char* Vt, const LdsOffsets& off,
                                           const u32x4 (&qb)[QT][D / 32],
                                           f32x4 (&o)[QT][D / 16], float (&m)[QT], f32x4 (&lacc)[QT],
                                           int k0, int qw0, int seqK, int causal, float sc, int li, int g) {
 #pragma unroll
     for (int kc = 0; kc < 2; ++kc)
-        chunk_body<D, QT, kBf16, kMask>(Kt, Vt, off, qb, o, m, lacc, kc, k0, qw0, seqK, causal, sc, li, g);
+        chunk_body<D, QT, kBf16, kMask, kTwo>(Kt, Vt, off, qb, o, m, lacc, kc, k0, qw0, seqK, causal, sc, li, g);
 }
 
 // One K/V tile: issue the asynchronous copy of the next tile into (kn, vn), then compute the
@@ -208,7 +214,9 @@ __device__ __forceinline__ void tile_step(const uint16_t* __restrict__ kt, const
     }
     if (!(a.causal && k0 > wave_qmax)) {
         const bool need_mask = (a.causal && k0 + kBc - 1 > qw0) || (k0 + kBc > a.seqK);
-        if (need_mask)
+        if (kBf16 && k0 < kLoKeys)   // keys 0..63 (kBc = 64): weights with a second bf16 term
+            tile_body<D, QT, kBf16, true, kBf16>((const char*)kt, (const char*)vt, off, qb, o, m, lacc, k0, qw0, a.seqK, a.causal, a.sc, li, g);
+        else if (need_mask)
             tile_body<D, QT, kBf16, true>((const char*)kt, (const char*)vt, off, qb, o, m, lacc, k0, qw0, a.seqK, a.causal, a.sc, li, g);
         else
             tile_body<D, QT, kBf16, false>((const char*)kt, (const char*)vt, off, qb, o, m, lacc, k0, qw0, a.seqK, a.causal, a.sc, li, g);
@@ -216,7 +224,7 @@ __device__ __forceinline__ void tile_step(const uint16_t* __restrict__ kt, const
 }
 
 template <int D, int W, int QT, bool kBf16>
-__global__ __launch_bounds__(64 * W) void fa_mfma(PrefillArgs a) {
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void fa_mfma(PrefillArgs a) {
     constexpr int ND = D / 32;    // 32-wide d chunks (K dimension of S^T)
     constexpr int NDT = D / 16;   // 16-wide d tiles (M dimension of O^T)
     constexpr int BM = W * QT * 16;
@@ -414,8 +422,9 @@ struct TileCopy {
 
 // Region j (see above). Kn (K tile of chunk j + 1, half kcn) always points into the LDS ring;
 // when chunk j + 1 does not exist for this wave (has_next false, tail only) the scores formed
-// from it are ignored. Vc / kcc: V tile and half of chunk j. kTail: mask chunk j + 1.
-template <int D, int QT, bool kBf16, bool kTail, bool kCopy, int NI>
+// from it are ignored. Vc / kcc: V tile and half of chunk j. kTail: mask chunk j + 1. kTwo (bf16,
+// tail tile 0 only): chunk j also enters with its weights' second bf16 term (see kLoKeys).
+template <int D, int QT, bool kBf16, bool kTail, bool kCopy, int NI, bool kTwo = false>
 __device__ __forceinline__ void pipe_region(const char* Kn, int kcn, const char* Vc, int kcc, const LdsOffsets& off,
                                            const u32x4 (&qb)[QT][D / 32], f32x4 (&s)[QT][2], f32x4 (&o)[QT][D / 16],
                                            float (&m)[QT], float (&thr)[QT], f32x4 (&lacc)[QT], const u32x4& ones,
@@ -427,6 +436,15 @@ __device__ __forceinline__ void pipe_region(const char* Kn, int kcn, const char*
     constexpr int SL = NP / NK;        // P values per interleave slot
     constexpr int kAhead = 2;          // LDS operand reads issued ahead of their MFMAs
     static_assert(NP % NK == 0 && SL % 2 == 0, "softmax slices must pair up for the packing");
+    if constexpr (kTwo) {
+        // Chunk j's keys lie below kLoKeys: first the P.V product of its weights' second bf16 term
+        // (s holds chunk j's masked scores, m is the reference P_j is formed against; the sum into
+        // O and l does not depend on the order), before chunk j + 1's scores are live.
+        u32x4 pl[QT];
+        softmax_lo_chunk<QT>(s, m, pl, sc);
+        pv_chunk<D, QT, true>(Vc, off, pl, o, lacc, kcc);
+        __builtin_amdgcn_sched_barrier(0);   // the region's reads stay after this block
+    }
     float p[QT][8];
     u32x4 pb[QT];
     f32x4 sn[QT][2];
@@ -692,8 +710,9 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
         }
 
         // tile t sits in buffer bc = t % NB (a literal in the unrolled main loop)
-        auto tile_iter = [&](int t, auto tail, int bc) {
+        auto tile_iter = [&](int t, auto tail, auto two, int bc) {
             constexpr bool kTail = decltype(tail)::value;
+            constexpr bool kTwo = decltype(two)::value;
             const int bn = bc == NB - 1 ? 0 : bc + 1;   // buffer of tile t + 1
             const char* Kt = (const char*)(lds + bc * 2 * kTile);
             const char* Vt = (const char*)(lds + bc * 2 * kTile + kTile);
@@ -707,7 +726,7 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
                 pipe_region<D, QT, kBf16, false, false, NI>(Kt, 1, Vt, 0, off, qb, s, o, m, thr, lacc, ones, true,
                                                             (j0 + 1) * 32, qw0, a.seqK, a.causal, a.sc, inv_sc, li, g, cp);
             else if (j0 < nch)
-                pipe_region<D, QT, kBf16, true, false, NI>(Kt, 1, Vt, 0, off, qb, s, o, m, thr, lacc, ones, j0 + 1 < nch,
+                pipe_region<D, QT, kBf16, true, false, NI, kTwo>(Kt, 1, Vt, 0, off, qb, s, o, m, thr, lacc, ones, j0 + 1 < nch,
                                                            (j0 + 1) * 32, qw0, a.seqK, a.causal, a.sc, inv_sc, li, g, cp);
             if (!kTail || t + 1 < ntiles) {
                 // tile t + 1 landed and is visible; every wave is past region 2t - 1, the last reader
@@ -724,16 +743,24 @@ __global__ __launch_bounds__(64 * W) void fa_pipe(PrefillArgs a) {
                 pipe_region<D, QT, kBf16, false, true, NI>(Kn, 0, Vt, 1, off, qb, s, o, m, thr, lacc, ones, true,
                                                            (j1 + 1) * 32, qw0, a.seqK, a.causal, a.sc, inv_sc, li, g, cp);
             else if (j1 < nch)
-                pipe_region<D, QT, kBf16, true, false, NI>(Kn, 0, Vt, 1, off, qb, s, o, m, thr, lacc, ones, j1 + 1 < nch,
+                pipe_region<D, QT, kBf16, true, false, NI, kTwo>(Kn, 0, Vt, 1, off, qb, s, o, m, thr, lacc, ones, j1 + 1 < nch,
                                                            (j1 + 1) * 32, qw0, a.seqK, a.causal, a.sc, inv_sc, li, g, cp);
         };
         int t = 0;
         for (; t + NB <= t_main; t += NB) {
 #pragma unroll
-            for (int i = 0; i < NB; ++i) tile_iter(t + i, std::false_type{}, i);
+            for (int i = 0; i < NB; ++i) tile_iter(t + i, std::false_type{}, std::false_type{}, i);
         }
-        for (; t < t_main; ++t) tile_iter(t, std::false_type{}, t % NB);
-        for (; t < ntiles; ++t) tile_iter(t, std::true_type{}, t % NB);
+        for (; t < t_main; ++t) tile_iter(t, std::false_type{}, std::false_type{}, t % NB);
+        // bf16: keys 0..63 (tile 0, reached in the tail only when the main loop is empty) enter
+        // with their weights' second bf16 term, in a copy of the tail step of its own
+        if constexpr (kBf16) {
+            if (t == 0 && ntiles > 0) {
+                tile_iter(0, std::true_type{}, std::true_type{}, 0);
+                t = 1;
+            }
+        }
+        for (; t < ntiles; ++t) tile_iter(t, std::true_type{}, std::false_type{}, t % NB);
         if (item + (int)gridDim.x < nitems) load_q(item_of(item + (int)gridDim.x));
 
         // ---- O = O^T / l: lane holds d = 16dt + 4g + e of query li, and its query's full l.

@@ -4,13 +4,23 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-for p in (ROOT, os.path.join(ROOT, "amd-incstinct-labs_amd")):
+for p in (ROOT, os.path.join(ROOT, "amd-incstinct-labs_amd"), os.path.dirname(os.path.abspath(__file__))):
     if p not in sys.path:
         sys.path.insert(0, p)
+
+import parity_log  # noqa: E402
 
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    lines = parity_log.summary_lines()
+    if lines:
+        terminalreporter.section("parity margins")
+        for line in lines:
+            terminalreporter.write_line(line)
 
 
 def gpu_available() -> bool:

@@ -12,6 +12,7 @@ import pytest
 
 import cdna4
 import oracle
+import parity_log
 from cdna4 import model_format as mf
 
 pytestmark = pytest.mark.gpu
@@ -52,7 +53,7 @@ def _prompt(meta, n, seed):
     return np.random.default_rng(seed).integers(0, int(meta["vocab_size"]), n).astype(np.int32)
 
 
-def _check_generation(meta, t, ids, out, max_seq):
+def _check_generation(meta, t, ids, out, max_seq, what=""):
     toks, logits = out["tokens"], out["logits"]
     ref = oracle.LLM(meta, t, max_seq).forward(np.concatenate([ids, toks[:-1]]).astype(np.int32),
                                                all_logits=True)[len(ids) - 1:]
@@ -60,6 +61,7 @@ def _check_generation(meta, t, ids, out, max_seq):
     err = _row_err(logits, ref)
     print(f"  steps {len(toks)}: max |logit - oracle| / scale = {err:.2e}, "
           f"abs {float(np.abs(logits - ref).max()):.2e}", flush=True)
+    parity_log.record(err, LOGIT_TOL, "logit", None, what)
     assert err < LOGIT_TOL, err
     for i, tok in enumerate(toks):
         best = oracle.reference_argmax(ref[i])
@@ -89,6 +91,7 @@ def test_prefill_logits_match_oracle(model, n):
     ref = oracle.LLM(meta, t, 128).forward(ids)
     err = _row_err(got, ref)
     print(f"  prompt {n}: max |logit - oracle| / scale = {err:.2e}", flush=True)
+    parity_log.record(err, LOGIT_TOL, "logit")
     assert err < LOGIT_TOL, err
 
 
@@ -183,6 +186,25 @@ def test_cfg5_shape_matches_oracle(tmp_path):
     with cdna4.Session(d, max_seq=128) as s:
         out = s.generate_ex(ids, cdna4.GenerateCfg(6), with_logits=True)
     _check_generation(meta, t, ids, out, 128)
+
+
+def test_cfg5_full_workload_matches_oracle(tmp_path):
+    # BASELINE config 5 exactly as bench.py runs it (Session::generate, session.hpp:263-296): the
+    # bench's model (seed 5), its 512-token prompt (default_rng(5)) and 128 greedy tokens. Every
+    # step's logits against the oracle under teacher forcing (the oracle runs the prompt and the
+    # 127 tokens the GPU fed back, ~20 s on one host thread), every token against the oracle's
+    # argmax with the reference's tie-break.
+    L, H, nH, F, V, prompt, new = 12, 768, 12, 3072, 32000, 512, 128
+    d = str(tmp_path / "cfg5_full")
+    mf.random_model(d, n_layers=L, hidden=H, n_heads=nH, ffn_dim=F, vocab_size=V, norm="layernorm", seed=5)
+    meta, t = mf.read_model(d)
+    ids = np.random.default_rng(5).integers(0, V, prompt).astype(np.int32)
+    with cdna4.Session(d, max_seq=prompt + new) as s:
+        out = s.generate_ex(ids, cdna4.GenerateCfg(new), with_logits=True)
+    assert len(out["tokens"]) == new
+    print(f"cfg5 full workload: {prompt} + {new} tokens generated", flush=True)
+    _check_generation(meta, t, ids, out, prompt + new,
+                      what=f"cfg5 ({prompt}-token prompt + {new} greedy tokens, 12 layers d768) logits")
 
 
 def test_cpp_session_program(model):
