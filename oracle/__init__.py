@@ -296,21 +296,22 @@ class _OrcLLM(ctypes.Structure):
                                   "n2b")]
 
 
-def reference_argmax(logits) -> int:
-    """argmax_kernel (cdna3-prims/include/cdna3/runtime/forward.hpp:244-262), one block of 256
-    threads, restated step by step: thread t keeps the first strictly larger value of logits[t],
-    logits[t + 256], ... starting from -1e30 (index 0), then a tree over the threads in which the
-    right partner replaces the left only when strictly larger (strides 128, 64, ..., 1)."""
+def reference_argmax(logits, threads: int = 256) -> int:
+    """argmax_kernel (cdna3-prims/include/cdna3/runtime/forward.hpp:244-262), one block of
+    `threads` threads (the reference launches 256; a power of two), restated step by step:
+    thread t keeps the first strictly larger value of logits[t], logits[t + threads], ...
+    starting from -1e30 (index 0), then a tree over the threads in which the right partner
+    replaces the left only when strictly larger (strides threads/2, ..., 1)."""
     x = np.ascontiguousarray(logits, np.float32).reshape(-1)
-    bv = np.full(256, np.float32(-1e30), np.float32)
-    bi = np.zeros(256, np.int64)
-    for t in range(min(256, x.size)):
-        col = x[t::256]
+    bv = np.full(threads, np.float32(-1e30), np.float32)
+    bi = np.zeros(threads, np.int64)
+    for t in range(min(threads, x.size)):
+        col = x[t::threads]
         run = np.maximum.accumulate(col)
         first = int(np.argmax(col == run[-1]))          # first index of the column maximum
         if run[-1] > bv[t]:
-            bv[t], bi[t] = run[-1], t + 256 * first
-    s = 128
+            bv[t], bi[t] = run[-1], t + threads * first
+    s = threads // 2
     while s > 0:
         for t in range(s):
             if bv[t + s] > bv[t]:

@@ -317,6 +317,42 @@ extern "C" int hook_runtime_kernels(int which, const void* a, void* b, const voi
             hipLaunchKernelGGL(pack_kv_kernel, grid1d((long long)i0 * i1 * i2), dim3(256), 0, s, (const __half*)a,
                                (__half*)b, i0, i1, i2, i3);
             break;
+        case 5: case 6: case 7: case 8: case 9: {
+            // the GEMMs: X = a, W = c, B = d (case 6), Y = b; M = i0, N = i1, K = i2, block i3 x i4
+            // (the reference: 16 x 16), grid covering N x M
+            const dim3 tb((unsigned)i3, (unsigned)i4), gr((unsigned)((i1 + i3 - 1) / i3), (unsigned)((i0 + i4 - 1) / i4));
+            if (which == 5)
+                hipLaunchKernelGGL(gemm_f32in_f16out_kernel, gr, tb, 0, s, (const float*)a, (const __half*)c,
+                                   (__half*)b, i0, i1, i2);
+            else if (which == 6)
+                hipLaunchKernelGGL(gemm_f32in_f16out_bias_kernel, gr, tb, 0, s, (const float*)a, (const __half*)c,
+                                   (const __half*)d, (__half*)b, i0, i1, i2);
+            else if (which == 7)
+                hipLaunchKernelGGL(gemm_f32in_f32out_kernel, gr, tb, 0, s, (const float*)a, (const __half*)c,
+                                   (float*)b, i0, i1, i2);
+            else if (which == 8)
+                hipLaunchKernelGGL(gemm_f16in_f32out_kernel, gr, tb, 0, s, (const __half*)a, (const __half*)c,
+                                   (float*)b, i0, i1, i2);
+            else
+                hipLaunchKernelGGL(gemm_xwT_kernel, gr, tb, 0, s, (const __half*)a, (const __half*)c, (__half*)b, i0,
+                                   i1, i2);
+            break;
+        }
+        case 10:  // silu_mul_f32_kernel(gate = b, up = a, n = i0), i1 threads per block, grid covering n
+            hipLaunchKernelGGL(silu_mul_f32_kernel, dim3((unsigned)((i0 + i1 - 1) / i1)), dim3((unsigned)i1), 0, s,
+                               (float*)b, (const float*)a, (size_t)i0);
+            break;
+        case 11:  // add_f32_kernel(x = b, y = a, n = i0)
+            hipLaunchKernelGGL(add_f32_kernel, dim3((unsigned)((i0 + i1 - 1) / i1)), dim3((unsigned)i1), 0, s,
+                               (float*)b, (const float*)a, (size_t)i0);
+            break;
+        case 12:  // embed_gather_f32_kernel(embed = a, ids = c, out = b, T = i0, H = i1), grid T x 256
+            hipLaunchKernelGGL(embed_gather_f32_kernel, dim3((unsigned)i0), dim3(256), 0, s, (const __half*)a,
+                               (const int*)c, (float*)b, i0, i1);
+            break;
+        case 13:  // argmax_kernel(logits = a, V = i0, out = b), one block of i1 threads (the reference: 256)
+            hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3((unsigned)i1), 0, s, (const __half*)a, i0, (int*)b);
+            break;
         default: return 1;
     }
     return (int)hipGetLastError();
