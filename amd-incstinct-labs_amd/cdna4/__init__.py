@@ -22,6 +22,7 @@ fallback: if the library is missing, every call raises.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import re
@@ -208,6 +209,19 @@ def _stream(stream) -> ctypes.c_void_p:
     return ctypes.c_void_p(int(stream))
 
 
+def _on_stream(stream):
+    """Context under which torch allocations belong to the stream the call launches on. A
+    temporary (split-K workspace, contiguous copy, scan workspace) freed when the call returns
+    then goes back to that stream's pool, so the caching allocator can hand it out again only to
+    work ordered after the kernels that still use it; allocated on another stream, it could be
+    reused and overwritten while they run."""
+    if stream is None:
+        return contextlib.nullcontext()
+    if not isinstance(stream, torch.cuda.Stream):
+        stream = torch.cuda.ExternalStream(int(stream))
+    return torch.cuda.stream(stream)
+
+
 def _ptr(t: Optional[torch.Tensor]) -> ctypes.c_void_p:
     return ctypes.c_void_p(0 if t is None else t.data_ptr())
 
@@ -265,7 +279,7 @@ def decode(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, o: torch.Tensor, c
            workspace="auto", stream=None) -> None:
     """cdna3::attn::decode with batch: q, o [batch][nQH][D]; K, V [batch][nKVH][stride][D];
     fp16 or bf16. `workspace`: "auto" (default) allocates the split-K workspace from torch's
-    caching allocator on the current stream; a uint8 tensor of >= decode_workspace_size(cfg)
+    caching allocator on the stream the call launches on; a uint8 tensor of >= decode_workspace_size(cfg)
     bytes is used as given; None runs the one-launch plan that needs no workspace (the
     reference launchers' contract)."""
     _dev(q, K, V, o)
@@ -277,17 +291,18 @@ def decode(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, o: torch.Tensor, c
         raise ValueError("q/o smaller than the configuration")
     if min(K.numel(), V.numel()) < cfg.batch * cfg.nKVHeads * stride * cfg.D:
         raise ValueError("K/V smaller than the configuration")
-    if isinstance(workspace, str):
-        if workspace != "auto":
-            raise ValueError("workspace must be 'auto', None or a uint8 tensor")
-        need = decode_workspace_size(cfg)
-        workspace = torch.empty(need, dtype=torch.uint8, device=q.device) if need > 0 else None
-    ws_bytes = 0
-    if workspace is not None:
-        _dev(workspace)
-        ws_bytes = workspace.numel() * workspace.element_size()
-    _check(lib().cdna3_attn_decode(_ptr(q), _ptr(K), _ptr(V), _ptr(o), ctypes.byref(cfg), dt, _ptr(workspace),
-                                   ws_bytes, _stream(stream)), "cdna3_attn_decode")
+    if isinstance(workspace, str) and workspace != "auto":
+        raise ValueError("workspace must be 'auto', None or a uint8 tensor")
+    with _on_stream(stream):
+        if isinstance(workspace, str):
+            need = decode_workspace_size(cfg)
+            workspace = torch.empty(need, dtype=torch.uint8, device=q.device) if need > 0 else None
+        ws_bytes = 0
+        if workspace is not None:
+            _dev(workspace)
+            ws_bytes = workspace.numel() * workspace.element_size()
+        _check(lib().cdna3_attn_decode(_ptr(q), _ptr(K), _ptr(V), _ptr(o), ctypes.byref(cfg), dt, _ptr(workspace),
+                                       ws_bytes, _stream(stream)), "cdna3_attn_decode")
 
 
 def decode_noalloc(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, o: torch.Tensor, cfg: DecodeCfg,
@@ -355,12 +370,13 @@ def reduce(x: torch.Tensor, op="sum", out: Optional[torch.Tensor] = None,
     _dev(x)
     dt, o = _dtype(x), _OPS[op]
     n = x.numel()
-    if out is None:
-        out = torch.empty(1, dtype=_acc_dtype(x), device=x.device)
-    if workspace is None:
-        workspace = torch.empty(reduce_workspace_size(n, dt), dtype=torch.uint8, device=x.device)
-    _check(lib().cdna3_reduce(o, dt, _ptr(x), n, _ptr(out), _ptr(workspace), workspace.numel(), _stream(stream)),
-           "cdna3_reduce")
+    with _on_stream(stream):
+        if out is None:
+            out = torch.empty(1, dtype=_acc_dtype(x), device=x.device)
+        if workspace is None:
+            workspace = torch.empty(reduce_workspace_size(n, dt), dtype=torch.uint8, device=x.device)
+        _check(lib().cdna3_reduce(o, dt, _ptr(x), n, _ptr(out), _ptr(workspace), workspace.numel(),
+                                  _stream(stream)), "cdna3_reduce")
     return out
 
 
@@ -373,16 +389,17 @@ def scan_inclusive(x: torch.Tensor, op="sum", out: Optional[torch.Tensor] = None
     _dev(x)
     dt, o = _dtype(x), _OPS[op]
     n = x.numel()
-    if out is None:
-        out = torch.empty(n, dtype=_acc_dtype(x), device=x.device)
-    if workspace is None:
-        workspace = torch.empty(max(1, scan_workspace_size(n, dt)), dtype=torch.uint8, device=x.device)
-    _check(lib().cdna3_scan_inclusive(o, dt, _ptr(x), n, _ptr(out), _ptr(workspace), workspace.numel(),
-                                      _stream(stream)), "cdna3_scan_inclusive")
-    if check and n > 0:
-        st = scan_status(workspace, stream)
-        if st != 0:
-            raise CDNA4Error("cdna3_scan_inclusive: look-back wait exceeded its bound; result invalid", 1)
+    with _on_stream(stream):
+        if out is None:
+            out = torch.empty(n, dtype=_acc_dtype(x), device=x.device)
+        if workspace is None:
+            workspace = torch.empty(max(1, scan_workspace_size(n, dt)), dtype=torch.uint8, device=x.device)
+        _check(lib().cdna3_scan_inclusive(o, dt, _ptr(x), n, _ptr(out), _ptr(workspace), workspace.numel(),
+                                          _stream(stream)), "cdna3_scan_inclusive")
+        if check and n > 0:
+            st = scan_status(workspace, stream)
+            if st != 0:
+                raise CDNA4Error("cdna3_scan_inclusive: look-back wait exceeded its bound; result invalid", 1)
     return out
 
 
@@ -402,7 +419,8 @@ def rmsnorm_f32(X: torch.Tensor, W: torch.Tensor, eps: float = 1e-6, out: Option
     if X.dtype != torch.float32 or W.dtype != torch.float16:
         raise ValueError("X must be fp32 and W fp16")
     M, H = X.shape
-    out = torch.empty_like(X) if out is None else out
+    with _on_stream(stream):
+        out = torch.empty_like(X) if out is None else out
     _check(lib().cdna3_rmsnorm_f32(_ptr(X), _ptr(W), _ptr(out), M, H, eps, _stream(stream)), "cdna3_rmsnorm_f32")
     return out
 
@@ -412,7 +430,8 @@ def layernorm_f32(X: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps:
     """Two-pass layernorm: X, Y fp32 [M][H]; gamma, beta fp32 [H]."""
     _dev(X, gamma, beta)
     M, H = X.shape
-    out = torch.empty_like(X) if out is None else out
+    with _on_stream(stream):
+        out = torch.empty_like(X) if out is None else out
     _check(lib().cdna3_layernorm_f32(_ptr(X), _ptr(gamma), _ptr(beta), _ptr(out), M, H, eps, _stream(stream)),
            "cdna3_layernorm_f32")
     return out
@@ -427,12 +446,15 @@ def gemm_f16_nt(X: torch.Tensor, W: torch.Tensor, out: Optional[torch.Tensor] = 
     N = W.shape[0]
     if W.shape[1] != K or X.dtype != torch.float16 or W.dtype != torch.float16:
         raise ValueError("gemm_f16_nt: X [M][K] and W [N][K] fp16")
-    if out is None:
-        out = (torch.zeros if accum else torch.empty)(M, N, device=X.device, dtype=out_dtype)
-    if out.dtype not in (torch.float32, torch.float16) or out.shape[0] != M or out.shape[1] != N or out.stride(1) != 1:
+    if out is not None and (out.dtype not in (torch.float32, torch.float16) or out.shape[0] != M
+                            or out.shape[1] != N or out.stride(1) != 1):
         raise ValueError("gemm_f16_nt: out fp32 or fp16 [M][N], rows contiguous")
-    _check(lib().cdna4_gemm_f16_nt(_ptr(X.contiguous()), _ptr(W.contiguous()), _ptr(out), int(out.dtype == torch.float32),
-                                   int(accum), M, N, K, out.stride(0), _stream(stream)), "cdna4_gemm_f16_nt")
+    with _on_stream(stream):       # the contiguous copies below live until the kernel has read them
+        if out is None:
+            out = (torch.zeros if accum else torch.empty)(M, N, device=X.device, dtype=out_dtype)
+        Xc, Wc = X.contiguous(), W.contiguous()
+        _check(lib().cdna4_gemm_f16_nt(_ptr(Xc), _ptr(Wc), _ptr(out), int(out.dtype == torch.float32), int(accum), M,
+                                       N, K, out.stride(0), _stream(stream)), "cdna4_gemm_f16_nt")
     return out
 
 
@@ -446,8 +468,9 @@ def rope_f16(T: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, seq: int, he
 def rope_table_f32(pos0: int, T: int, D: int, theta: float = 10000.0, device=None, stream=None):
     """Session::fill_rope on the device: cos, sin fp32 [T][D] for positions pos0 .. pos0+T-1."""
     device = device or torch.device("cuda", torch.cuda.current_device())
-    cos = torch.empty((T, D), dtype=torch.float32, device=device)
-    sin = torch.empty((T, D), dtype=torch.float32, device=device)
+    with _on_stream(stream):
+        cos = torch.empty((T, D), dtype=torch.float32, device=device)
+        sin = torch.empty((T, D), dtype=torch.float32, device=device)
     _check(lib().cdna3_rope_table_f32(_ptr(cos), _ptr(sin), pos0, T, D, theta, _stream(stream)),
            "cdna3_rope_table_f32")
     return cos, sin

@@ -51,9 +51,9 @@ extern "C" const char* cdna3_error_string(int code) {
         case CDNA4_OK: return "success";
         case CDNA4_ERR_INVALID_VALUE: return "invalid value (shape, dtype, op or workspace size)";
         case CDNA4_ERR_SCRATCH_TOO_SMALL:
-            return "out of memory (from cdna3_attn_decode_noalloc: the call needs more split-K scratch than "
-                   "the library's static array holds, cdna3_attn_decode_noalloc_max_bytes; pass a workspace "
-                   "to cdna3_attn_decode instead)";
+            return "cdna3_attn_decode_noalloc: the call needs more split-K scratch than the library's static "
+                   "array holds (cdna3_attn_decode_noalloc_max_bytes); pass a workspace to cdna3_attn_decode "
+                   "instead";
         case CDNA4_ERR_INVALID_DEVICE_FUNCTION: return "current device is not gfx950 (MI355X)";
         default: return hipGetErrorString((hipError_t)code);
     }

@@ -327,24 +327,37 @@ def bench_decode(torch, cdna4, steps, warmup):
     del kv
     torch.cuda.empty_cache()
     # The reference's own decode benchmark shape (batch 1, 32q/8kv, D 128, N 8192: 803.4 us on
-    # MI300X, research/flash-attention-mi300x/results/2026-06-15_fa_decode_mi300x.txt:17); 33.5 MB
-    # of K/V per call, so 32 sets rotate through 1 GiB.
-    cfg1b = cdna4.DecodeCfg(D, N, HQ, HK, 1, 0)
-    q1 = q[:1].contiguous()
-    kv1 = [(torch.randn(1, HK, N, D, device="cuda", dtype=torch.float16, generator=g),
-            torch.randn(1, HK, N, D, device="cuda", dtype=torch.float16, generator=g)) for _ in range(32)]
-    o1 = torch.empty_like(q1)
-    ws1 = torch.empty(cdna4.decode_workspace_size(cfg1b), dtype=torch.uint8, device="cuda")
-    cdna4.decode(q1, kv1[0][0], kv1[0][1], o1, cfg1b, workspace=ws1)
-    fn1 = abi_launcher(torch, cdna4, "cdna3_attn_decode",
-                       [(q1.data_ptr(), k.data_ptr(), v.data_ptr(), o1.data_ptr(), ctypes.byref(cfg1b), cdna4.F16,
-                         ws1.data_ptr(), ws1.numel()) for k, v in kv1])
-    ms1, _ = time_launches(torch, fn1, steps, warmup)
-    nb1 = 2.0 * HK * N * D * 2 + 2.0 * HQ * D * 2
-    batch1 = {"us": ms1 * 1e3, "GBs": nb1 / (ms1 * 1e-3) / 1e9, "reference_us_mi300x": 803.4,
-              "config": {"batch": 1, "q_heads": HQ, "kv_heads": HK, "head_dim": D, "kv_len": N, "dtype": "fp16"}}
-    del kv1
-    torch.cuda.empty_cache()
+    # MI300X, research/flash-attention-mi300x/results/2026-06-15_fa_decode_mi300x.txt:17), and N
+    # 4096; K/V sets rotate through >= 1 GiB. Timed twice: with a split-K workspace
+    # (cdna3_attn_decode's workspace form, the decode overloads taking one), and as the reference's
+    # launchers call it, without a workspace (cdna3::attn::decode / decode_dme, fa_decode::launch):
+    # the one-launch plan, one workgroup per (batch, kv head), i.e. 8 workgroups here.
+    batch1 = {}
+    for n1 in (8192, 4096):
+        cfg1b = cdna4.DecodeCfg(D, n1, HQ, HK, 1, 0)
+        q1 = q[:1].contiguous()
+        nb1 = 2.0 * HK * n1 * D * 2 + 2.0 * HQ * D * 2
+        nsets = max(2, int((1 << 30) // nb1))
+        kv1 = [(torch.randn(1, HK, n1, D, device="cuda", dtype=torch.float16, generator=g),
+                torch.randn(1, HK, n1, D, device="cuda", dtype=torch.float16, generator=g)) for _ in range(nsets)]
+        o1 = torch.empty_like(q1)
+        ws1 = torch.empty(cdna4.decode_workspace_size(cfg1b), dtype=torch.uint8, device="cuda")
+        cdna4.decode(q1, kv1[0][0], kv1[0][1], o1, cfg1b, workspace=ws1)
+        cdna4.decode(q1, kv1[0][0], kv1[0][1], o1, cfg1b, workspace=None)
+        entry = {"config": {"batch": 1, "q_heads": HQ, "kv_heads": HK, "head_dim": D, "kv_len": n1, "dtype": "fp16"}}
+        if n1 == 8192:
+            entry["reference_us_mi300x"] = 803.4
+        for key, ws_ptr, ws_n in (("workspace", ws1.data_ptr(), ws1.numel()), ("no_workspace", None, 0)):
+            fn1 = abi_launcher(torch, cdna4, "cdna3_attn_decode",
+                               [(q1.data_ptr(), k.data_ptr(), v.data_ptr(), o1.data_ptr(), ctypes.byref(cfg1b),
+                                 cdna4.F16, ws_ptr, ws_n) for k, v in kv1])
+            ms1, _ = time_launches(torch, fn1, steps, warmup)
+            plan = cdna4.decode_plan(cfg1b, torch.float16, with_workspace=ws_ptr is not None)
+            entry[key] = {"us": round(ms1 * 1e3, 2), "GBs": round(nb1 / (ms1 * 1e-3) / 1e9, 1),
+                          "plan": plan.name, "grid": int(plan.grid)}
+        batch1[f"N{n1}"] = entry
+        del kv1
+        torch.cuda.empty_cache()
     return {"value": gbs, "unit": "GB/s", "avg_us": avg_ms * 1e3, "vs_torch_sdpa": sdpa, "batch1": batch1,
             "config": {"workload": "flash decode, BASELINE config 4", "batch": B, "q_heads": HQ, "kv_heads": HK,
                        "head_dim": D, "kv_len": N, "dtype": "fp16"},

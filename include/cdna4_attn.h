@@ -10,7 +10,10 @@
  *     when the current device is not gfx950, otherwise the launch error;
  *   - never allocates device memory and keeps no device buffers between calls (the session
  *     API below owns the memory of its session);
- * All entry points are re-entrant from any host thread; ordering comes from the stream.
+ * Entry points are re-entrant from any host thread, ordering coming from the stream, with one
+ * exception: cdna3_attn_decode_noalloc, whose calls on one GPU share a static device array, so
+ * calls of it that overlap on one GPU race (see its declaration). A caller's workspace or
+ * session must likewise not be used by calls that overlap.
  *
  * Tensor layouts are row-major and contiguous unless a stride is given.
  */
@@ -32,8 +35,9 @@ typedef struct ihipStream_t* cdna4_stream_t;
 enum {
     CDNA4_OK = 0,
     CDNA4_ERR_INVALID_VALUE = 1,
-    CDNA4_ERR_SCRATCH_TOO_SMALL = 2,   /* hipErrorOutOfMemory: the call needs more than the
-                                          static scratch of cdna3_attn_decode_noalloc holds */
+    CDNA4_ERR_SCRATCH_TOO_SMALL = 0x4344,  /* outside the hipError_t range: the call needs more
+                                              than the static scratch of
+                                              cdna3_attn_decode_noalloc holds */
     CDNA4_ERR_INVALID_DEVICE_FUNCTION = 98
 };
 
@@ -280,8 +284,9 @@ int cdna3_rope_append_kv_f16(const void* q, const void* k, const void* v, void* 
  * Numerics follow the reference: fp32 residual stream, fp16 activations into each projection
  * with fp32 accumulation, fp16 Q/K/V and KV cache, fp32 SiLU product; logits are accumulated in
  * fp32 and stored as fp16 (returned widened to fp32), and the greedy argmax breaks ties as the
- * reference's argmax_kernel does (forward.hpp:244-262: the smallest index mod 256, then the
- * smallest index).
+ * reference's argmax_kernel does (forward.hpp:244-262, a 256-thread strided scan and tree
+ * reduction): among equal maxima, the index i with the smallest bit-reversed (i mod 256) as an
+ * 8-bit number, then the smallest i / 256.
  * The session owns one HIP stream, a rocBLAS handle, the weights and the KV cache
  * [layers][n_kv_heads][max_seq][head_dim]. Calls on one session must not overlap.
  */

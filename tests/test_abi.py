@@ -83,7 +83,7 @@ def test_invalid_arguments_rejected_without_gpu():
     assert l.cdna3_rope_append_kv_f16(p, p, p, p, p, p, p, p, 4, 8, 2, 64, 14, 16, None) == 1  # past the cache
     assert l.cdna3_attn_decode_noalloc(p, p, p, p, ctypes.byref(dcfg), cdna4.F32, None) == 1       # dtype
     big = cdna4.DecodeCfg(128, 4096, 64, 4, 1001)   # 33 MB of partials (4,004 rows: the split-K plan)
-    assert l.cdna3_attn_decode_noalloc(p, p, p, p, ctypes.byref(big), cdna4.F16, None) == 2
+    assert l.cdna3_attn_decode_noalloc(p, p, p, p, ctypes.byref(big), cdna4.F16, None) == 0x4344
     info = cdna4.PlanInfo()
     assert l.cdna3_attn_prefill_plan(ctypes.byref(bad[0]), cdna4.BF16, ctypes.byref(info)) == 1
     assert l.cdna3_attn_decode_plan(ctypes.byref(dcfg), cdna4.F32, 1, ctypes.byref(info)) == 1

@@ -3,8 +3,8 @@
 It runs the split-K plan of cdna3_attn_decode with a workspace, with the partials in the
 library's static per-GPU scratch array instead, so its output must equal that entry point's bit
 for bit. Two calls in a row, the second on a smaller input (the array keeps the first call's
-partials; the second must not read them), and a call whose partials exceed the array is rejected
-before anything is launched.
+partials; the second must not read them), a call whose partials exceed the array is rejected
+before anything is launched, and a call captured in a HIP graph replays correctly on new inputs.
 """
 import ctypes
 
@@ -74,5 +74,38 @@ def test_noalloc_rejects_calls_beyond_the_scratch():
     assert cdna4.decode_workspace_size(cfg) > cdna4.decode_noalloc_max_bytes()
     small = torch.empty(4096, dtype=torch.float16, device=DEV)   # never read: rejected before launch
     rc = _noalloc_abi(small, small, small, small, cfg, torch.float16)
-    assert rc == 2, rc
+    assert rc == 0x4344, rc                     # CDNA4_ERR_SCRATCH_TOO_SMALL, outside the hipError_t range
     assert "static array" in cdna4.error_string(rc)
+    assert "static array" not in cdna4.error_string(2)    # hipErrorOutOfMemory keeps its own message
+
+
+def test_noalloc_captured_in_a_graph_and_replayed_with_new_inputs():
+    # The entry point's purpose: a call captured into a HIP graph (no allocation inside the
+    # capture), replayed after new inputs are written into the same buffers. Each replay, with
+    # eager work and synchronisations between replays, must equal the workspace entry point on
+    # the same inputs bit for bit.
+    cfg = cdna4.DecodeCfg(128, 8192, 32, 8, 8)
+    dtype = torch.float16
+    assert cdna4.decode_plan(cfg, dtype, with_workspace=True).name == "decode_split"
+    q, K, V = _inputs(cfg, dtype, 20)
+    o = torch.empty_like(q)
+    ws = torch.empty(cdna4.decode_workspace_size(cfg), dtype=torch.uint8, device=DEV)
+    assert _noalloc_abi(q, K, V, o, cfg, dtype) == 0   # first call on the device outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = _noalloc_abi(q, K, V, o, cfg, dtype)
+    assert rc == 0
+    for seed in (21, 22, 23):
+        q2, K2, V2 = _inputs(cfg, dtype, seed)
+        q.copy_(q2)
+        K.copy_(K2)
+        V.copy_(V2)
+        o.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        o_ws = torch.empty_like(q)
+        cdna4.decode(q, K, V, o_ws, cfg, workspace=ws)
+        torch.cuda.synchronize()
+        print(f"replay seed {seed}: equal {torch.equal(o, o_ws)}", flush=True)
+        assert torch.equal(o, o_ws)
