@@ -392,8 +392,8 @@ def scan_inclusive(x: torch.Tensor, op="sum", out: Optional[torch.Tensor] = None
     with _on_stream(stream):
         if out is None:
             out = torch.empty(n, dtype=_acc_dtype(x), device=x.device)
-        if workspace is None:
-            workspace = torch.empty(max(1, scan_workspace_size(n, dt)), dtype=torch.uint8, device=x.device)
+        if workspace is None:   # zeroed: no word of it can carry a valid look-back tag
+            workspace = torch.zeros(max(1, scan_workspace_size(n, dt)), dtype=torch.uint8, device=x.device)
         _check(lib().cdna3_scan_inclusive(o, dt, _ptr(x), n, _ptr(out), _ptr(workspace), workspace.numel(),
                                           _stream(stream)), "cdna3_scan_inclusive")
         if check and n > 0:

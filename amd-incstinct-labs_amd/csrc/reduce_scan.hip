@@ -10,10 +10,14 @@
 //           (per-lane serial + wave scan per 64x16-byte chunk); the four waves of a
 //           workgroup meet their tile totals in a line of the workspace, and the group
 //           publishes its aggregate, reads its predecessor groups' aggregates / prefixes 64
-//           at a time (one per lane) and writes the output. A small fill kernel clears the
-//           group flags first. No LDS in either.
+//           at a time (one per lane) and writes the output. Every published word carries the
+//           call's epoch, so words left by earlier calls read as "not ready" and the flags need
+//           no clearing between calls. No LDS in either.
 #include "common.hpp"
+#include <atomic>
 #include <stdlib.h>
+#include <time.h>
+#include <unistd.h>
 #include "scan_layout.hpp"
 #include "wave_primitives/detail/xlane.hpp"
 
@@ -237,17 +241,25 @@ template <> struct ScanElem<CDNA4_BF16> : ScanElem16<CDNA4_BF16> {};
 template <int DT> struct ScanTile { static constexpr int U = 32; };
 template <int DT, bool kVec> constexpr int scan_u() { return kVec ? ScanTile<DT>::U : ScanTile<DT>::U / 2; }
 
-// Per-tile look-back state. A tile publishes its aggregate into agg and, once known, its inclusive
-// prefix into pre. Every 64-bit word carries a tag in its upper half (1 = aggregate, 2 = prefix)
-// and 32 value bits in its lower half; 64-bit values use two words (low, high half), and a reader
-// accepts a slot only when all its words carry the tag, so a torn read is just "not ready". Value
-// and tag travel in one atomic word, so relaxed device-scope atomics suffice: no release/acquire
-// fences, which on this multi-XCD part would write back / invalidate the L2 on every publish and
-// every poll.
+// Per-group look-back state. A group publishes its aggregate into agg and, once known, its
+// inclusive prefix into pre. Every 64-bit word carries a tag in its upper half and 32 value bits
+// in its lower half; 64-bit values use two words (low, high half), and a reader accepts a slot only
+// when all its words carry the tag it looks for, so a torn read is just "not ready". Value and tag
+// travel in one atomic word, so relaxed device-scope atomics suffice: no release/acquire fences,
+// which on this multi-XCD part would write back / invalidate the L2 on every publish and every
+// poll. The tag is (epoch << 2) | kind (kind 1 = aggregate, 2 = prefix), the epoch a number the
+// host draws per call (scan_epoch, never 0): a word left in the workspace by an earlier call
+// carries another epoch and reads as "not ready", so the slots need no clearing between calls (an
+// earlier build cleared them in a separate launch before every call). A zeroed workspace holds no
+// valid tag at all; memory never written by a scan could, by chance, hold the exact 32-bit tag of
+// the call in a word's upper half.
 struct ScanState {
-    uint64_t* agg;    // per tile: NW words
-    uint64_t* pre;    // per tile: NW words
-    uint32_t* error;  // set when a look-back wait exceeds its bound
+    uint64_t* agg;    // per group: NW words
+    uint64_t* pre;    // per group: NW words
+    uint32_t* error;  // set to the epoch when a look-back wait exceeds its bound
+    uint32_t* epoch_word;   // the epoch of the last call on this workspace
+    uint32_t epoch;
+    uint64_t tag_agg, tag_pre;
     uint32_t spin_limit;   // sleeps a look-back waits for a predecessor before it gives up
     unsigned char* xchg;   // per group a 128-byte line: its waves' tile totals, then its prefix
 };
@@ -264,7 +276,13 @@ uint32_t scan_spin_limit() {
     const unsigned long v = strtoul(e, &end, 10);
     return (end && *end == 0 && v <= kSpinLimit) ? (uint32_t)v : kSpinLimit;
 }
-constexpr uint64_t kTagAgg = 1, kTagPre = 2;
+// Per-call epochs: 1 .. 2^30 - 2 in sequence from a start drawn per process (clock and pid), so
+// that consecutive calls on a workspace, also from different processes, carry different tags.
+uint32_t scan_epoch() {
+    static std::atomic<uint32_t> next{(uint32_t)((uint64_t)time(nullptr) * 2654435761u) ^ ((uint32_t)getpid() << 16)};
+    const uint32_t x = next.fetch_add(1, std::memory_order_relaxed);
+    return x % 0x3FFFFFFEu + 1u;   // 1 .. 2^30 - 2: no tag is all ones
+}
 
 template <typename Acc> struct Words { static constexpr int NW = sizeof(Acc) / 4; };
 
@@ -282,12 +300,6 @@ __device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
 }
 __device__ __forceinline__ void st_word(uint64_t* p, uint64_t w) {
     __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__global__ __launch_bounds__(256) void scan_clear(uint64_t* words, size_t nwords, uint32_t* error) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < nwords) words[i] = 0ull;
-    if (i == 0) *error = 0u;
 }
 
 // Lanes 0 .. NW-1 each write one word of tile t's slot.
@@ -334,8 +346,8 @@ __device__ Acc look_back(const ScanState& st, size_t tile, Op op) {
         for (uint32_t spin = 0;; ++spin) {
             if (t >= 0) {
                 Acc pv, av;
-                const bool p = read_slot<Acc>(st.pre, t, kTagPre, pv);
-                const bool q = read_slot<Acc>(st.agg, t, kTagAgg, av);
+                const bool p = read_slot<Acc>(st.pre, t, st.tag_pre, pv);
+                const bool q = read_slot<Acc>(st.agg, t, st.tag_agg, av);
                 s = p ? 2u : (q ? 1u : 0u);
                 v = p ? pv : (q ? av : id);
             }
@@ -344,7 +356,7 @@ __device__ Acc look_back(const ScanState& st, size_t tile, Op op) {
             const uint64_t below = mpre ? ((mpre & (~mpre + 1ull)) - 1ull) : ~0ull;  // lanes before first prefix
             if ((mzero & below) == 0ull) break;
             if (spin >= st.spin_limit) {
-                if (lane == 0) __hip_atomic_store(st.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (lane == 0) __hip_atomic_store(st.error, st.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
@@ -462,11 +474,12 @@ __global__ __launch_bounds__(64 * scan_layout::kScanWaves) void scan_tiles(const
     if (wave == 0) {
         Acc gex = id;
         if (group == 0) {
-            publish(st.pre, group, gtot, kTagPre);
+            publish(st.pre, group, gtot, st.tag_pre);
+            if (lane == 0) *st.epoch_word = st.epoch;   // scan status: the workspace's latest call
         } else {
-            publish(st.agg, group, gtot, kTagAgg);
+            publish(st.agg, group, gtot, st.tag_agg);
             gex = look_back<Acc>(st, group, op);
-            publish(st.pre, group, op(gex, gtot), kTagPre);
+            publish(st.pre, group, op(gex, gtot), st.tag_pre);
         }
         if (lane == 0) *s_excl = gex;
     }
@@ -515,9 +528,10 @@ __global__ __launch_bounds__(64) void scan_tail(const void* __restrict__ in_, si
     Op op;
     Acc acc = Op::template identity<Acc>();
     bool ok = true;
-    if (ngroups > 0) ok = read_slot<Acc>(st.pre, (long long)ngroups - 1, kTagPre, acc);
+    if (ngroups > 0) ok = read_slot<Acc>(st.pre, (long long)ngroups - 1, st.tag_pre, acc);
     if (threadIdx.x == 0) {
-        if (!ok) __hip_atomic_store(st.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (ngroups == 0) *st.epoch_word = st.epoch;   // no scan_tiles launch: this call's epoch here
+        if (!ok) __hip_atomic_store(st.error, st.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         for (size_t i = from; i < n; ++i) {
             acc = op(acc, E::load1(in + i));
             out[i] = (Out)acc;
@@ -562,13 +576,14 @@ int scan_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
     char* w = (char*)ws;
     ScanState st;
     st.error = (uint32_t*)w;
+    st.epoch_word = (uint32_t*)w + 1;
+    st.epoch = scan_epoch();
+    st.tag_agg = ((uint64_t)st.epoch << 2) | 1u;
+    st.tag_pre = ((uint64_t)st.epoch << 2) | 2u;
     st.spin_limit = scan_spin_limit();
     st.agg = (uint64_t*)(w + scan_layout::agg_offset());
     st.pre = (uint64_t*)(w + scan_layout::pre_offset(ngroups));
     st.xchg = (unsigned char*)w + scan_layout::xchg_offset(ngroups);
-    // Both slot arrays are cleared in one pass (the pre array directly follows the agg array).
-    const size_t nwords = scan_layout::clear_words(ngroups, Words<Acc>::NW);
-    scan_clear<<<(unsigned)(nwords == 0 ? 1 : ceil_div(nwords, 256)), 256, 0, s>>>(st.agg, nwords, st.error);
     constexpr unsigned kThreads = 64 * scan_layout::kScanWaves;
     if (ngroups > 0) {
         if (vec)
@@ -641,11 +656,13 @@ extern "C" int cdna3_scan_inclusive(int op, int dtype, const void* in, size_t n,
 extern "C" int cdna3_scan_status(const void* workspace, int* status, cdna4_stream_t stream) {
     if (workspace == nullptr || status == nullptr) return CDNA4_ERR_INVALID_VALUE;
     if (int e = check_device()) return e;
-    uint32_t word = 0;
+    // words 0 and 1 of the workspace: the epoch of a call whose look-back gave up, the epoch of the
+    // latest call; equal (and set) only when the latest call gave up
+    uint32_t words[2] = {0u, 0u};
     hipStream_t s = (hipStream_t)stream;
-    hipError_t e = hipMemcpyAsync(&word, workspace, sizeof(word), hipMemcpyDeviceToHost, s);
+    hipError_t e = hipMemcpyAsync(words, workspace, sizeof(words), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return (int)e;
-    *status = (int)word;
+    *status = (words[1] != 0u && words[0] == words[1]) ? 1 : 0;
     return 0;
 }

@@ -16,7 +16,7 @@ constexpr size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 constexpr size_t tile_elems(int vec, int u) { return (size_t)64 * vec * u; }
 constexpr size_t tiles_for(size_t n, int vec, int u) { return (n + tile_elems(vec, u) - 1) / tile_elems(vec, u); }
 
-// Workspace for `nslots` look-back slots (one per tile group): [error word, padded to 256 B]
+// Workspace for `nslots` look-back slots (one per tile group): [error and epoch words, padded to 256 B]
 // [agg slots: align256(nslots * 16)][pre slots: align256(nslots * 16)][exchange lines:
 // nslots * kXchgStride], two 64-bit words per slot and array (one used by 32-bit values), and per
 // group one 128-byte line in which its waves leave their tile totals and wave 0 the group's prefix
@@ -27,9 +27,6 @@ constexpr size_t ws_bytes(size_t ntiles) { return 256 + 2 * align256(ntiles * 16
 constexpr size_t agg_offset() { return 256; }
 constexpr size_t pre_offset(size_t ntiles) { return 256 + align256(ntiles * 16); }
 constexpr size_t xchg_offset(size_t ntiles) { return pre_offset(ntiles) + align256(ntiles * 16); }
-// 64-bit words the clear kernel zeroes from the start of the agg array: the whole agg array and
-// the used part of the pre array that follows it.
-constexpr size_t clear_words(size_t ntiles, int nw) { return (align256(ntiles * 16) + ntiles * (size_t)nw * 8) / 8; }
 
 // Aligned calls scan whole VEC-element vectors in the tiles and the last n % VEC elements in a
 // one-wave tail; misaligned calls scan everything element by element.

@@ -195,11 +195,17 @@ int cdna3_attn_decode_plan(const cdna3_decode_cfg* cfg, int dtype, int with_work
  * (fp32 accumulation, fp32 result). Integer sums wrap in two's complement.
  * reduce: `out` receives one element. scan: `out` receives n elements.
  * n == 0: reduce writes the operator's identity; scan writes nothing.
- * Workspace: >= the returned size, no initialisation needed.
+ * Workspace: >= the returned size. The scan's look-back flags carry a per-call epoch, so a
+ * workspace needs no clearing between calls (one launch per call, plus a one-wave tail launch
+ * for the last n % 4 elements of an aligned call). A zeroed workspace, or one last used by
+ * another scan, is always safe; memory never written by a scan is accepted too, with the caveat
+ * that a 64-bit word of it whose upper half happens to equal the call's 32-bit tag would be read
+ * as published (so zero a fresh workspace once to rule that out).
  * Scan status: the scan's decoupled look-back waits a bounded time for a predecessor tile; if a
- * wait ever exceeds that bound the result is not valid and the first 32-bit word of the
- * workspace is set non-zero (each scan call clears it first). cdna3_scan_status synchronises
- * `stream` and returns that word in *status (0 = the last scan on this workspace is valid).
+ * wait ever exceeds that bound the result is not valid and the call marks the workspace
+ * (its first word takes the call's epoch, the second word holds the epoch of the latest call).
+ * cdna3_scan_status synchronises `stream` and returns 1 in *status when the latest scan on this
+ * workspace gave up a wait, else 0.
  * The bound is 2^22 sleeps per wait; CDNA4_SCAN_SPIN_LIMIT in the environment (read on every
  * call) lowers it, so that tests can force the timeout path.
  */

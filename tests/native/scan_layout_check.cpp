@@ -4,8 +4,7 @@
 // (amd-incstinct-labs_amd/csrc/scan_layout.hpp) and walks, for each element type, tile size and
 // input size given, every vector / element load and store of every lane of every tile (tiles in
 // groups of kScanWaves waves, the last group's extra waves touching nothing), every slot word a
-// tile group publishes or reads during its look-back, the clear kernel's range and the tail's
-// reads, checking each against the sizes of the input, output and workspace buffers (the
+// tile group publishes or reads during its look-back, the header words and the tail's reads, checking each against the sizes of the input, output and workspace buffers (the
 // workspace sized as cdna3_scan_workspace_size sizes it). Both the aligned (16-byte vector) and the
 // misaligned (element-wise, half-size tiles) paths are replayed.
 // Usage: scan_layout_check [--plant] U n [n ...]   (U = vectors per lane of the aligned path;
@@ -63,8 +62,8 @@ static void replay(const Type& T, int U, size_t n, size_t in_off) {
     CHECK(ngroups <= ws_tiles, "%s U%d n%zu: %zu groups, workspace sized for %zu", T.name, U, n, ngroups, ws_tiles);
     CHECK(sl::agg_offset() >= 4 && sl::agg_offset() + slot_bytes <= sl::pre_offset(ngroups), "%s n%zu agg", T.name, n);
     CHECK(sl::pre_offset(ngroups) + slot_bytes <= ws, "%s n%zu pre", T.name, n);
-    const size_t clear_end = sl::agg_offset() + sl::clear_words(ngroups, T.NW) * 8;
-    CHECK(clear_end <= ws && clear_end >= sl::pre_offset(ngroups) + slot_bytes, "%s n%zu clear", T.name, n);
+    // header: the error and epoch words (two u32) before the agg array
+    CHECK(8 <= sl::agg_offset() && sl::agg_offset() <= ws, "%s n%zu header", T.name, n);
     // every wave of every group maps to one tile; exactly the tiles below ntiles are live
     size_t live_tiles = 0;
     for (size_t g = 0; g < ngroups; ++g)

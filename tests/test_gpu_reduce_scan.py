@@ -92,13 +92,46 @@ def test_scan_tile_boundaries(dtype):
 
 
 def test_scan_repeated_calls_reuse_workspace():
-    # Flags in the workspace are cleared by each call: the same workspace serves many calls.
+    # The look-back flags carry a per-call epoch, so one workspace serves many calls with no
+    # clearing: calls alternate between two inputs and two dtypes, so that a flag left by the
+    # previous call, if it were accepted, would hand a group the other input's prefix.
     n = 300007
-    h, t = make(oracle.I32, n, 5)
-    ws = torch.empty(cdna4.scan_workspace_size(n, cdna4.I32), dtype=torch.uint8, device=DEV)
-    want = oracle.scan_inclusive(oracle.SUM, oracle.I32, h)
-    for _ in range(5):
-        assert np.array_equal(cdna4.scan_inclusive(t, "sum", workspace=ws).cpu().numpy(), want)
+    ha, ta = make(oracle.I32, n, 5)
+    hb, tb = make(oracle.I32, n, 6)
+    hc, tc = make(oracle.I64, n, 7)
+    ws = torch.empty(cdna4.scan_workspace_size(n, cdna4.I64), dtype=torch.uint8, device=DEV)
+    want = {id(ta): oracle.scan_inclusive(oracle.SUM, oracle.I32, ha), id(tb): oracle.scan_inclusive(oracle.SUM, oracle.I32, hb),
+            id(tc): oracle.scan_inclusive(oracle.SUM, oracle.I64, hc)}
+    for t in (ta, tb, ta, tc, tb, tc, ta, tb):
+        got = cdna4.scan_inclusive(t, "sum", workspace=ws, check=False)
+        assert cdna4.scan_status(ws) == 0
+        assert np.array_equal(got.cpu().numpy(), want[id(t)])
+
+
+@pytest.mark.parametrize("fill", ["zeros", "ones", "random", "stale_tags"])
+def test_scan_workspace_needs_no_clearing(fill):
+    # A workspace of any prior content: zeroed, all 0xFF, random bytes, or slot words whose upper
+    # halves hold every small tag value (epoch 1, both kinds), never the call's own tag.
+    n = (1 << 22) + 3
+    h, t = make(oracle.F32, n, 9)
+    size = cdna4.scan_workspace_size(n, cdna4.F32)
+    if fill == "zeros":
+        ws = torch.zeros(size, dtype=torch.uint8, device=DEV)
+    elif fill == "ones":
+        ws = torch.full((size,), 0xFF, dtype=torch.uint8, device=DEV)
+    elif fill == "random":
+        ws = torch.randint(0, 256, (size,), dtype=torch.uint8, device=DEV,
+                           generator=torch.Generator(device=DEV).manual_seed(3))
+    else:
+        words = torch.arange(size // 8, dtype=torch.int64, device=DEV)
+        ws = ((((words % 2) + 5) << 32) | (words & 0xFFFF)).view(torch.uint8)   # tags 5, 6 = epoch 1
+    want = oracle.scan_inclusive(oracle.SUM, oracle.F32, h)
+    for _ in range(3):
+        got = cdna4.scan_inclusive(t, "sum", workspace=ws, check=False)
+        assert cdna4.scan_status(ws) == 0
+        g = got.cpu().numpy().astype(np.float64)
+        scale = np.maximum(1.0, np.sqrt(np.arange(1, n + 1, dtype=np.float64)))
+        assert np.max(np.abs(g - want) / scale) <= 1e-3
 
 
 @pytest.mark.parametrize("dtype", [oracle.I32, oracle.I64, oracle.F32, oracle.F64, oracle.F16, oracle.BF16])
