@@ -38,7 +38,7 @@ __all__ = [
     "rope_table_f32", "flash_attn", "flash_attn_decode", "CDNA4Error", "PrefillStrides", "prefill_strided",
     "scatter_kv_f16", "repack_f16", "rope_append_kv_f16", "ModelCfg", "GenerateCfg", "Session",
     "PlanInfo", "prefill_plan", "decode_plan", "scan_status", "KERNEL_NAMES", "decode_noalloc",
-    "decode_noalloc_max_bytes",
+    "decode_noalloc_max_bytes", "softmax_rows_f32",
 ]
 
 # Element types and operators (include/cdna4_attn.h).
@@ -129,6 +129,7 @@ def _declare(l: ctypes.CDLL) -> None:
     sig = {
         "cdna3_abi_version": (c_int, []),
         "cdna3_error_string": (ctypes.c_char_p, [c_int]),
+        "cdna3_softmax_rows_f32": (c_int, [vp, vp, c_int, c_int, vp]),
         "cdna3_attn_prefill": (c_int, [vp, vp, vp, vp, ctypes.POINTER(PrefillCfg), c_int, vp]),
         "cdna3_attn_prefill_strided": (c_int, [vp, vp, vp, vp, ctypes.POINTER(PrefillCfg),
                                                ctypes.POINTER(PrefillStrides), c_int, vp]),
@@ -434,6 +435,18 @@ def layernorm_f32(X: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps:
         out = torch.empty_like(X) if out is None else out
     _check(lib().cdna3_layernorm_f32(_ptr(X), _ptr(gamma), _ptr(beta), _ptr(out), M, H, eps, _stream(stream)),
            "cdna3_layernorm_f32")
+    return out
+
+
+def softmax_rows_f32(X: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Row softmax of X fp32 [M][H] (softmax_kernel, bench_softmax.hip:59-105) into out (may be X)."""
+    _dev(X)
+    if X.dtype != torch.float32 or X.dim() != 2:
+        raise ValueError("X must be fp32 [M][H]")
+    M, H = X.shape
+    with _on_stream(stream):
+        out = torch.empty_like(X) if out is None else out
+    _check(lib().cdna3_softmax_rows_f32(_ptr(X), _ptr(out), M, H, _stream(stream)), "cdna3_softmax_rows_f32")
     return out
 
 

@@ -1,10 +1,11 @@
-// Runtime norm and RoPE entry points for gfx950: RMSNorm and two-pass LayerNorm with one
-// wave per row (DPP/permlane butterfly reductions, zero LDS), rotate-half RoPE with one
+// Runtime norm and RoPE entry points for gfx950: RMSNorm, two-pass LayerNorm and row softmax with
+// one wave per row (DPP/permlane butterfly reductions, zero LDS), rotate-half RoPE with one
 // thread per (d, d + D/2) pair, and the RoPE cos/sin table built on the device.
 //
 // Reference behaviour restated:
 //   rmsnorm_f32_kernel  cdna3-prims/include/cdna3/runtime/forward.hpp:34-56
 //   layernorm_kernel    research/wave-primitives/benchmarks/bench_layernorm.hip:51-114
+//   softmax_kernel<DPP> research/wave-primitives/benchmarks/bench_softmax.hip:59-105
 //   rope_kernel         cdna3-prims/include/cdna3/runtime/forward.hpp:135-148
 //   Session::fill_rope  cdna3-prims/include/cdna3/runtime/session.hpp:120-135
 #include "common.hpp"
@@ -14,6 +15,7 @@ namespace cdna4 {
 namespace {
 
 using wave::xlane::allreduce;
+using wave::xlane::Max;
 using wave::xlane::row_allreduce;
 using wave::xlane::Sum;
 
@@ -230,6 +232,80 @@ __global__ __launch_bounds__(256) void layernorm_any(const float* __restrict__ X
     for (int c = lane; c < H; c += 64) y[c] = (x[c] - mean) * inv * G[c] + B[c];
 }
 
+// ---- row softmax: y = exp(x - max(x)) / sum(exp(x - max(x))) per row ------------------------
+// The reference's order of work: the row maximum (DPP max), exp(x - m) (__expf), their sum (DPP
+// sum), then each value times 1 / sum. Columns past H take -inf into the maximum and 0 into the
+// sum. Same row layouts as the norms: one wave per row with the row in registers (H <= 256 NV),
+// 16 lanes per row for H <= 64, two passes for anything else.
+template <int NV, bool kNT>
+__global__ __launch_bounds__(256) void softmax_vec(const float* __restrict__ X, float* __restrict__ Y, int M, int H) {
+    const unsigned lane = threadIdx.x & 63u;
+    const int row = blockIdx.x * kNormWaves + (int)(threadIdx.x >> 6);
+    if (row >= M) return;
+    const float* x = X + (size_t)row * H;
+    float* y = Y + (size_t)row * H;
+    float4 v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int c = (k * 64 + (int)lane) * 4;
+        v[k] = (c < H) ? ld4<kNT>(x + c) : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) m = fmaxf(fmaxf(m, fmaxf(v[k].x, v[k].y)), fmaxf(v[k].z, v[k].w));
+    m = allreduce(m, Max{});
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        v[k] = make_float4(__expf(v[k].x - m), __expf(v[k].y - m), __expf(v[k].z - m), __expf(v[k].w - m));
+        sum += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+    }
+    const float inv = 1.f / allreduce(sum, Sum{});
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int c = (k * 64 + (int)lane) * 4;
+        if (c < H) st4<kNT>(y + c, make_float4(v[k].x * inv, v[k].y * inv, v[k].z * inv, v[k].w * inv));
+    }
+}
+
+template <bool kNT>
+__global__ __launch_bounds__(256) void softmax_row16(const float* __restrict__ X, float* __restrict__ Y, int M, int H) {
+    const int c = (int)(threadIdx.x & 15u) * 4;
+    const int row0 = blockIdx.x * (kRows16 * kRowsPerLane) + (int)(threadIdx.x >> 4);
+    float4 v[kRowsPerLane];
+#pragma unroll
+    for (int r = 0; r < kRowsPerLane; ++r) {
+        const int row = row0 + r * kRows16;
+        v[r] = row < M && c < H ? ld4<kNT>(X + (size_t)row * H + c)
+                                : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    }
+#pragma unroll
+    for (int r = 0; r < kRowsPerLane; ++r) {
+        const int row = row0 + r * kRows16;
+        float m = row_allreduce(fmaxf(fmaxf(v[r].x, v[r].y), fmaxf(v[r].z, v[r].w)), Max{});
+        if (m == -INFINITY) m = 0.f;   // rows past M: all -inf, kept finite (nothing is stored)
+        const float4 e = make_float4(__expf(v[r].x - m), __expf(v[r].y - m), __expf(v[r].z - m), __expf(v[r].w - m));
+        const float inv = 1.f / row_allreduce((e.x + e.y) + (e.z + e.w), Sum{});
+        if (row < M && c < H) st4<kNT>(Y + (size_t)row * H + c, make_float4(e.x * inv, e.y * inv, e.z * inv, e.w * inv));
+    }
+}
+
+// Reads each value three times and may run in place (X == Y), so X and Y are not restrict.
+__global__ __launch_bounds__(256) void softmax_any(const float* X, float* Y, int M, int H) {
+    const unsigned lane = threadIdx.x & 63u;
+    const int row = blockIdx.x * kNormWaves + (int)(threadIdx.x >> 6);
+    if (row >= M) return;
+    const float* x = X + (size_t)row * H;
+    float* y = Y + (size_t)row * H;
+    float m = -INFINITY;
+    for (int c = lane; c < H; c += 64) m = fmaxf(m, x[c]);
+    m = allreduce(m, Max{});
+    float s = 0.f;
+    for (int c = lane; c < H; c += 64) s += __expf(x[c] - m);
+    const float inv = 1.f / allreduce(s, Sum{});
+    for (int c = lane; c < H; c += 64) y[c] = __expf(x[c] - m) * inv;
+}
+
 // One thread per (row, head, d) with d < D/2: reads t[d] and t[d + D/2] once, writes both.
 __global__ __launch_bounds__(256) void rope_pairs(uint16_t* __restrict__ T, const float* __restrict__ cosv,
                                                   const float* __restrict__ sinv, int seq, int heads, int D) {
@@ -330,6 +406,30 @@ extern "C" int cdna3_layernorm_f32(const float* X, const float* gamma, const flo
     return dispatch_nv(H, [&](auto nv) {
         if (nt) layernorm_vec<decltype(nv)::value, true><<<grid, 256, 0, s>>>(X, gamma, beta, Y, M, H, eps);
         else layernorm_vec<decltype(nv)::value, false><<<grid, 256, 0, s>>>(X, gamma, beta, Y, M, H, eps);
+        return launch_status();
+    });
+}
+
+extern "C" int cdna3_softmax_rows_f32(const float* X, float* Y, int M, int H, cdna4_stream_t stream) {
+    if (M < 0 || H <= 0 || (M > 0 && (!X || !Y))) return CDNA4_ERR_INVALID_VALUE;
+    if (M == 0) return 0;
+    if (int e = check_device()) return e;
+    hipStream_t s = (hipStream_t)stream;
+    const unsigned grid = ceil_div((size_t)M, kNormWaves);
+    const bool vec = (H % 4 == 0) && H <= 4096 && aligned16(X) && aligned16(Y);
+    if (!vec) {
+        softmax_any<<<grid, 256, 0, s>>>(X, Y, M, H);
+        return launch_status();
+    }
+    const bool nt = (size_t)M * (size_t)H * sizeof(float) >= kStreamBytes;
+    if (H <= 64) {
+        if (nt) softmax_row16<true><<<ceil_div((size_t)M, kRows16 * kRowsPerLane), 256, 0, s>>>(X, Y, M, H);
+        else softmax_row16<false><<<ceil_div((size_t)M, kRows16 * kRowsPerLane), 256, 0, s>>>(X, Y, M, H);
+        return launch_status();
+    }
+    return dispatch_nv(H, [&](auto nv) {
+        if (nt) softmax_vec<decltype(nv)::value, true><<<grid, 256, 0, s>>>(X, Y, M, H);
+        else softmax_vec<decltype(nv)::value, false><<<grid, 256, 0, s>>>(X, Y, M, H);
         return launch_status();
     });
 }

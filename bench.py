@@ -451,12 +451,13 @@ def bench_norms(torch, cdna4, steps, warmup):
     """The runtime norms at the reference's LayerNorm benchmark shapes (65536 rows x 64 and x 512
     f32 columns; research/wave-primitives/benchmarks/bench_layernorm.hip, published in
     docs/paper-draft.md:447,450 as 35.7 and 65.3 us on MI300X): two-pass LayerNorm (eps 1e-5, f32
-    gamma/beta) and RMSNorm (eps 1e-6, fp16 weights). Inputs and outputs rotate over >= 1 GiB so
+    gamma/beta), RMSNorm (eps 1e-6, fp16 weights) and the row softmax (bench_softmax.hip, 65536 x 512
+    published as 65.5 us on MI300X, docs/paper-draft.md:466). Inputs and outputs rotate over >= 1 GiB so
     the Infinity Cache cannot serve repeats. Algorithmic bytes 2*M*H*4 (read X, write Y)."""
     M = 65536
     ref_us = {64: 35.7, 512: 65.3}
     g = torch.Generator(device="cuda").manual_seed(9)
-    out = {"config": {"workload": "reference LayerNorm benchmark shapes", "rows": M, "dtype": "f32"}}
+    out = {"config": {"workload": "reference LayerNorm and softmax benchmark shapes", "rows": M, "dtype": "f32"}}
     for H in (64, 512):
         nb = max(2, (1 << 30) // (2 * M * H * 4))
         xs = [torch.randn(M, H, device="cuda", generator=g) for _ in range(nb)]
@@ -473,11 +474,16 @@ def bench_norms(torch, cdna4, steps, warmup):
                            for x, y in zip(xs, ys)])
         rms = abi_launcher(torch, cdna4, "cdna3_rmsnorm_f32",
                            [(x.data_ptr(), w16.data_ptr(), y.data_ptr(), M, H, 1e-6) for x, y in zip(xs, ys)])
-        for name, fn in (("layernorm", ln), ("rmsnorm", rms)):
+        cdna4.softmax_rows_f32(xs[0], out=ys[0])
+        sm = abi_launcher(torch, cdna4, "cdna3_softmax_rows_f32",
+                          [(x.data_ptr(), y.data_ptr(), M, H) for x, y in zip(xs, ys)])
+        for name, fn in (("layernorm", ln), ("rmsnorm", rms), ("softmax", sm)):
             ms, _ = time_launches(torch, fn, steps, warmup)
             gbs = nbytes / (ms * 1e-3) / 1e9
             entry[name] = {"us": round(ms * 1e3, 2), "GBs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
         entry["layernorm"]["reference_us_mi300x"] = ref_us[H]
+        if H == 512:
+            entry["softmax"]["reference_us_mi300x"] = 65.5   # docs/paper-draft.md:466
         out[f"{M}x{H}"] = entry
         del xs, ys
         torch.cuda.empty_cache()

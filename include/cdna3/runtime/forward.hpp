@@ -32,6 +32,10 @@ inline hipError_t layernorm_f32(const float* X, const float* gamma, const float*
                                 float eps = 1e-5f, hipStream_t stream = nullptr) {
     return (hipError_t)cdna3_layernorm_f32(X, gamma, beta, Y, M, H, eps, (cdna4_stream_t)stream);
 }
+// Row softmax of M rows of H fp32 values (bench_softmax.hip:59-105's softmax_kernel); X may equal Y.
+inline hipError_t softmax_rows_f32(const float* X, float* Y, int M, int H, hipStream_t stream = nullptr) {
+    return (hipError_t)cdna3_softmax_rows_f32(X, Y, M, H, (cdna4_stream_t)stream);
+}
 inline hipError_t rope_f16(__half* T, const float* cos, const float* sin, int seq, int heads, int D,
                            hipStream_t stream = nullptr) {
     return (hipError_t)cdna3_rope_f16(T, cos, sin, seq, heads, D, (cdna4_stream_t)stream);

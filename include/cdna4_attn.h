@@ -217,6 +217,15 @@ int cdna3_scan_inclusive(int op, int dtype, const void* in, size_t n, void* out,
                          void* workspace, size_t ws_bytes, cdna4_stream_t stream);
 int cdna3_scan_status(const void* workspace, int* status, cdna4_stream_t stream);
 
+/* ---- row softmax ---------------------------------------------------------------
+ * cdna3_softmax_rows_f32 replaces softmax_kernel<DPP> (research/wave-primitives/benchmarks/
+ * bench_softmax.hip:59-105, launched there with one 64-lane block per row of 64 x ELEMS_PER_LANE
+ * columns): Y[r][c] = exp(X[r][c] - max_c X[r]) / sum_c exp(X[r][c] - max_c X[r]) for M rows of
+ * H fp32 values, any H >= 1 (the reference's kernel fixed H at compile time); X may equal Y.
+ * Invalid: M < 0, H < 1, null pointers with M > 0.
+ */
+int cdna3_softmax_rows_f32(const float* X, float* Y, int M, int H, cdna4_stream_t stream);
+
 /* ---- runtime norms and RoPE ---------------------------------------------------
  * cdna3_rmsnorm_f32 replaces rmsnorm_f32_kernel (cdna3-prims/include/cdna3/runtime/
  * forward.hpp:34-56): Y[m][i] = X[m][i] * rsqrt(mean_i(X[m][:]^2) + eps) * W[i],

@@ -57,6 +57,7 @@ def lib() -> ctypes.CDLL:
         l.orc_scan_inclusive.argtypes = [c_int, c_int, vp, c_size, vp]
         l.orc_rmsnorm_f32.argtypes = [_f32p, _u16p, _f32p, c_int, c_int, c_float]
         l.orc_layernorm_f32.argtypes = [_f32p, _f32p, _f32p, _f32p, c_int, c_int, c_float]
+        l.orc_softmax_rows_f32.argtypes = [_f32p, _f32p, c_int, c_int]
         l.orc_rope_table.argtypes = [_f32p, _f32p, c_int, c_int, c_int, c_float]
         l.orc_rope_f16.argtypes = [_u16p, _f32p, _f32p, c_int, c_int, c_int]
         l.orc_scatter_kv_f16.argtypes = [_u16p, _u16p] + [c_int] * 5
@@ -186,6 +187,16 @@ def layernorm(X: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float) ->
     Y = np.empty_like(X)
     lib().orc_layernorm_f32(X.reshape(-1), np.ascontiguousarray(gamma, np.float32),
                             np.ascontiguousarray(beta, np.float32), Y.reshape(-1), M, H, eps)
+    return Y
+
+
+def softmax_rows(X: np.ndarray) -> np.ndarray:
+    """Row softmax of a [M][H] fp32 array (bench_softmax.hip:59-105), exponentials and sums in
+    double, rounded to fp32."""
+    X = np.ascontiguousarray(X, np.float32)
+    M, H = X.shape
+    Y = np.empty_like(X)
+    lib().orc_softmax_rows_f32(X.reshape(-1), Y.reshape(-1), M, H)
     return Y
 
 

@@ -20,6 +20,8 @@
  *   orc_scan_inclusive wave::dpp::scan_inclusive_* semantics (wave_scan_dpp.hpp:51-70)
  *   orc_rmsnorm_f32   cdna3-prims/include/cdna3/runtime/forward.hpp:34-56
  *   orc_layernorm_f32 research/wave-primitives/benchmarks/bench_layernorm.hip:51-114
+ *   orc_softmax_rows_f32 research/wave-primitives/benchmarks/bench_softmax.hip:59-105
+ *                     (softmax_kernel: row max, exp(x - max), row sum, x 1/sum), statistics in double
  *   orc_rope_table    cdna3-prims/include/cdna3/runtime/session.hpp:120-135 (fill_rope)
  *   orc_rope_f16      cdna3-prims/include/cdna3/runtime/forward.hpp:135-148 (rope_kernel),
  *                     reading every input element before any is written
@@ -350,6 +352,20 @@ void orc_layernorm_f32(const float* X, const float* G, const float* B, float* Y,
         for (int i = 0; i < H; ++i) { const double d = x[i] - mean; q += d * d; }
         const double inv = 1.0 / sqrt(q / H + (double)eps);
         for (int i = 0; i < H; ++i) y[i] = (float)((x[i] - mean) * inv * G[i] + B[i]);
+    }
+}
+
+/* bench_softmax.hip:59-105: m = max of the row, e = exp(x - m), y = e * (1 / sum(e)); the sum and
+ * the exponentials in double, rounded to float at the end. */
+void orc_softmax_rows_f32(const float* X, float* Y, int M, int H) {
+    for (int r = 0; r < M; ++r) {
+        const float* x = X + (size_t)r * H;
+        float* y = Y + (size_t)r * H;
+        float m = -INFINITY;
+        for (int i = 0; i < H; ++i) m = x[i] > m ? x[i] : m;
+        double s = 0.0;
+        for (int i = 0; i < H; ++i) s += exp((double)x[i] - (double)m);
+        for (int i = 0; i < H; ++i) y[i] = (float)(exp((double)x[i] - (double)m) / s);
     }
 }
 

@@ -74,6 +74,9 @@ def test_invalid_arguments_rejected_without_gpu():
     assert l.cdna3_scan_inclusive(cdna4.SUM, cdna4.F32, p, 10, p, None, 0, None) == 1
     assert l.cdna3_scan_inclusive(cdna4.SUM, cdna4.F32, p, 0, p, None, 0, None) == 0      # n == 0: nothing to do
     assert l.cdna3_rmsnorm_f32(p, p, p, 4, 0, 1e-6, None) == 1
+    assert l.cdna3_softmax_rows_f32(p, p, 4, 0, None) == 1                                  # H < 1
+    assert l.cdna3_softmax_rows_f32(None, p, 4, 8, None) == 1                               # null
+    assert l.cdna3_softmax_rows_f32(p, p, 0, 8, None) == 0                                  # M == 0
     assert l.cdna3_rope_f16(p, p, p, 4, 2, 63, None) == 1                                   # odd D
     assert l.cdna3_rope_table_f32(p, p, 0, 4, 64, -1.0, None) == 1
     assert l.cdna3_scatter_kv_f16(p, p, 4, 2, 64, 10, 12, None) == 1                        # pos0 + T > max_seq

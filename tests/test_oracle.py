@@ -282,6 +282,27 @@ def test_rmsnorm_invariants():
     np.testing.assert_allclose(oracle.rmsnorm(X, w2, 1e-6), 2.0 * Y, atol=1e-6)
 
 
+def test_softmax_rows_against_scipy_and_invariants():
+    from scipy.special import softmax
+    X = _lcg_rows(64, 512)                                  # bench_softmax.hip:117 input generator
+    Y = oracle.softmax_rows(X)
+    np.testing.assert_allclose(Y.sum(axis=1, dtype=np.float64), 1.0, atol=1e-6)   # bench_softmax.hip:123-133
+    want = softmax(X.astype(np.float64), axis=1)
+    np.testing.assert_allclose(Y, want, rtol=2e-7, atol=0)
+    # Shift invariance (exact: the oracle subtracts the row maximum first), a constant row is
+    # uniform, one dominant entry takes all the weight, and a permutation of a row permutes it.
+    np.testing.assert_array_equal(oracle.softmax_rows(X + 2.0), Y)
+    assert np.all(oracle.softmax_rows(np.full((2, 77), 3.5, np.float32)) == np.float32(1.0 / 77))
+    row = np.zeros((1, 9), np.float32)
+    row[0, 4] = 200.0
+    assert oracle.softmax_rows(row)[0, 4] == 1.0 and oracle.softmax_rows(row).sum() == 1.0
+    perm = np.random.default_rng(0).permutation(512)
+    np.testing.assert_array_equal(oracle.softmax_rows(X[:, perm]), Y[:, perm])
+    Z = oracle.normal(6, 3 * 1000, 0.0, 8.0).reshape(3, 1000)   # wide spread: tiny weights stay relative
+    np.testing.assert_allclose(oracle.softmax_rows(Z), softmax(Z.astype(np.float64), axis=1), rtol=2e-7,
+                               atol=1e-44)
+
+
 def test_rope_table_and_rotation():
     D, T, heads = 64, 20, 3
     c, s = oracle.rope_table(0, T, D, 10000.0)
