@@ -342,6 +342,14 @@ constexpr int kWgChunks = 8;
 // default policy (the runtime's decode step measured 3 % slower with non-temporal copies).
 constexpr double kStreamBytes = 256.0 * 1024 * 1024;
 
+// CDNA4_DECODE_SPLIT_K=1 in the environment (read on every call, including the workspace-size and
+// plan queries) keeps calls with a workspace on the split-K plan where whole rounds of CUs would
+// otherwise take the one-launch plan, so the two plans can be timed against each other.
+bool force_split_k() {
+    const char* e = getenv("CDNA4_DECODE_SPLIT_K");
+    return e && e[0] == '1';
+}
+
 bool plan_decode(const cdna3_decode_cfg& c, bool split_k, Plan& p) {
     if (c.D != 64 && c.D != 128) return false;
     if (c.N < 1 || c.nQHeads < 1 || c.nKVHeads < 1 || c.batch < 1) return false;
@@ -354,7 +362,7 @@ bool plan_decode(const cdna3_decode_cfg& c, bool split_k, Plan& p) {
     const long long rows = (long long)c.batch * c.nKVHeads * p.HB;
     const int cus = device_cus();
     p.nt = 4.0 * c.batch * c.nKVHeads * (double)c.N * c.D > kStreamBytes;
-    p.wg = !split_k || c.N <= W * kWgChunks * kDecT || (cus > 0 && rows % cus == 0);
+    p.wg = !split_k || c.N <= W * kWgChunks * kDecT || (cus > 0 && rows % cus == 0 && !force_split_k());
     if (p.wg) {   // one workgroup per (batch, kv head, head group); W contiguous key ranges
         p.KPW = wg_keys_per_wave(c.N, W);
         p.P = 1;

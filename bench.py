@@ -312,6 +312,22 @@ def bench_decode(torch, cdna4, steps, warmup):
         torch, lambda i=0: cdna4.decode(q, kv[i % 2][0], kv[i % 2][1], o, cfg, workspace=ws), steps, warmup)
     nbytes = 2.0 * B * HK * N * D * 2 + 2.0 * B * HQ * D * 2
     gbs = nbytes / (avg_ms * 1e-3) / 1e9
+    plan_main = cdna4.decode_plan(cfg, torch.float16, with_workspace=True)
+    # Config 4 names split-K across workgroups with a DPP final reduce. Batch x kv heads is the CU
+    # count here, so the library takes the one-launch plan (whole rounds of CUs, the waves of each
+    # workgroup merging in LDS); the split-K grid + DPP merge is timed beside it, forced with
+    # CDNA4_DECODE_SPLIT_K=1 (read by the library on every call).
+    os.environ["CDNA4_DECODE_SPLIT_K"] = "1"
+    try:
+        plan_split = cdna4.decode_plan(cfg, torch.float16, with_workspace=True)
+        ws_split = torch.empty(cdna4.decode_workspace_size(cfg), dtype=torch.uint8, device="cuda")
+        split_ms, _ = time_launches(
+            torch, lambda i=0: cdna4.decode(q, kv[i % 2][0], kv[i % 2][1], o, cfg, workspace=ws_split), steps, warmup)
+    finally:
+        del os.environ["CDNA4_DECODE_SPLIT_K"]
+    split_k = {"us": round(split_ms * 1e3, 2), "GBs": round(nbytes / (split_ms * 1e-3) / 1e9, 1),
+               "plan": plan_split.name, "partials_per_head": int(plan_split.partials)}
+    del ws_split
     # PyTorch's SDPA (flash backend, GQA broadcast) on the same q / K / V, for comparison
     sdpa = None
     try:
@@ -358,7 +374,8 @@ def bench_decode(torch, cdna4, steps, warmup):
         batch1[f"N{n1}"] = entry
         del kv1
         torch.cuda.empty_cache()
-    return {"value": gbs, "unit": "GB/s", "avg_us": avg_ms * 1e3, "vs_torch_sdpa": sdpa, "batch1": batch1,
+    return {"value": gbs, "unit": "GB/s", "avg_us": avg_ms * 1e3, "plan": plan_main.name, "split_k_plan": split_k,
+            "vs_torch_sdpa": sdpa, "batch1": batch1,
             "config": {"workload": "flash decode, BASELINE config 4", "batch": B, "q_heads": HQ, "kv_heads": HK,
                        "head_dim": D, "kv_len": N, "dtype": "fp16"},
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",

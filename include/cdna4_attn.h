@@ -137,7 +137,9 @@ int cdna3_attn_prefill_strided(const void* Q, const void* K, const void* V, void
  * the one-launch plan, which needs no memory beyond q, K, V and o: one workgroup per (batch,
  * kv head, group of 16 query heads) streams the whole cache, like the reference's launchers,
  * which take no workspace. Both forms are capturable and re-entrant across streams (a
- * workspace must not be shared by calls that overlap).
+ * workspace must not be shared by calls that overlap). CDNA4_DECODE_SPLIT_K=1 in the environment
+ * (read on every call, by the workspace-size and plan queries too) keeps calls with a workspace
+ * on the split-K plan at whole rounds of CUs as well, to time the two plans against each other.
  */
 size_t cdna3_attn_decode_workspace_size(const cdna3_decode_cfg* cfg);
 int cdna3_attn_decode(const void* q, const void* K, const void* V, void* o,

@@ -342,6 +342,17 @@ def test_decode_whole_rounds_one_launch_d128_strided_cached():
     check_decode(128, 1500, 32, HK, _cus() // HK, torch.bfloat16, "decode_wg", stride=2048, seed=12)
 
 
+def test_decode_whole_rounds_split_k_when_forced(monkeypatch):
+    # CDNA4_DECODE_SPLIT_K=1: the whole-rounds shape above (config 4's kind) on the split-K grid and
+    # its DPP merge instead of the one-launch plan.
+    HK = 8
+    monkeypatch.setenv("CDNA4_DECODE_SPLIT_K", "1")
+    check_decode(128, 1500, 32, HK, _cus() // HK, torch.float16, "decode_split", seed=13)
+    monkeypatch.delenv("CDNA4_DECODE_SPLIT_K")
+    cfg = cdna4.DecodeCfg(128, 1500, 32, HK, _cus() // HK, 0)
+    assert cdna4.decode_plan(cfg, torch.float16, with_workspace=True).name == "decode_wg"
+
+
 @pytest.mark.parametrize("N,HQ,HK,B", [(8192, 32, 8, 1), (3000, 40, 2, 2), (4097, 12, 12, 1)])
 def test_decode_without_workspace_one_launch(N, HQ, HK, B):
     # The reference launchers' contract: no workspace, one launch, any cache length.
