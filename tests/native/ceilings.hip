@@ -8,8 +8,9 @@
 //                    preloaded register pairs (no VALU work);
 //   mfma_bf16_exp    the same with one v_exp_f32 beside every two MFMAs (the prefill's ratio of
 //                    exponentials to matrix instructions);
-// each the median of five timed runs (HIP events), printed as one JSON line. `ceilings mfma S [exp]`
-// instead runs only the MFMA stream for about S seconds, one line per 50 launches.
+//   mfma_f16(_exp)   both with v_mfma_f32_16x16x32_f16 on the same bit patterns;
+// each the median of five timed runs (HIP events), printed as one JSON line. `ceilings mfma S [exp]
+// [f16]` instead runs only one MFMA stream for about S seconds, one line per 50 launches.
 // The buffer reads are 1 GiB, four times the 256 MB Infinity Cache, so no read is served from it.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -31,6 +32,7 @@
 
 using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 using cdna4::mfma::bf16x8;
+using cdna4::mfma::f16x8;
 using cdna4::mfma::f32x4;
 
 // Each workgroup reads one contiguous chunk of the buffer (its share, in 256 x U vector steps, the U
@@ -70,10 +72,10 @@ __global__ __launch_bounds__(256) void copy_nt(const u32x4* __restrict__ src, u3
     for (; i < hi; i += 256) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
-template <bool kExp>
+template <bool kExp, class T>
 __global__ __launch_bounds__(512) void mfma_stream(const uint32_t* __restrict__ seed, int iters, float* out) {
     const int lane = threadIdx.x & 63;
-    bf16x8 a[4], b[4];
+    T a[4], b[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         u32x4 wa, wb;
@@ -82,8 +84,8 @@ __global__ __launch_bounds__(512) void mfma_stream(const uint32_t* __restrict__ 
             wa[e] = seed[(j * 8 + e) * 64 + lane];
             wb[e] = seed[(j * 8 + 4 + e) * 64 + lane];
         }
-        a[j] = __builtin_bit_cast(bf16x8, wa);
-        b[j] = __builtin_bit_cast(bf16x8, wb);
+        a[j] = __builtin_bit_cast(T, wa);
+        b[j] = __builtin_bit_cast(T, wb);
     }
     f32x4 c[4] = {};
     float x[4] = {0.5f, 0.25f, 0.125f, 0.0625f};
@@ -92,7 +94,7 @@ __global__ __launch_bounds__(512) void mfma_stream(const uint32_t* __restrict__ 
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                c[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j], b[(j + r) & 3], c[j], 0, 0, 0);
+                c[j] = cdna4::mfma::mma_16x16x32(a[j], b[(j + r) & 3], c[j]);
                 if (kExp && (j & 1)) x[(r * 2 + j / 2) & 3] = __builtin_amdgcn_exp2f(-x[(r * 2 + j / 2) & 3]);
             }
     }
@@ -129,9 +131,16 @@ static float time_ms(F&& launch, int reps) {
     return median(t);
 }
 
-// `ceilings mfma SECONDS [exp]`: only the MFMA stream (with the exponentials when `exp` is given),
-// launched back to back for about SECONDS, for sampling board power and clocks beside it.
-static int mfma_loop(int cus, double seconds, bool with_exp) {
+// `ceilings mfma SECONDS [exp] [f16]`: only one MFMA stream (with the exponentials when `exp` is
+// given, fp16 operands when `f16` is), launched back to back for about SECONDS, for sampling board
+// power and clocks beside it.
+template <class T>
+static void launch_mfma(bool with_exp, int cus, const uint32_t* seed, int iters, float* out) {
+    if (with_exp) mfma_stream<true, T><<<cus, 512>>>(seed, iters, out);
+    else mfma_stream<false, T><<<cus, 512>>>(seed, iters, out);
+}
+
+static int mfma_loop(int cus, double seconds, bool with_exp, bool f16) {
     std::vector<uint32_t> h(32 * 64);
     uint32_t s = 12345u;
     for (auto& v : h) {
@@ -152,8 +161,8 @@ static int mfma_loop(int cus, double seconds, bool with_exp) {
     while (total_ms < seconds * 1e3) {
         CK(hipEventRecord(e0));
         for (int r = 0; r < 50; ++r) {
-            if (with_exp) mfma_stream<true><<<cus, 512>>>(buf, iters, fout);
-            else mfma_stream<false><<<cus, 512>>>(buf, iters, fout);
+            if (f16) launch_mfma<f16x8>(with_exp, cus, buf, iters, fout);
+            else launch_mfma<bf16x8>(with_exp, cus, buf, iters, fout);
         }
         CK(hipEventRecord(e1));
         CK(hipEventSynchronize(e1));
@@ -161,8 +170,8 @@ static int mfma_loop(int cus, double seconds, bool with_exp) {
         CK(hipEventElapsedTime(&ms, e0, e1));
         total_ms += ms;
         launches += 50;
-        printf("{\"mfma_loop\": \"%s\", \"elapsed_s\": %.1f, \"TFLOPs\": %.1f}\n", with_exp ? "bf16+exp" : "bf16",
-               total_ms * 1e-3, 50 * flop / (ms * 1e-3) / 1e12);
+        printf("{\"mfma_loop\": \"%s%s\", \"elapsed_s\": %.1f, \"TFLOPs\": %.1f}\n", f16 ? "f16" : "bf16",
+               with_exp ? "+exp" : "", total_ms * 1e-3, 50 * flop / (ms * 1e-3) / 1e12);
         fflush(stdout);
     }
     CK(hipGetLastError());
@@ -174,8 +183,14 @@ int main(int argc, char** argv) {
     hipDeviceProp_t prop;
     CK(hipGetDeviceProperties(&prop, 0));
     const int cus = prop.multiProcessorCount;
-    if (argc >= 3 && strcmp(argv[1], "mfma") == 0)
-        return mfma_loop(cus, atof(argv[2]), argc >= 4 && strcmp(argv[3], "exp") == 0);
+    if (argc >= 3 && strcmp(argv[1], "mfma") == 0) {
+        bool with_exp = false, f16 = false;
+        for (int i = 3; i < argc; ++i) {
+            with_exp |= strcmp(argv[i], "exp") == 0;
+            f16 |= strcmp(argv[i], "f16") == 0;
+        }
+        return mfma_loop(cus, atof(argv[2]), with_exp, f16);
+    }
     const size_t bytes = (size_t)1 << 30, nvec = bytes / 16;
     u32x4 *a = nullptr, *b = nullptr;
     uint32_t* sink = nullptr;
@@ -209,14 +224,18 @@ int main(int argc, char** argv) {
     const int iters = 40000;
     const double flop = (double)cus * 8 * iters * 16 * (2.0 * 16 * 16 * 32);
     float* fout = (float*)(sink + 2048);
-    const float m0 = time_ms([&] { mfma_stream<false><<<cus, 512>>>(sink, iters, fout); }, 5);
-    const float m1 = time_ms([&] { mfma_stream<true><<<cus, 512>>>(sink, iters, fout); }, 5);
+    const float m0 = time_ms([&] { launch_mfma<bf16x8>(false, cus, sink, iters, fout); }, 5);
+    const float m1 = time_ms([&] { launch_mfma<bf16x8>(true, cus, sink, iters, fout); }, 5);
+    const float h0 = time_ms([&] { launch_mfma<f16x8>(false, cus, sink, iters, fout); }, 5);
+    const float h1 = time_ms([&] { launch_mfma<f16x8>(true, cus, sink, iters, fout); }, 5);
     CK(hipGetLastError());
     printf("{\"cus\": %d, \"read_nt_GBs\": %.1f, \"read_GBs\": %.1f, \"copy_nt_GBs\": %.1f, "
-           "\"mfma_bf16_TFLOPs\": %.1f, \"mfma_bf16_exp_TFLOPs\": %.1f, "
+           "\"mfma_bf16_TFLOPs\": %.1f, \"mfma_bf16_exp_TFLOPs\": %.1f, \"mfma_f16_TFLOPs\": %.1f, "
+           "\"mfma_f16_exp_TFLOPs\": %.1f, "
            "\"shapes\": {\"read_nt\": [%d, %d], \"read\": [%d, %d], \"copy_nt\": [%d, %d]}}\n",
            cus, bytes / (r_nt.ms * 1e-3) / 1e9, bytes / (r_df.ms * 1e-3) / 1e9, 2.0 * bytes / (c_nt.ms * 1e-3) / 1e9,
-           flop / (m0 * 1e-3) / 1e12, flop / (m1 * 1e-3) / 1e12, r_nt.grid, r_nt.u, r_df.grid, r_df.u, c_nt.grid,
+           flop / (m0 * 1e-3) / 1e12, flop / (m1 * 1e-3) / 1e12, flop / (h0 * 1e-3) / 1e12,
+           flop / (h1 * 1e-3) / 1e12, r_nt.grid, r_nt.u, r_df.grid, r_df.u, c_nt.grid,
            c_nt.u);
     CK(hipFree(a));
     CK(hipFree(b));
