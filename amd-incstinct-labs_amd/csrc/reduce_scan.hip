@@ -13,6 +13,7 @@
 //           at a time (one per lane) and writes the output. Every published word carries the
 //           call's epoch, so words left by earlier calls read as "not ready" and the flags need
 //           no clearing between calls. No LDS in either.
+#include <type_traits>
 #include "common.hpp"
 #include <atomic>
 #include <stdlib.h>
@@ -219,10 +220,29 @@ int reduce_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) 
 // 1 KiB of contiguous lines (16-byte loads of 8 values left each lane's 32-byte output as two
 // stores 32 bytes apart, and the half-filled lines were written twice).
 using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
-template <int DT> struct ScanElem : Elem<DT> { using Load = u32x4; };
+template <int DT> struct ScanElem : Elem<DT> {
+    using Load = u32x4;
+    // A vector of the op's identity, for the vectors past the end of the last tile.
+    template <class Op> __device__ static Load ident() {
+        using Acc = typename Elem<DT>::Acc;
+        Acc a[Elem<DT>::VEC];
+#pragma unroll
+        for (int e = 0; e < Elem<DT>::VEC; ++e) a[e] = Op::template identity<Acc>();
+        return __builtin_bit_cast(Load, a);
+    }
+};
 template <int DT> struct ScanElem16 : Elem<DT> {
     using Load = u32x2;
     static constexpr int VEC = 4;
+    // Four packed copies of the op's identity (0, -inf for max, +inf for min), for the vectors past
+    // the end of the last tile.
+    template <class Op> __device__ static Load ident() {
+        constexpr bool kBf = DT == CDNA4_BF16;
+        uint32_t h = 0u;
+        if constexpr (std::is_same<Op, wave::xlane::Max>::value) h = kBf ? 0xFF80u : 0xFC00u;
+        if constexpr (std::is_same<Op, wave::xlane::Min>::value) h = kBf ? 0x7F80u : 0x7C00u;
+        return Load{h | (h << 16), h | (h << 16)};
+    }
     __device__ static void unpack(const u32x2& v, float (&o)[4]) {
         const uint32_t w[2] = {v[0], v[1]};
         float x[8];
@@ -234,12 +254,12 @@ template <int DT> struct ScanElem16 : Elem<DT> {
 };
 template <> struct ScanElem<CDNA4_F16> : ScanElem16<CDNA4_F16> {};
 template <> struct ScanElem<CDNA4_BF16> : ScanElem16<CDNA4_BF16> {};
-// Tile = 64 lanes x U vectors per lane. The look-back costs about the same per tile whatever its
-// size, so tiles are as large as the register file allows at three waves per SIMD: 32 vectors
-// (128 values per lane, ~150 VGPRs) for every input type. Measured at 2^26: 24 / 36 / 40 vectors
-// for 32-bit inputs ran 3-8 % slower than 32, and 40 for 16-bit ones (two waves) 4-6 % slower.
-template <int DT> struct ScanTile { static constexpr int U = 32; };
-template <int DT, bool kVec> constexpr int scan_u() { return kVec ? ScanTile<DT>::U : ScanTile<DT>::U / 2; }
+// Tile = 64 lanes x U vectors per lane (scan_layout::scan_u). The look-back costs about the same
+// per tile whatever its size, so tiles are as large as the register file allows at three waves per
+// SIMD (~155 VGPRs with the tile held as loaded): 32 16-byte vectors for 32- and 64-bit inputs (24 /
+// 36 / 40 ran 3-8 % slower), 64 8-byte vectors of four 16-bit values (48: 83 us, 64: 77 us, 80 at
+// two waves: 87 us at 2^26; held as fp32 values they had fitted 32, 83 us).
+template <int DT, bool kVec> constexpr int scan_u() { return scan_layout::scan_u((int)sizeof(typename Elem<DT>::In), kVec); }
 
 // Per-group look-back state. A group publishes its aggregate into agg and, once known, its
 // inclusive prefix into pre. Every 64-bit word carries a tag in its upper half and 32 value bits
@@ -406,59 +426,102 @@ __global__ __launch_bounds__(64 * scan_layout::kScanWaves) void scan_tiles(const
 
     // Aligned calls (kVec): n counts the elements of whole VEC-element vectors only (the host
     // scans the remaining n % VEC elements in scan_tail). Every tile but the last is full and
-    // takes a straight-line path of vector loads at fixed offsets from one base, all issued
-    // before any arithmetic; the last tile guards each vector with a 32-bit tile-local index against the
+    // takes a straight-line path of vector loads at fixed offsets from one base, all issued before
+    // any arithmetic; the last tile guards each vector with a 32-bit tile-local index against the
     // uniform vector count. Misaligned calls go element by element.
+    // 16- and 64-bit inputs on the aligned path (kRaw) keep the tile in registers as loaded (16-bit
+    // values packed, two VGPRs per four) while only its total is formed, a fold per lane and one
+    // over the wave, so the group's aggregate goes out before the tile's scan is computed, after the
+    // look-back; past the end of the last tile the vectors hold the op's identity. Packed 16-bit
+    // tiles hold twice the elements of scanned fp32 ones (f16 82 -> 76.5 us at 2^26, bf16 84 -> 78;
+    // 64-bit 200 -> 198 us). 32-bit inputs hold the scanned values across the look-back instead,
+    // so the stores follow it at once (held as loaded: f32 101.1 -> 101.8 us, i32 100.9 -> 103.0).
     const typename E::In* tin = in + base;
     const bool full = live && kVec && scan_layout::tile_full(base, TILE, n);
     const uint32_t rem = live ? scan_layout::tile_rem(base, TILE, n) : 0u;  // elements (0: none)
-    Acc v[U][VEC];
-    if constexpr (kVec) {
-        const typename E::Load* src = (const typename E::Load*)tin + lane;
-        if (full) {
+    // Local inclusive scan of one vector of VEC values per lane: within the lane, then across the
+    // wave (DPP), carried on from `run`, the combined value of the tile's earlier vectors.
+    auto scan_vec = [&](Acc (&x)[VEC], Acc& run) {
 #pragma unroll
-            for (int j = 0; j < U; ++j) E::unpack(__builtin_nontemporal_load(src + j * 64), v[j]);
-            __builtin_amdgcn_sched_barrier(0);
-        } else {
-#pragma unroll
-            for (int j = 0; j < U; ++j) {
-                if (scan_layout::vec_live(false, j, lane, rem, VEC)) {
-                    E::unpack(__builtin_nontemporal_load(src + j * 64), v[j]);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < VEC; ++e) v[j][e] = id;
-                }
-            }
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < U; ++j)
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                const uint32_t i = scan_layout::elem_in_tile(j, lane, e, VEC);
-                v[j][e] = i < rem ? E::load1(tin + i) : id;
-            }
-    }
-    // Tile-local inclusive scan in registers.
-    Acc run = id;
-#pragma unroll
-    for (int j = 0; j < U; ++j) {
-#pragma unroll
-        for (int e = 1; e < VEC; ++e) v[j][e] = op(v[j][e - 1], v[j][e]);
+        for (int e = 1; e < VEC; ++e) x[e] = op(x[e - 1], x[e]);
         Acc carry;
-        const Acc inc = scan_with_carry(v[j][VEC - 1], op, carry);
+        const Acc inc = scan_with_carry(x[VEC - 1], op, carry);
         const Acc exc = dpp<kRowShr1>(carry, inc);          // lane's exclusive within chunk
         const Acc pre = op(run, exc);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) v[j][e] = op(pre, v[j][e]);
+        for (int e = 0; e < VEC; ++e) x[e] = op(pre, x[e]);
         run = op(run, wave::xlane::lane63(inc));             // chunk total, on every lane
+    };
+    constexpr bool kRaw = kVec && sizeof(typename E::In) != 4;
+    typename E::Load r[kRaw ? U : 1];   // kRaw: the tile as loaded
+    Acc v[kRaw ? 1 : U][VEC];           // otherwise: the tile's scanned values
+    Acc run = id;                       // the tile's total, on every lane
+    if constexpr (kRaw) {
+        const typename E::Load* src = (const typename E::Load*)tin + lane;
+        if (full) {
+#pragma unroll
+            for (int j = 0; j < U; ++j) r[j] = __builtin_nontemporal_load(src + j * 64);
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+#pragma unroll
+            for (int j = 0; j < U; ++j)
+                r[j] = scan_layout::vec_live(false, j, lane, rem, VEC) ? __builtin_nontemporal_load(src + j * 64)
+                                                                      : E::template ident<Op>();
+        }
+        // For a float sum this total can differ from the last value of the scan after the look-back
+        // by the rounding of the tile's total (a different order), which the next tiles then carry.
+        Acc part[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) part[e] = id;
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            Acc x[VEC];
+            E::unpack(r[j], x);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) part[e] = op(part[e], x[e]);
+        }
+#pragma unroll
+        for (int e = 1; e < VEC; ++e) part[0] = op(part[0], part[e]);
+        run = allreduce(part[0], op);
+        // The loaded tile, not this fold's values, is what stays live across the look-back.
+#pragma unroll
+        for (int j = 0; j < U; ++j) asm volatile("" : "+v"(r[j]));
+    } else {
+        if constexpr (kVec) {
+            const typename E::Load* src = (const typename E::Load*)tin + lane;
+            if (full) {
+#pragma unroll
+                for (int j = 0; j < U; ++j) E::unpack(__builtin_nontemporal_load(src + j * 64), v[j]);
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < U; ++j) {
+                    if (scan_layout::vec_live(false, j, lane, rem, VEC)) {
+                        E::unpack(__builtin_nontemporal_load(src + j * 64), v[j]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < VEC; ++e) v[j][e] = id;
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < U; ++j)
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    const uint32_t i = scan_layout::elem_in_tile(j, lane, e, VEC);
+                    v[j][e] = i < rem ? E::load1(tin + i) : id;
+                }
+        }
+#pragma unroll
+        for (int j = 0; j < U; ++j) scan_vec(v[j], run);
+        // Materialise the scanned values here: left alone, the compiler sinks the last addition of
+        // every element past the look-back loop and keeps two extra values per chunk live across it.
+#pragma unroll
+        for (int j = 0; j < U; ++j)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) asm volatile("" : "+v"(v[j][e]));
     }
-    // Materialise the scanned values here: left alone, the compiler sinks the last addition of
-    // every element past the look-back loop and keeps two extra values per chunk live across it.
-#pragma unroll
-    for (int j = 0; j < U; ++j)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) asm volatile("" : "+v"(v[j][e]));
     // Group combine: each wave's prefix within the group and the group total; wave 0 publishes
     // and runs the look-back (publish and look_back take the lane from threadIdx.x: wave 0 only).
     // The barriers order the exchange line's writes before its reads within the workgroup.
@@ -490,12 +553,21 @@ __global__ __launch_bounds__(64 * scan_layout::kScanWaves) void scan_tiles(const
     if constexpr (kVec) {
         constexpr int kWords = (int)(sizeof(Out) * VEC / 16);
         u32x4* dst = (u32x4*)tout + lane * kWords;
+        Acc run2 = id;
 #pragma unroll
         for (int j = 0; j < U; ++j) {
+            Acc x[VEC];
+            if constexpr (kRaw) {   // the tile's scan, vector by vector from the loaded tile
+                E::unpack(r[j], x);
+                scan_vec(x, run2);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) x[e] = v[j][e];
+            }
             if (scan_layout::vec_live(full, j, lane, rem, VEC)) {
                 Out o[VEC];
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) o[e] = (Out)op(excl, v[j][e]);
+                for (int e = 0; e < VEC; ++e) o[e] = (Out)op(excl, x[e]);
 #pragma unroll
                 for (int w = 0; w < kWords; ++w) {
                     u32x4 q;

@@ -12,7 +12,11 @@ namespace scan_layout {
 
 constexpr size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// A tile is 64 lanes x U vectors of VEC elements.
+// A tile is 64 lanes x U vectors of VEC elements. U on the aligned path: kScanU for 4- and 8-byte
+// inputs, twice that for 16-bit inputs (held packed, 8 bytes per vector); on the misaligned
+// (element-wise) path half of kScanU.
+constexpr int kScanU = 32;
+constexpr int scan_u(int in_bytes, bool vec, int base = kScanU) { return vec ? (in_bytes == 2 ? 2 * base : base) : base / 2; }
 constexpr size_t tile_elems(int vec, int u) { return (size_t)64 * vec * u; }
 constexpr size_t tiles_for(size_t n, int vec, int u) { return (n + tile_elems(vec, u) - 1) / tile_elems(vec, u); }
 

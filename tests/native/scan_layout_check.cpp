@@ -7,7 +7,8 @@
 // tile group publishes or reads during its look-back, the header words and the tail's reads, checking each against the sizes of the input, output and workspace buffers (the
 // workspace sized as cdna3_scan_workspace_size sizes it). Both the aligned (16-byte vector) and the
 // misaligned (element-wise, half-size tiles) paths are replayed.
-// Usage: scan_layout_check [--plant] U n [n ...]   (U = vectors per lane of the aligned path;
+// Usage: scan_layout_check [--plant] U n [n ...]   (U = vectors per lane of the aligned path for 4- and
+// 8-byte inputs, twice that for 16-bit ones, half of it on the misaligned path: scan_layout::scan_u;
 // prints "ok <checks>" or the first violation and exits 1). --plant replays a deliberately wrong
 // guard for the last tile (one vector more per lane than the tile holds) to show that the replay
 // catches such an overrun.
@@ -48,9 +49,9 @@ static bool g_plant = false;
 static void replay(const Type& T, int U, size_t n, size_t in_off) {
     const bool vec = in_off == 0;
     const int VEC = T.VEC;
-    const int u = vec ? U : U / 2;
-    // workspace as sized by cdna3_scan_workspace_size: the misaligned (half-size) tiles' count
-    const size_t ws_tiles = sl::tiles_for(n, VEC, U / 2);
+    const int u = sl::scan_u(T.in_bytes, vec, U);
+    // workspace as sized by cdna3_scan_workspace_size: the misaligned (smaller) tiles' count
+    const size_t ws_tiles = sl::tiles_for(n, VEC, sl::scan_u(T.in_bytes, false, U));
     const size_t ws = sl::ws_bytes(ws_tiles);
     const size_t n_main = sl::main_elems(n, vec, VEC);
     const size_t ntiles = sl::tiles_for(n_main, VEC, u);
