@@ -151,6 +151,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "cdna3_rmsnorm_f32": (c_int, [vp, vp, vp, c_int, c_int, c_float, vp]),
         "cdna3_layernorm_f32": (c_int, [vp, vp, vp, vp, c_int, c_int, c_float, vp]),
         "cdna4_gemm_f16_nt": (c_int, [vp, vp, vp, c_int, c_int, c_int, c_int, c_int, c_int, vp]),
+        "cdna4_gemm_f16_nt_tile": (c_int, [c_int, c_int, c_int, ctypes.POINTER(c_int), ctypes.POINTER(c_int)]),
         "cdna3_rope_f16": (c_int, [vp, vp, vp, c_int, c_int, c_int, vp]),
         "cdna3_rope_table_f32": (c_int, [vp, vp, c_int, c_int, c_int, c_float, vp]),
         "cdna3_scatter_kv_f16": (c_int, [vp, vp] + [c_int] * 5 + [vp]),
@@ -469,6 +470,13 @@ def gemm_f16_nt(X: torch.Tensor, W: torch.Tensor, out: Optional[torch.Tensor] = 
         _check(lib().cdna4_gemm_f16_nt(_ptr(Xc), _ptr(Wc), _ptr(out), int(out.dtype == torch.float32), int(accum), M,
                                        N, K, out.stride(0), _stream(stream)), "cdna4_gemm_f16_nt")
     return out
+
+
+def gemm_f16_nt_tile(M: int, N: int, K: int):
+    """(BM, BN): the tile (rows of X, rows of W per workgroup) gemm_f16_nt takes for a shape."""
+    bm, bn = ctypes.c_int(0), ctypes.c_int(0)
+    _check(lib().cdna4_gemm_f16_nt_tile(M, N, K, ctypes.byref(bm), ctypes.byref(bn)), "cdna4_gemm_f16_nt_tile")
+    return bm.value, bn.value
 
 
 def rope_f16(T: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, seq: int, heads: int, D: int,

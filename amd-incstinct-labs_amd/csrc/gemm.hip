@@ -6,16 +6,24 @@
 // the [out][in] weight as the model files hold it, beta 0 (Q|K|V, gate|up) or 1 (the O and down
 // projections added into the fp32 residual).
 //
-// MI355X design: at prompt lengths of a few hundred tokens these GEMMs are small (0.6-4.8 GFLOP)
-// and rocBLAS's choice for them ran at ~180 TFLOP/s. Here a workgroup of four waves computes a
-// BM x BN tile of Y^T = W X^T on v_mfma_f32_16x16x32_f16: W rows are the A operand and X rows the
-// B operand, so a lane's accumulator holds four consecutive columns n of one row m and leaves as
-// one 16-byte (fp32) or 8-byte (fp16) store. Each 64-wide K step of both operand tiles is copied
-// HBM -> registers -> LDS (16-byte loads, eight threads per 128-byte row), double-buffered: the
-// next step's loads are in flight while the MFMAs consume the current one. Rows past M or N read
-// the last valid row (their results are not stored). The tile is the largest of 128 x 128,
-// 64 x 128 and 64 x 64 (m x n) whose grid still covers the CUs.
-#include "common.hpp"
+// MI355X design: at prompt lengths of a few hundred tokens these GEMMs are small (0.6-4.8 GFLOP,
+// 2-10 MB of operands) and a launch is over in a few microseconds, so what sets the time is how
+// many workgroups the grid gives each CU and how many bytes each CU keeps in flight. The tile
+// (BM x BN, from a small menu) is chosen per shape so that the grid is about one round of one
+// workgroup per CU, and each workgroup streams 64-wide K stages of both operand tiles HBM -> LDS
+// with asynchronous copies (global_load_lds_dwordx4) into a ring of S stages, S - 1 ahead of the
+// stage being multiplied (S as deep as 128 KB of LDS allows, up to 8). Four waves compute Y^T =
+// W X^T on v_mfma_f32_16x16x32_f16: W rows are the A operand, X rows the B operand.
+//
+// LDS layout (the prefill's K tile at D = 64, whose reads were measured free of bank conflicts):
+// a stage holds BN rows of W then BM rows of X, 128 bytes per row; 16-byte chunk c of row r sits
+// at position c ^ swz_k<64>(r % 32). An operand block (16 rows) of 32-row group G is read in the
+// permuted row order 32 G + 8 (l / 4) + l % 4 + 4 u (A-row / B-column l, u = 0 or 1): the lanes
+// of one read then touch every bank once, and a lane's four accumulator values are four
+// consecutive output columns n (one 16-byte or 8-byte store). Wave (wm, wn) takes block u = wn of
+// every W group and u = wm of every X group of the tile. Rows past M or N read the last valid row
+// (their results are not stored).
+#include "attn_stream.hpp"
 
 namespace cdna4 {
 namespace {
@@ -24,73 +32,122 @@ typedef _Float16 gf16x8 __attribute__((ext_vector_type(8)));
 typedef float gf32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 gf16x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kKMul = 64;   // K must be a multiple of this (the smallest stage)
+constexpr int kBK = 64;        // K per stage (one 128-byte LDS row per operand row)
+constexpr int kKMul = kBK;     // K must be a multiple of this
+constexpr int kRowBytes = kBK * 2;
+constexpr int kLdsBudget = 128 * 1024;
 
-// KT: K per LDS stage (KT / 32 MFMA K steps); rows padded by 8 halves against bank conflicts.
-template <int BM, int BN, int KT, bool kF32Out, bool kAccum>
-__global__ __launch_bounds__(256) void gemm_f16_nt(const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
-                                                   void* __restrict__ Y, int M, int N, int K, int ldy) {
-    constexpr int FN = BN / 32, FM = BM / 32;   // 16-row MFMA blocks per wave (n, m)
-    constexpr int kLdsRow = KT + 8;
-    constexpr int kRowChunks = KT / 8;          // 16-byte chunks per row and stage
-    constexpr int CX = BM * kRowChunks / 256;   // 16-byte chunks per thread and stage (X)
-    constexpr int CW = BN * kRowChunks / 256;   // (W)
-    __shared__ __attribute__((aligned(16))) uint16_t xs[2][BM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) uint16_t ws[2][BN * kLdsRow];
-    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// Ring depth for a BM x BN tile: as many stages as kLdsBudget holds, at most 8.
+constexpr int ring_stages(int bm, int bn) {
+    const int s = kLdsBudget / ((bm + bn) * kRowBytes);
+    return s > 8 ? 8 : s;
+}
+
+// Wait until at most `younger` stages' copies (kPerStage each per wave) are still in flight.
+template <int kPerStage, int S>
+__device__ __forceinline__ void wait_stages(int younger) {
+    static_assert(S >= 2 && S <= 12 && (S - 2) * kPerStage <= 63, "ring depth within the vmcnt range");
+#define CDNA4_GEMM_WAIT(y) \
+    case y: asm volatile("s_waitcnt vmcnt(%0)" : : "n"((y) * kPerStage) : "memory"); break;
+    switch (younger) {
+        CDNA4_GEMM_WAIT(0) CDNA4_GEMM_WAIT(1) CDNA4_GEMM_WAIT(2) CDNA4_GEMM_WAIT(3)
+        CDNA4_GEMM_WAIT(4) CDNA4_GEMM_WAIT(5) CDNA4_GEMM_WAIT(6) CDNA4_GEMM_WAIT(7)
+        CDNA4_GEMM_WAIT(8) CDNA4_GEMM_WAIT(9) CDNA4_GEMM_WAIT(10)
+        default: asm volatile("s_waitcnt vmcnt(0)" : : : "memory"); break;
+    }
+#undef CDNA4_GEMM_WAIT
+}
+
+// Tile of workgroup b in a grid of tm x tn tiles (1-D). Workgroups go to the 8 XCDs round-robin
+// (XCD = b % 8); when tn is a multiple of 8, XCD x takes the n tiles x tn/8 .. (x+1) tn/8 - 1 with
+// every m tile (m fastest), so each W row is fetched into one XCD's L2 only and re-read there by
+// that XCD's tiles, and X (the smaller operand at prompt lengths) is what each XCD fetches whole.
+__device__ __forceinline__ void tile_of(int b, int tm, int tn, int& mt, int& nt) {
+    if ((tn & 7) == 0) {
+        const int x = b & 7, s = b >> 3;
+        mt = s % tm;
+        nt = x * (tn >> 3) + s / tm;
+    } else {
+        mt = b % tm;
+        nt = b / tm;
+    }
+}
+
+template <int BM, int BN, bool kF32Out, bool kAccum>
+__global__ __launch_bounds__(256) void gemm_ring(const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
+                                                 void* __restrict__ Y, int M, int N, int K, int ldy) {
+    static_assert(BM % 32 == 0 && BN % 32 == 0, "tiles are whole 32-row groups");
+    constexpr int S = ring_stages(BM, BN);
+    constexpr int FM = BM / 32, FN = BN / 32;        // 16-row blocks per wave: X (m), W (n)
+    constexpr int kStage = (BN + BM) * kRowBytes;    // bytes per ring stage
+    constexpr int kCopies = (BN + BM) / 8;           // 1 KB copy instructions per stage
+    constexpr int kCopiesW = kCopies / 4;            // per wave
+    static_assert(kCopies % 4 == 0, "copies split evenly over the four waves");
+    __shared__ __attribute__((aligned(16))) char lds[S * kStage];
+
+    const int lane = (int)(threadIdx.x & 63u);
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int li = lane & 15, g = lane >> 4;
     const int wm = wave & 1, wn = wave >> 1;
-    const int m0 = (int)blockIdx.x * BM, n0 = (int)blockIdx.y * BN;
+    int mt, nt;
+    tile_of((int)blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
 
-    // Loader: chunk c = tid + 256 j of a stage is row c / kRowChunks, 16-byte column c % kRowChunks.
-    u32x4 rx[CX], rw[CW];
-    auto gload = [&](int k0) {
+    // Copy j of this wave is instruction c = wave + 4 j of a stage: its lane l fills LDS row
+    // 8 c + l / 8 at chunk position l % 8 (1 KB of the stage at byte 1024 c) from global chunk
+    // (l % 8) ^ swz(row) of W row n0 + row (rows below BN) or X row m0 + row - BN; whether the
+    // instruction copies W or X is uniform over the wave.
+    uint32_t coff[kCopiesW];
+    bool cw[kCopiesW];
 #pragma unroll
-        for (int j = 0; j < CX; ++j) {
-            const int c = tid + 256 * j, r = min(m0 + c / kRowChunks, M - 1);
-            rx[j] = *(const u32x4*)(X + (size_t)r * K + k0 + (c % kRowChunks) * 8);
-        }
+    for (int j = 0; j < kCopiesW; ++j) {
+        const int c = wave + 4 * j;
+        const int row = c * 8 + (lane >> 3);
+        const int chunk = (lane & 7) ^ tile::swz_k<64>(row & 31);
+        cw[j] = c * 8 < BN;
+        const int r = cw[j] ? min(n0 + row, N - 1) : min(m0 + row - BN, M - 1);
+        coff[j] = (uint32_t)r * (uint32_t)K * 2u + (uint32_t)chunk * 16u;
+    }
+    auto issue = [&](int kt, int buf) {   // the copies of stage kt (k0 = 64 kt) into ring slot buf
+        const uint16_t* wk = W + (size_t)kt * kBK;
+        const uint16_t* xk = X + (size_t)kt * kBK;
 #pragma unroll
-        for (int j = 0; j < CW; ++j) {
-            const int c = tid + 256 * j, r = min(n0 + c / kRowChunks, N - 1);
-            rw[j] = *(const u32x4*)(W + (size_t)r * K + k0 + (c % kRowChunks) * 8);
-        }
+        for (int j = 0; j < kCopiesW; ++j)
+            stream::dma16_s(cw[j] ? wk : xk, coff[j], lds + buf * kStage + (wave + 4 * j) * 1024);
     };
-    auto lstore = [&](int st) {
-#pragma unroll
-        for (int j = 0; j < CX; ++j) {
-            const int c = tid + 256 * j;
-            *(u32x4*)(&xs[st][(c / kRowChunks) * kLdsRow + (c % kRowChunks) * 8]) = rx[j];
-        }
-#pragma unroll
-        for (int j = 0; j < CW; ++j) {
-            const int c = tid + 256 * j;
-            *(u32x4*)(&ws[st][(c / kRowChunks) * kLdsRow + (c % kRowChunks) * 8]) = rw[j];
-        }
-    };
+
+    // Operand reads: W block i (group i, u = wn), X block j (group j, u = wm); K step kc of a stage
+    // flips bit 6 (chunk c -> c + 4).
+    const int r0 = 8 * (li >> 2) + (li & 3);
+    const uint32_t rd = (uint32_t)(r0 * kRowBytes + ((g ^ tile::swz_k<64>(r0)) * 16));
+    const uint32_t rw = rd + (uint32_t)wn * 512u;
+    const uint32_t rx = (uint32_t)BN * kRowBytes + rd + (uint32_t)wm * 512u;
 
     gf32x4 acc[FN][FM];
 #pragma unroll
-    for (int a = 0; a < FN; ++a)
+    for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int b = 0; b < FM; ++b) acc[a][b] = gf32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < FM; ++j) acc[i][j] = gf32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int nk = K / KT;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    const int r16 = lane & 15, g8 = (lane >> 4) * 8;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int st = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * KT);
+    const int nk = K / kBK;
 #pragma unroll
-        for (int ks = 0; ks < KT; ks += 32) {
+    for (int st = 0; st < S - 1; ++st)
+        if (st < nk) issue(st, st);
+    for (int kt = 0; kt < nk; ++kt) {
+        // stage kt landed (this wave's copies; the barrier: every wave's), and every wave is past
+        // stage kt - 1, whose slot now receives stage kt + S - 1
+        wait_stages<kCopiesW, S>(min(S - 2, nk - 1 - kt));
+        __syncthreads();
+        if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+        const char* st = lds + (kt % S) * kStage;
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+            const uint32_t flip = (uint32_t)kc * 64u;
             u32x4 a[FN], b[FM];
 #pragma unroll
-            for (int i = 0; i < FN; ++i)
-                a[i] = *(const u32x4*)(&ws[st][(wn * (BN / 2) + i * 16 + r16) * kLdsRow + ks + g8]);
+            for (int i = 0; i < FN; ++i) a[i] = *(const u32x4*)(st + ((rw + (uint32_t)i * 4096u) ^ flip));
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
-                b[i] = *(const u32x4*)(&xs[st][(wm * (BM / 2) + i * 16 + r16) * kLdsRow + ks + g8]);
+            for (int j = 0; j < FM; ++j) b[j] = *(const u32x4*)(st + ((rx + (uint32_t)j * 4096u) ^ flip));
 #pragma unroll
             for (int i = 0; i < FN; ++i)
 #pragma unroll
@@ -99,18 +156,16 @@ __global__ __launch_bounds__(256) void gemm_f16_nt(const uint16_t* __restrict__ 
                                                                        __builtin_bit_cast(gf16x8, b[j]), acc[i][j], 0,
                                                                        0, 0);
         }
-        if (kt + 1 < nk) lstore(st ^ 1);
-        __syncthreads();
     }
 
-    // acc[i][j] lane l: Y[m][n .. n + 3], m = row r16 of X block j, n = 4 (l / 16) of W block i.
+    // acc[i][j] lane (li, g): Y[m][n .. n + 3], m = m0 + 32 j + r0 + 4 wm, n = n0 + 32 i + 8 g + 4 wn.
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
-        const int m = m0 + wm * (BM / 2) + j * 16 + r16;
+        const int m = m0 + 32 * j + r0 + 4 * wm;
         if (m >= M) continue;
 #pragma unroll
         for (int i = 0; i < FN; ++i) {
-            const int n = n0 + wn * (BN / 2) + i * 16 + (lane >> 4) * 4;
+            const int n = n0 + 32 * i + 8 * g + 4 * wn;
             if (n >= N) continue;
             gf32x4 v = acc[i][j];
             if constexpr (kF32Out) {
@@ -129,46 +184,80 @@ __global__ __launch_bounds__(256) void gemm_f16_nt(const uint16_t* __restrict__ 
     }
 }
 
-template <int BM, int BN, int KT>
+template <int BM, int BN>
 int gemm_launch(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, bool accum, int M, int N, int K, int ldy,
                 hipStream_t s) {
-    const dim3 grid((unsigned)ceil_div((size_t)M, BM), (unsigned)ceil_div((size_t)N, BN));
+    const unsigned grid = ceil_div((size_t)M, BM) * ceil_div((size_t)N, BN);
     if (y_f32) {
-        if (accum) gemm_f16_nt<BM, BN, KT, true, true><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
-        else gemm_f16_nt<BM, BN, KT, true, false><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
+        if (accum) gemm_ring<BM, BN, true, true><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
+        else gemm_ring<BM, BN, true, false><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
     } else {
-        if (accum) gemm_f16_nt<BM, BN, KT, false, true><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
-        else gemm_f16_nt<BM, BN, KT, false, false><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
+        if (accum) gemm_ring<BM, BN, false, true><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
+        else gemm_ring<BM, BN, false, false><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
     }
     return launch_status();
+}
+
+// The tile menu, and the estimate the dispatcher ranks it by: rounds of workgroups over the CUs
+// (two workgroups per CU when the ring leaves room for a second in the 160 KB of LDS) times one
+// workgroup's time: a fixed cost per K stage (the copy round trip the ring does not hide) plus its
+// operand bytes at a per-CU stream rate and its MFMA work at a per-CU matrix rate. Calibrated on
+// the cfg5 prompt shapes, where it picks the fastest tile of the menu measured on the box (Q|K|V
+// 64 x 96: 7.7 us; O 32 x 32: 5.7; gate|up 128 x 96: 11.5; down 32 x 32: 13.6, event-timed).
+struct Tile { int bm, bn; };
+constexpr Tile kTiles[] = {{32, 32}, {64, 64}, {64, 96}, {64, 128}, {128, 64}, {128, 96}, {128, 128}};
+constexpr double kStageUs = 0.1;           // per 64-wide K stage
+constexpr double kCuBytesPerUs = 2.0e5;    // ~200 GB/s of operand tiles per CU
+constexpr double kCuFlopsPerUs = 8.0e6;    // ~8 TFLOP/s of fp16 MFMA per CU
+
+Tile pick_tile(int M, int N, int K, int cus) {
+    Tile best = kTiles[0];
+    double best_t = 1e300;
+    for (const Tile& t : kTiles) {
+        const int lds = ring_stages(t.bm, t.bn) * (t.bm + t.bn) * kRowBytes;
+        const int per_cu = (160 * 1024) / lds >= 2 ? 2 : 1;
+        const double tiles = (double)ceil_div((size_t)M, t.bm) * ceil_div((size_t)N, t.bn);
+        const double rounds = ceil(tiles / ((double)cus * per_cu));
+        const double wg = (double)(K / kBK) * kStageUs + (double)(t.bm + t.bn) * K * 2 / kCuBytesPerUs +
+                          2.0 * t.bm * t.bn * K / kCuFlopsPerUs;
+        const double est = rounds * wg;
+        if (est < best_t) {
+            best_t = est;
+            best = t;
+        }
+    }
+    return best;
 }
 
 }  // namespace
 
 // Returns -1, launching nothing, for a shape this kernel does not take (K not a multiple of 64,
-// N or ldy not a multiple of 4, X / W not 16-byte or Y not 16- (fp32) / 8-byte (fp16) aligned);
-// the caller then uses rocBLAS. Otherwise 0 or the launch's error.
+// N or ldy not a multiple of 4, X / W not 16-byte or Y not 16- (fp32) / 8-byte (fp16) aligned,
+// operands past 4 GiB); the caller then uses rocBLAS. Otherwise 0 or the launch's error.
 int llm_gemm_f16(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, bool accum, int M, int N, int K, int ldy,
                  hipStream_t s) {
     if (M <= 0 || N <= 0 || K <= 0 || K % kKMul || N % 4 || ldy % 4 || ldy < N) return -1;
     if (((uintptr_t)X | (uintptr_t)W) % 16 || (uintptr_t)Y % (y_f32 ? 16 : 8)) return -1;
-    const size_t cus = (size_t)(device_cus() > 0 ? device_cus() : 256);
-    auto tiles = [&](size_t bm, size_t bn) { return ceil_div((size_t)M, bm) * ceil_div((size_t)N, bn); };
-    // the deepest stage (fewest exposed memory round trips) that divides K and fits the LDS
-    if (tiles(128, 128) >= cus) {
-        if (K % 128 == 0) return gemm_launch<128, 128, 128>(X, W, Y, y_f32, accum, M, N, K, ldy, s);
-        return gemm_launch<128, 128, 64>(X, W, Y, y_f32, accum, M, N, K, ldy, s);
-    }
-    if (tiles(64, 128) >= cus) {
-        if (K % 128 == 0) return gemm_launch<64, 128, 128>(X, W, Y, y_f32, accum, M, N, K, ldy, s);
-        return gemm_launch<64, 128, 64>(X, W, Y, y_f32, accum, M, N, K, ldy, s);
-    }
-    if (K % 256 == 0) return gemm_launch<64, 64, 256>(X, W, Y, y_f32, accum, M, N, K, ldy, s);
-    if (K % 128 == 0) return gemm_launch<64, 64, 128>(X, W, Y, y_f32, accum, M, N, K, ldy, s);
-    return gemm_launch<64, 64, 64>(X, W, Y, y_f32, accum, M, N, K, ldy, s);
+    if ((uint64_t)M * K * 2 >= (1ull << 32) || (uint64_t)N * K * 2 >= (1ull << 32)) return -1;   // 32-bit copy offsets
+    const int cus = device_cus() > 0 ? device_cus() : 256;
+    const Tile t = pick_tile(M, N, K, cus);
+#define CDNA4_GEMM_TILE(a, b) \
+    if (t.bm == a && t.bn == b) return gemm_launch<a, b>(X, W, Y, y_f32, accum, M, N, K, ldy, s);
+    CDNA4_GEMM_TILE(32, 32) CDNA4_GEMM_TILE(64, 64) CDNA4_GEMM_TILE(64, 96) CDNA4_GEMM_TILE(64, 128)
+    CDNA4_GEMM_TILE(128, 64) CDNA4_GEMM_TILE(128, 96) CDNA4_GEMM_TILE(128, 128)
+#undef CDNA4_GEMM_TILE
+    return -1;
 }
 
 }  // namespace cdna4
+
+extern "C" int cdna4_gemm_f16_nt_tile(int M, int N, int K, int* bm, int* bn) {
+    if (M <= 0 || N <= 0 || K <= 0 || !bm || !bn) return CDNA4_ERR_INVALID_VALUE;
+    const cdna4::Tile t = cdna4::pick_tile(M, N, K, cdna4::device_cus() > 0 ? cdna4::device_cus() : 256);
+    *bm = t.bm;
+    *bn = t.bn;
+    return 0;
+}
 
 extern "C" int cdna4_gemm_f16_nt(const void* X, const void* W, void* Y, int y_f32, int accum, int M, int N, int K,
                                  int ldy, cdna4_stream_t stream) {

@@ -24,8 +24,8 @@
 //     index live in a device step state that the kernels read and the argmax advances, so one
 //     graph serves every step with the same attention plan (re-captured when the plan changes
 //     with the cache length). CDNA4_SESSION_GRAPH=0 launches the same kernels one by one.
-//   * The prompt's Q|K|V GEMM runs on the library's own MFMA GEMM (gemm.hip) when its shape
-//     allows, the other prompt GEMMs on rocBLAS; CDNA4_SESSION_ROCBLAS=1 sends all to rocBLAS.
+//   * The prompt's GEMMs run on the library's own MFMA GEMM (gemm.hip) when their shapes
+//     allow, otherwise on rocBLAS; CDNA4_SESSION_ROCBLAS=1 sends all to rocBLAS.
 #include "common.hpp"
 #include <rocblas/rocblas.h>
 #include <math.h>
@@ -312,14 +312,14 @@ int Session::reserve(int T) {
 // accumulation, fp32 or fp16 Y. rocBLAS is column-major: row-major Y is column-major Y^T [N][M],
 // and Y^T = W X^T, where the row-major W [N][K] read column-major is W^T (so op(A) = transpose,
 // lda = K) and the row-major X [M][K] read column-major is X^T (op(B) = none, ldb = K). The
-// reference derives the same call (rocblas_gemm.hpp:8-20). The library's MFMA GEMM takes the
-// fp16-output product (Q|K|V) when its shape allows: at the cfg5 prompt (T 512) it ran 13.5 us
-// against rocBLAS's 16.8; on the fp32-output products (O, gate|up, down) rocBLAS was faster
-// (gate|up 14.9 against 17.7-23.5 us, down 11.6 against 20.7), so those stay on rocBLAS.
+// reference derives the same call (rocblas_gemm.hpp:8-20). The library's MFMA GEMM (gemm.hip)
+// takes every product whose shape it allows; at the cfg5 prompt (T 512, under the kernel trace)
+// it measured Q|K|V 8.3 us, O ~5, gate|up 12.4, down 13.7 against rocBLAS's 16.8, 10.5, 14.8 and
+// 16.5. rocBLAS serves the rest (and everything with CDNA4_SESSION_ROCBLAS=1).
 int Session::gemm(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, float beta, int M, int N, int K,
                   int ldy) {
-    if (!rocblas_only && !y_f32 && beta == 0.f) {
-        const int e = llm_gemm_f16(X, W, Y, false, false, M, N, K, ldy, stream);
+    if (!rocblas_only && (beta == 0.f || beta == 1.f)) {
+        const int e = llm_gemm_f16(X, W, Y, y_f32, beta == 1.f, M, N, K, ldy, stream);
         if (e != -1) return e;   // -1: a shape the kernel does not take
     }
     const float alpha = 1.f;

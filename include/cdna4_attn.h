@@ -262,6 +262,9 @@ int cdna3_rope_table_f32(float* cos_tab, float* sin_tab, int pos0, int T, int D,
  */
 int cdna4_gemm_f16_nt(const void* X, const void* W, void* Y, int y_f32, int accum, int M, int N,
                       int K, int ldy, cdna4_stream_t stream);
+/* The BM x BN tile (rows of X x rows of W per workgroup) cdna4_gemm_f16_nt takes for a shape on
+ * the current device (no counterpart in the reference: tests use it to cover every tile). */
+int cdna4_gemm_f16_nt_tile(int M, int N, int K, int* bm, int* bn);
 
 /*
  * KV cache and layout kernels of the runtime layer loop (all fp16, device pointers).

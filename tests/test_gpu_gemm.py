@@ -1,7 +1,8 @@
 """The runtime's prompt GEMM (cdna4_gemm_f16_nt) on gfx950 against a PyTorch fp32 product of the
 same fp16 operands: the session's four prompt shapes at cfg5 (Q|K|V, O, gate|up, down), ragged M
-and N, each tile size the dispatcher picks, fp16 output, accumulation into Y, and the shapes the
-kernel refuses (the session then uses rocBLAS)."""
+and N, every tile of the dispatcher's menu (checked with cdna4_gemm_f16_nt_tile), rings shorter
+and longer than the K loop, fp16 output, accumulation into Y, and the shapes the kernel refuses
+(the session then uses rocBLAS)."""
 import pytest
 import torch
 
@@ -18,20 +19,26 @@ def _operands(M, N, K, seed):
     return X, W
 
 
-@pytest.mark.parametrize("M,N,K,out_dtype,accum", [
-    (512, 2304, 768, torch.float16, False),   # Q|K|V, cfg5
-    (512, 768, 768, torch.float32, True),     # O projection into the residual
-    (512, 6144, 768, torch.float32, False),   # gate|up
-    (512, 768, 3072, torch.float32, True),    # down projection into the residual
-    (4096, 4096, 256, torch.float32, False),  # 128 x 128 tiles, 128-wide K stages
-    (2048, 2048, 192, torch.float32, True),   # 128 x 128 tiles, 64-wide K stages
-    (512, 6144, 320, torch.float16, False),   # 64 x 128 tiles, 64-wide K stages
-    (37, 100, 64, torch.float32, False),      # ragged M and N, one K step
-    (1, 4, 128, torch.float16, True),
-    (129, 260, 192, torch.float32, True),
-    (300, 1000, 640, torch.float16, False),
+@pytest.mark.parametrize("M,N,K,out_dtype,accum,tile", [
+    (512, 2304, 768, torch.float16, False, (64, 96)),    # Q|K|V, cfg5
+    (512, 768, 768, torch.float32, True, (32, 32)),      # O projection into the residual
+    (512, 6144, 768, torch.float32, False, (128, 96)),   # gate|up
+    (512, 768, 3072, torch.float32, True, (32, 32)),     # down projection into the residual
+    (37, 100, 64, torch.float32, False, (32, 32)),       # ragged M and N, one K stage
+    (1, 4, 128, torch.float16, True, (32, 32)),
+    (129, 260, 192, torch.float32, True, (32, 32)),
+    (300, 1000, 640, torch.float16, False, (32, 32)),
+    (100, 6144, 64, torch.float32, True, (64, 64)),
+    (300, 6144, 64, torch.float16, False, (64, 128)),
+    (4128, 448, 64, torch.float16, True, (128, 64)),
+    (640, 6144, 64, torch.float32, False, (128, 128)),
+    (4096, 4096, 256, torch.float32, False, (128, 128)),  # several rounds of workgroups
+    (200, 6144, 960, torch.float16, False, (64, 96)),     # 15 stages through a 6-deep ring
 ])
-def test_gemm_against_torch_fp32(M, N, K, out_dtype, accum):
+def test_gemm_against_torch_fp32(M, N, K, out_dtype, accum, tile):
+    # the tile the dispatcher takes on a 256-CU part (a part with another CU count may pick another)
+    if torch.cuda.get_device_properties(DEV).multi_processor_count == 256:
+        assert cdna4.gemm_f16_nt_tile(M, N, K) == tile
     X, W = _operands(M, N, K, M * 31 + N * 7 + K)
     ref = X.float() @ W.float().t()
     Y0 = torch.randn(M, N, device=DEV).to(out_dtype) if accum else None

@@ -82,15 +82,19 @@ def test_config_read_from_meta(model):
     assert abs(c["norm_eps"] - (1e-5 if c["layernorm"] else 1e-6)) < 1e-9
 
 
+@pytest.mark.parametrize("gemm", ["library", "rocblas"])
 @pytest.mark.parametrize("n", [1, 5, 64, 100])
-def test_prefill_logits_match_oracle(model, n):
+def test_prefill_logits_match_oracle(model, monkeypatch, n, gemm):
+    # the prompt GEMMs on the library's MFMA GEMM (the default) or all on rocBLAS
     d, meta, t = model
+    if gemm == "rocblas":
+        monkeypatch.setenv("CDNA4_SESSION_ROCBLAS", "1")
     ids = _prompt(meta, n, n)
     with cdna4.Session(d, max_seq=128) as s:
         got = s.prefill_logits(ids)
     ref = oracle.LLM(meta, t, 128).forward(ids)
     err = _row_err(got, ref)
-    print(f"  prompt {n}: max |logit - oracle| / scale = {err:.2e}", flush=True)
+    print(f"  prompt {n} ({gemm} GEMMs): max |logit - oracle| / scale = {err:.2e}", flush=True)
     parity_log.record(err, LOGIT_TOL, "logit")
     assert err < LOGIT_TOL, err
 

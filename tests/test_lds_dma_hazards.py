@@ -19,7 +19,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "amd-incstinct-labs_amd")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["prefill.hip", "decode.hip"]
+SOURCES = ["prefill.hip", "decode.hip", "gemm.hip"]
 
 
 def _flags(src):
