@@ -152,6 +152,8 @@ def _declare(l: ctypes.CDLL) -> None:
         "cdna3_layernorm_f32": (c_int, [vp, vp, vp, vp, c_int, c_int, c_float, vp]),
         "cdna4_gemm_f16_nt": (c_int, [vp, vp, vp, c_int, c_int, c_int, c_int, c_int, c_int, vp]),
         "cdna4_gemm_f16_nt_tile": (c_int, [c_int, c_int, c_int, ctypes.POINTER(c_int), ctypes.POINTER(c_int)]),
+        "cdna4_gemm_f16_nt_silu": (c_int, [vp, vp, vp, c_int, c_int, c_int, c_int, vp]),
+        "cdna4_gemm_f16_nt_silu_tile": (c_int, [c_int, c_int, c_int, ctypes.POINTER(c_int), ctypes.POINTER(c_int)]),
         "cdna3_rope_f16": (c_int, [vp, vp, vp, c_int, c_int, c_int, vp]),
         "cdna3_rope_table_f32": (c_int, [vp, vp, c_int, c_int, c_int, c_float, vp]),
         "cdna3_scatter_kv_f16": (c_int, [vp, vp] + [c_int] * 5 + [vp]),
@@ -470,6 +472,35 @@ def gemm_f16_nt(X: torch.Tensor, W: torch.Tensor, out: Optional[torch.Tensor] = 
         _check(lib().cdna4_gemm_f16_nt(_ptr(Xc), _ptr(Wc), _ptr(out), int(out.dtype == torch.float32), int(accum), M,
                                        N, K, out.stride(0), _stream(stream)), "cdna4_gemm_f16_nt")
     return out
+
+
+def gemm_f16_nt_silu(X: torch.Tensor, W: torch.Tensor, out: Optional[torch.Tensor] = None,
+                     stream=None) -> torch.Tensor:
+    """Y = fp16(silu(X Wg^T) * (X Wu^T)), W = [Wg; Wu] fp16 [2F][K], X fp16 [M][K], Y fp16 [M][F]
+    (the SwiGLU gate|up product and the SiLU product in one launch; raises for the shapes it does
+    not take)."""
+    _dev(X, W)
+    M, K = X.shape
+    if W.shape[0] % 2 or W.shape[1] != K or X.dtype != torch.float16 or W.dtype != torch.float16:
+        raise ValueError("gemm_f16_nt_silu: X [M][K] and W [2F][K] fp16")
+    F = W.shape[0] // 2
+    if out is not None and (out.dtype != torch.float16 or tuple(out.shape) != (M, F) or out.stride(1) != 1):
+        raise ValueError("gemm_f16_nt_silu: out fp16 [M][F], rows contiguous")
+    with _on_stream(stream):
+        if out is None:
+            out = torch.empty(M, F, device=X.device, dtype=torch.float16)
+        Xc, Wc = X.contiguous(), W.contiguous()
+        _check(lib().cdna4_gemm_f16_nt_silu(_ptr(Xc), _ptr(Wc), _ptr(out), M, F, K, out.stride(0), _stream(stream)),
+               "cdna4_gemm_f16_nt_silu")
+    return out
+
+
+def gemm_f16_nt_silu_tile(M: int, F: int, K: int):
+    """(BM, BN): the tile gemm_f16_nt_silu takes (BN counts the gate and up rows together)."""
+    bm, bn = ctypes.c_int(0), ctypes.c_int(0)
+    _check(lib().cdna4_gemm_f16_nt_silu_tile(M, F, K, ctypes.byref(bm), ctypes.byref(bn)),
+           "cdna4_gemm_f16_nt_silu_tile")
+    return bm.value, bn.value
 
 
 def gemm_f16_nt_tile(M: int, N: int, K: int):

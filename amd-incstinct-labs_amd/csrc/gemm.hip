@@ -31,6 +31,7 @@ namespace {
 typedef _Float16 gf16x8 __attribute__((ext_vector_type(8)));
 typedef float gf32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 gf16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBK = 64;        // K per stage (one 128-byte LDS row per operand row)
 constexpr int kKMul = kBK;     // K must be a multiple of this
@@ -73,10 +74,21 @@ __device__ __forceinline__ void tile_of(int b, int tm, int tn, int& mt, int& nt)
     }
 }
 
-template <int BM, int BN, bool kF32Out, bool kAccum>
+// Output forms: fp16 or fp32 Y (Y = X W^T, + Y with kAccum), or the SiLU-gated product of the
+// SwiGLU MLP (kSilu): W holds 2F rows, gate rows 0 .. F - 1 then up rows F .. 2F - 1, and Y [M][F]
+// fp16 = fp16(silu(X Wg^T) * (X Wu^T)) in fp32, the rounding the separate silu_mul kernel applies
+// to the fp32 product. A kSilu tile of BN rows takes BN / 2 gate rows and the BN / 2 up rows of the
+// same output columns, so a lane holds both values of its columns.
+enum { kOutF16 = 0, kOutF32 = 1, kOutSilu = 2 };
+
+template <int BM, int BN, int kOut, bool kAccum>
 __global__ __launch_bounds__(256) void gemm_ring(const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
                                                  void* __restrict__ Y, int M, int N, int K, int ldy) {
     static_assert(BM % 32 == 0 && BN % 32 == 0, "tiles are whole 32-row groups");
+    static_assert(kOut != kOutSilu || (BN % 64 == 0 && !kAccum), "a SiLU tile pairs whole gate and up groups");
+    constexpr bool kSilu = kOut == kOutSilu;
+    constexpr int kTileCols = kSilu ? BN / 2 : BN;   // output columns per tile
+    const int ncols = kSilu ? N / 2 : N;              // output columns (F for kSilu)
     constexpr int S = ring_stages(BM, BN);
     constexpr int FM = BM / 32, FN = BN / 32;        // 16-row blocks per wave: X (m), W (n)
     constexpr int kStage = (BN + BM) * kRowBytes;    // bytes per ring stage
@@ -90,8 +102,8 @@ __global__ __launch_bounds__(256) void gemm_ring(const uint16_t* __restrict__ X,
     const int li = lane & 15, g = lane >> 4;
     const int wm = wave & 1, wn = wave >> 1;
     int mt, nt;
-    tile_of((int)blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, mt, nt);
-    const int m0 = mt * BM, n0 = nt * BN;
+    tile_of((int)blockIdx.x, (M + BM - 1) / BM, (ncols + kTileCols - 1) / kTileCols, mt, nt);
+    const int m0 = mt * BM, n0 = nt * kTileCols;
 
     // Copy j of this wave is instruction c = wave + 4 j of a stage: its lane l fills LDS row
     // 8 c + l / 8 at chunk position l % 8 (1 KB of the stage at byte 1024 c) from global chunk
@@ -105,7 +117,10 @@ __global__ __launch_bounds__(256) void gemm_ring(const uint16_t* __restrict__ X,
         const int row = c * 8 + (lane >> 3);
         const int chunk = (lane & 7) ^ tile::swz_k<64>(row & 31);
         cw[j] = c * 8 < BN;
-        const int r = cw[j] ? min(n0 + row, N - 1) : min(m0 + row - BN, M - 1);
+        int r;
+        if (!cw[j]) r = min(m0 + row - BN, M - 1);
+        else if (kSilu) r = row < BN / 2 ? min(n0 + row, ncols - 1) : ncols + min(n0 + row - BN / 2, ncols - 1);
+        else r = min(n0 + row, N - 1);
         coff[j] = (uint32_t)r * (uint32_t)K * 2u + (uint32_t)chunk * 16u;
     }
     auto issue = [&](int kt, int buf) {   // the copies of stage kt (k0 = 64 kt) into ring slot buf
@@ -158,17 +173,24 @@ __global__ __launch_bounds__(256) void gemm_ring(const uint16_t* __restrict__ X,
         }
     }
 
-    // acc[i][j] lane (li, g): Y[m][n .. n + 3], m = m0 + 32 j + r0 + 4 wm, n = n0 + 32 i + 8 g + 4 wn.
+    // acc[i][j] lane (li, g): Y[m][n .. n + 3], m = m0 + 32 j + r0 + 4 wm, n = n0 + 32 i + 8 g + 4 wn
+    // (kSilu: gate group i < FN / 2 and up group i + FN / 2 hold the same columns n).
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
         const int m = m0 + 32 * j + r0 + 4 * wm;
         if (m >= M) continue;
 #pragma unroll
-        for (int i = 0; i < FN; ++i) {
+        for (int i = 0; i < (kSilu ? FN / 2 : FN); ++i) {
             const int n = n0 + 32 * i + 8 * g + 4 * wn;
-            if (n >= N) continue;
+            if (n >= ncols) continue;
             gf32x4 v = acc[i][j];
-            if constexpr (kF32Out) {
+            if constexpr (kSilu) {
+                const gf32x4 u = acc[i + FN / 2][j];
+                uint32_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) h[e] = f32_to_f16_bits(v[e] / (1.f + expf(-v[e])) * u[e]);
+                *(u32x2*)((uint16_t*)Y + (size_t)m * ldy + n) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+            } else if constexpr (kOut == kOutF32) {
                 float* y = (float*)Y + (size_t)m * ldy + n;
                 if constexpr (kAccum) v += *(const gf32x4*)y;
                 *(gf32x4*)y = v;
@@ -189,12 +211,19 @@ int gemm_launch(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, bool 
                 hipStream_t s) {
     const unsigned grid = ceil_div((size_t)M, BM) * ceil_div((size_t)N, BN);
     if (y_f32) {
-        if (accum) gemm_ring<BM, BN, true, true><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
-        else gemm_ring<BM, BN, true, false><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
+        if (accum) gemm_ring<BM, BN, kOutF32, true><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
+        else gemm_ring<BM, BN, kOutF32, false><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
     } else {
-        if (accum) gemm_ring<BM, BN, false, true><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
-        else gemm_ring<BM, BN, false, false><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
+        if (accum) gemm_ring<BM, BN, kOutF16, true><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
+        else gemm_ring<BM, BN, kOutF16, false><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
     }
+    return launch_status();
+}
+
+template <int BM, int BN>
+int gemm_silu_launch(const uint16_t* X, const uint16_t* W, void* Y, int M, int F, int K, int ldy, hipStream_t s) {
+    const unsigned grid = ceil_div((size_t)M, BM) * ceil_div((size_t)F, BN / 2);
+    gemm_ring<BM, BN, kOutSilu, false><<<grid, 256, 0, s>>>(X, W, Y, M, 2 * F, K, ldy);
     return launch_status();
 }
 
@@ -210,10 +239,11 @@ constexpr double kStageUs = 0.1;           // per 64-wide K stage
 constexpr double kCuBytesPerUs = 2.0e5;    // ~200 GB/s of operand tiles per CU
 constexpr double kCuFlopsPerUs = 8.0e6;    // ~8 TFLOP/s of fp16 MFMA per CU
 
-Tile pick_tile(int M, int N, int K, int cus) {
-    Tile best = kTiles[0];
+Tile pick_tile(int M, int N, int K, int cus, bool silu = false) {
+    Tile best = {0, 0};
     double best_t = 1e300;
     for (const Tile& t : kTiles) {
+        if (silu && t.bn % 64) continue;   // a SiLU tile pairs whole gate and up groups
         const int lds = ring_stages(t.bm, t.bn) * (t.bm + t.bn) * kRowBytes;
         const int per_cu = (160 * 1024) / lds >= 2 ? 2 : 1;
         const double tiles = (double)ceil_div((size_t)M, t.bm) * ceil_div((size_t)N, t.bn);
@@ -249,7 +279,40 @@ int llm_gemm_f16(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, bool
     return -1;
 }
 
+// Y[M][F] fp16 = fp16(silu(X Wg^T) * (X Wu^T)), W = [Wg; Wu] fp16 [2F][K] (the SwiGLU gate|up
+// product followed by the SiLU product in one launch). Returns -1, launching nothing, for a shape
+// the kernel does not take (as llm_gemm_f16; F a multiple of 4, Y 8-byte aligned).
+int llm_gemm_f16_silu(const uint16_t* X, const uint16_t* W, void* Y, int M, int F, int K, int ldy, hipStream_t s) {
+    if (M <= 0 || F <= 0 || K <= 0 || K % kKMul || F % 4 || ldy % 4 || ldy < F) return -1;
+    if (((uintptr_t)X | (uintptr_t)W) % 16 || (uintptr_t)Y % 8) return -1;
+    if ((uint64_t)M * K * 2 >= (1ull << 32) || (uint64_t)2 * F * K * 2 >= (1ull << 32)) return -1;
+    const Tile t = pick_tile(M, 2 * F, K, device_cus() > 0 ? device_cus() : 256, true);
+#define CDNA4_GEMM_TILE(a, b) \
+    if (t.bm == a && t.bn == b) return gemm_silu_launch<a, b>(X, W, Y, M, F, K, ldy, s);
+    CDNA4_GEMM_TILE(64, 64) CDNA4_GEMM_TILE(64, 128) CDNA4_GEMM_TILE(128, 64) CDNA4_GEMM_TILE(128, 128)
+#undef CDNA4_GEMM_TILE
+    return -1;
+}
+
 }  // namespace cdna4
+
+extern "C" int cdna4_gemm_f16_nt_silu(const void* X, const void* W, void* Y, int M, int F, int K, int ldy,
+                                      cdna4_stream_t stream) {
+    if (M < 0 || F < 0 || K < 0) return CDNA4_ERR_INVALID_VALUE;
+    if (M == 0 || F == 0) return 0;
+    if (!X || !W || !Y) return CDNA4_ERR_INVALID_VALUE;
+    if (int e = cdna4::check_device()) return e;
+    const int e = cdna4::llm_gemm_f16_silu((const uint16_t*)X, (const uint16_t*)W, Y, M, F, K, ldy, (hipStream_t)stream);
+    return e == -1 ? CDNA4_ERR_INVALID_VALUE : e;
+}
+
+extern "C" int cdna4_gemm_f16_nt_silu_tile(int M, int F, int K, int* bm, int* bn) {
+    if (M <= 0 || F <= 0 || K <= 0 || !bm || !bn) return CDNA4_ERR_INVALID_VALUE;
+    const cdna4::Tile t = cdna4::pick_tile(M, 2 * F, K, cdna4::device_cus() > 0 ? cdna4::device_cus() : 256, true);
+    *bm = t.bm;
+    *bn = t.bn;
+    return 0;
+}
 
 extern "C" int cdna4_gemm_f16_nt_tile(int M, int N, int K, int* bm, int* bn) {
     if (M <= 0 || N <= 0 || K <= 0 || !bm || !bn) return CDNA4_ERR_INVALID_VALUE;

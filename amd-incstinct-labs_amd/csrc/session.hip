@@ -61,6 +61,7 @@ int attn_decode_replayable(const void* q, const void* K, const void* V, void* o,
 int llm_silu_mul(const float* gu, void* act, int T, int F, hipStream_t s);
 int llm_gemm_f16(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, bool accum, int M, int N, int K, int ldy,
                  hipStream_t s);
+int llm_gemm_f16_silu(const uint16_t* X, const uint16_t* W, void* Y, int M, int F, int K, int ldy, hipStream_t s);
 int llm_bias_add_f16(void* Y, const void* b, int T, int N, hipStream_t s);
 int kv_rope_append(const void* q, const void* k, const void* v, long long ldq, long long ldk, long long ldv,
                    void* q_out, void* K_cache, void* V_cache, const float* cos_tab, const float* sin_tab, int T,
@@ -373,8 +374,14 @@ int Session::run_layers(int T, int pos0, const int* pos_dev) {
         CK(cdna3_attn_prefill_strided(qh, Kl, Vl, attn, &pc, &ps, CDNA4_F16, s));
         CK(gemm(attn, l.wo, hidden, true, 1.f, T, H, QD, H));
         CK(llm_norm_cast(lnorm, hidden, l.n_mlp, l.n_mlp_b, xn, T, H, eps, stream));
-        CK(gemm(xn, l.wgu, gu, true, 0.f, T, 2 * F, H, 2 * F));
-        CK(llm_silu_mul(gu, act, T, F, stream));
+        // gate|up and the SiLU product in one launch where the library GEMM takes the shape
+        const int fused = rocblas_only ? -1 : llm_gemm_f16_silu(xn, l.wgu, act, T, F, H, F, stream);
+        if (fused == -1) {
+            CK(gemm(xn, l.wgu, gu, true, 0.f, T, 2 * F, H, 2 * F));
+            CK(llm_silu_mul(gu, act, T, F, stream));
+        } else {
+            CK(fused);
+        }
         CK(gemm(act, l.wdown, hidden, true, 1.f, T, H, F, H));
     }
     return 0;

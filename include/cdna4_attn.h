@@ -265,6 +265,15 @@ int cdna4_gemm_f16_nt(const void* X, const void* W, void* Y, int y_f32, int accu
 /* The BM x BN tile (rows of X x rows of W per workgroup) cdna4_gemm_f16_nt takes for a shape on
  * the current device (no counterpart in the reference: tests use it to cover every tile). */
 int cdna4_gemm_f16_nt_tile(int M, int N, int K, int* bm, int* bn);
+/* The SwiGLU gate|up product and the SiLU product in one launch: W = [Wg; Wu] fp16 [2F][K]
+ * (gate rows, then up rows), Y fp16 [M][F] (leading dimension ldy) = fp16(silu(g) * u) with
+ * g = X Wg^T and u = X Wu^T accumulated in fp32. Replaces the reference runtime's gate and up
+ * GEMMs followed by silu_mul_f32_kernel (cdna3-prims/include/cdna3/runtime/session.hpp:227-231,
+ * forward.hpp:154-160). Same shape rules as cdna4_gemm_f16_nt (F a multiple of 4, Y 8-byte
+ * aligned); cdna4_gemm_f16_nt_silu_tile reports its tile (BN counts gate and up rows). */
+int cdna4_gemm_f16_nt_silu(const void* X, const void* W, void* Y, int M, int F, int K, int ldy,
+                           cdna4_stream_t stream);
+int cdna4_gemm_f16_nt_silu_tile(int M, int F, int K, int* bm, int* bn);
 
 /*
  * KV cache and layout kernels of the runtime layer loop (all fp16, device pointers).

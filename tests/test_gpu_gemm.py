@@ -73,3 +73,34 @@ def test_gemm_refuses_shapes_it_does_not_take(M, N, K):
     X, W = _operands(M, N, K, 9)
     with pytest.raises(RuntimeError):
         cdna4.gemm_f16_nt(X, W)
+
+
+@pytest.mark.parametrize("M,F,K,tile", [
+    (512, 3072, 768, (128, 128)),   # cfg5 gate|up with the SiLU product
+    (37, 100, 64, (64, 64)),        # ragged M and F, one K stage
+    (300, 3072, 64, (64, 128)),
+    (4128, 224, 64, (128, 64)),
+    (129, 260, 640, (64, 64)),
+])
+def test_gemm_silu_against_torch_fp32(M, F, K, tile):
+    # Y = fp16(silu(X Wg^T) * (X Wu^T)) with W = [Wg; Wu]; the reference forms both products in fp32
+    # and rounds the SiLU product once, as the separate silu_mul kernel does
+    if torch.cuda.get_device_properties(DEV).multi_processor_count == 256:
+        assert cdna4.gemm_f16_nt_silu_tile(M, F, K) == tile
+    X, W = _operands(M, 2 * F, K, M * 13 + F * 5 + K)
+    g = X.float() @ W[:F].float().t()
+    u = X.float() @ W[F:].float().t()
+    ref = g / (1 + torch.exp(-g)) * u
+    got = cdna4.gemm_f16_nt_silu(X, W)
+    torch.cuda.synchronize()
+    assert got.dtype == torch.float16 and tuple(got.shape) == (M, F)
+    # fp32 sums in another order (1e-5 of the largest |g| |u|), then one fp16 rounding of the product
+    s = max(1.0, g.abs().max().item() * max(1.0, u.abs().max().item()))
+    err = ((got.float() - ref).abs() - 2.0 ** -11 * ref.abs()).max().item()
+    assert err <= 1e-5 * s, (M, F, K, err)
+
+
+def test_gemm_silu_refuses_shapes_it_does_not_take():
+    X, W = _operands(8, 2 * 6, 64, 3)   # F = 6, not a multiple of 4
+    with pytest.raises(RuntimeError):
+        cdna4.gemm_f16_nt_silu(X, W)
