@@ -27,7 +27,10 @@ Also reported in the same line:
           decode phase, with the time to the first token separately, and the CPU oracle's decode
           step beside it.
 Kernel durations come from HIP events recorded on the stream the kernels run on (torch's current
-stream). The CPU baseline times the reference's own fp32 cpu_prefill (built from the reference
+stream), around exactly --steps launches of each leg. Before them each leg runs at least --warmup
+untimed launches and keeps launching until at least 100 ms have passed (`warmup_rule`; the prefill
+legs report the count run as `warmup_run`): from an idle GPU the clocks take that long to settle.
+The CPU baseline times the reference's own fp32 cpu_prefill (built from the reference
 sources into oracle/_ref) on one (batch, head) of config 3, one thread; the oracle's restatement
 is timed instead when oracle/_ref is absent. `cpu_baseline_threads` is the same work on one
 (batch, head) per thread, up to 16 threads, labelled as such; the decode, cfg1 and dpp legs carry
@@ -66,13 +69,32 @@ def parse():
     return args
 
 
-def time_launches(torch, fn, steps, warmup):
+# Untimed launches of a leg before its timed steps: at least `warmup` of them and at least this
+# long. Coming from an idle GPU the clocks take ~100 ms to settle: the config-3 prefill measured
+# 1,166-1,181 TFLOP/s after 5 warm-up launches (9 ms) against 1,210-1,213 after 50 (three runs
+# each on one box), so a count-only warm-up of a few launches times the clock ramp.
+WARMUP_MIN_MS = 100.0
+WARMUP_RUN = {}   # leg name -> untimed launches its last time_launches call ran
+
+
+def time_launches(torch, fn, steps, warmup, leg=None):
     """Average duration of one step (ms) and the total (ms): HIP events recorded on the launch
     stream around `steps` back-to-back steps (no events between steps, which would add their own
-    gaps), after `warmup` untimed steps, with the device synchronised on both sides."""
+    gaps), after at least `warmup` untimed steps and WARMUP_MIN_MS of them, with the device
+    synchronised on both sides. The untimed count goes to WARMUP_RUN[leg]."""
+    t_start = time.perf_counter()
+    n = 0
     for _ in range(warmup):
         fn()
+        n += 1
     torch.cuda.synchronize()
+    while (time.perf_counter() - t_start) * 1e3 < WARMUP_MIN_MS:
+        for _ in range(max(1, warmup)):
+            fn()
+            n += 1
+        torch.cuda.synchronize()
+    if leg is not None:
+        WARMUP_RUN[leg] = n
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
     for i in range(steps):
@@ -266,11 +288,12 @@ def bench_prefill(torch, cdna4, steps, warmup, dtype=None):
     V = torch.randn(B, H, S, D, device="cuda", dtype=dtype, generator=g)
     O = torch.empty_like(Q)
     cfg = cdna4.PrefillCfg(D, S, S, H, H, B, 1)
-    avg_ms, total_ms = time_launches(torch, lambda i=0: cdna4.prefill(Q, K, V, O, cfg), steps, warmup)
+    leg = "prefill" if dtype == torch.bfloat16 else "prefill_fp16"
+    avg_ms, total_ms = time_launches(torch, lambda i=0: cdna4.prefill(Q, K, V, O, cfg), steps, warmup, leg)
     flop = 4.0 * B * H * D * S * (S + 1) / 2          # causal: S(S+1)/2 visible (q, k) pairs
     tflops = flop / (avg_ms * 1e-3) / 1e12
     assert torch.isfinite(O[:, :, :64].float()).all()
-    return {"avg_ms": avg_ms, "total_ms": total_ms, "tflops": tflops, "flop": flop,
+    return {"avg_ms": avg_ms, "total_ms": total_ms, "tflops": tflops, "flop": flop, "warmup_run": WARMUP_RUN[leg],
             "config": {"workload": "FA2 prefill, BASELINE config 3", "batch": B, "heads": H, "seq_len": S,
                        "head_dim": D, "causal": True, "dtype": "bf16" if dtype == torch.bfloat16 else "fp16"}}
 
@@ -574,12 +597,15 @@ def main():
     import torch
     import cdna4
     torch.cuda.set_device(0)
-    result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+    result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+              "warmup_rule": f"at least {args.warmup} untimed launches and at least {WARMUP_MIN_MS:.0f} ms of them "
+                             "per leg (clock settle); timed region exactly `steps` launches",
+              "higher_is_better": True,
               "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1))"}
     if "prefill" in args.legs:
         p = bench_prefill(torch, cdna4, args.steps, args.warmup)
         result.update({"value": p["tflops"], "unit": "TFLOPS", "ms_per_step": p["total_ms"] / args.steps,
-                       "config": p["config"],
+                       "warmup_run": p["warmup_run"], "config": p["config"],
                        "roofline": {"bound": "mfma", "achieved": p["tflops"], "peak": PEAK_BF16_TFLOPS,
                                     "unit": "TFLOP/s", "frac": p["tflops"] / PEAK_BF16_TFLOPS,
                                     "traffic": load_traffic("prefill"), "traffic_source": TRAFFIC_SOURCE,
@@ -588,7 +614,8 @@ def main():
         torch.cuda.empty_cache()
         p16 = bench_prefill(torch, cdna4, max(5, args.steps // 2), max(3, args.warmup // 2), torch.float16)
         result["prefill_fp16"] = {"value": p16["tflops"], "unit": "TFLOPS", "avg_ms": p16["avg_ms"],
-                                  "frac": p16["tflops"] / PEAK_BF16_TFLOPS, "config": p16["config"]}
+                                  "frac": p16["tflops"] / PEAK_BF16_TFLOPS, "warmup_run": p16["warmup_run"],
+                                  "config": p16["config"]}
         result["prefill_vs_torch_sdpa"] = bench_torch_sdpa(torch, result["value"])
     if "decode" in args.legs:
         result["decode"] = bench_decode(torch, cdna4, args.steps, args.warmup)
