@@ -175,5 +175,45 @@ __device__ __forceinline__ void merge_waves(const f32x4 (&o)[1][D / 16], const f
     }
 }
 
+// merge_waves for a workgroup that serves one of several key ranges of its heads: the merged
+// (M, L, O) of the W waves, unnormalised (O and L relative to 2^M, M in base-2 units), goes to the
+// split-K partial layout, part_ml[(row * P + split) * 2] = (M, L) and part_o[(row * P + split) * D
+// + d] = O[d] for the nrows query heads (rows) of the group, row = qrow0 + h.
+template <int D, int W>
+__device__ __forceinline__ void merge_waves_part(const f32x4 (&o)[1][D / 16], const f32x4 (&lacc)[1],
+                                                 const float (&m)[1], float* po, float* pml, int nrows,
+                                                 float* part_ml, float* part_o, size_t qrow0, int P, int split,
+                                                 int wave, int lane) {
+    constexpr int NDT = D / 16;
+    const int li = lane & 15, g = lane >> 4;
+    __syncthreads();   // every wave is done with its ring: reuse the LDS for the partials
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+        *(f32x4*)(po + ((size_t)wave * 16 + li) * D + dt * 16 + g * 4) = o[0][dt];
+    if (g == 0) {
+        pml[(wave * 16 + li) * 2] = m[0];
+        pml[(wave * 16 + li) * 2 + 1] = lacc[0][0];
+    }
+    __syncthreads();
+    for (int p = (int)threadIdx.x; p < nrows * (D / 2); p += 64 * W) {
+        const int h = p / (D / 2), d = 2 * (p % (D / 2));
+        float M = tile::kInitM;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, pml[(w * 16 + h) * 2]);
+        float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float wt = exp2f(pml[(w * 16 + h) * 2] - M);
+            L = fmaf(wt, pml[(w * 16 + h) * 2 + 1], L);
+            const float2 v = *(const float2*)(po + ((size_t)w * 16 + h) * D + d);
+            o0 = fmaf(wt, v.x, o0);
+            o1 = fmaf(wt, v.y, o1);
+        }
+        const size_t pidx = (qrow0 + h) * (size_t)P + split;
+        *(float2*)(part_o + pidx * D + d) = make_float2(o0, o1);
+        if (d == 0) *(float2*)(part_ml + pidx * 2) = make_float2(M, L);
+    }
+}
+
 }  // namespace stream
 }  // namespace cdna4

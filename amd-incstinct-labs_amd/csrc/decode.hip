@@ -187,8 +187,15 @@ constexpr int wg_ring_elems() { return W * kDecStages * kDecT * D; }
 // Keys per wave of the short-cache variant: N split into W ranges of whole 32-key chunks.
 __host__ __device__ constexpr int wg_keys_per_wave(int N, int W) { return ((N + W - 1) / W + kDecT - 1) / kDecT * kDecT; }
 
+// Keys per workgroup when the cache is split over P workgroups per (batch, kv head, head group):
+// N in P ranges of whole 32-key chunks.
+__host__ __device__ constexpr int wg_keys_per_split(int N, int P) { return ((N + P - 1) / P + kDecT - 1) / kDecT * kDecT; }
+
 // kNT: the copies take the non-temporal policy (long caches; see plan_decode).
-template <int D, bool kBf16, int W, bool kNT>
+// kPart: workgroup blockIdx.x of a.P serves the blockIdx.x-th of P key ranges (wg_keys_per_split)
+// and leaves the merged (m, l, O) of its waves in the split-K partials (a.part_ml, a.part_o)
+// instead of writing o; a consumer merges the P partials of each query head.
+template <int D, bool kBf16, int W, bool kNT, bool kPart = false>
 __global__ __launch_bounds__(64 * W) void decode_wg(DecodeArgs a, void* __restrict__ out) {
     constexpr int ND = D / 32, NDT = D / 16;
     constexpr int kStage = kDecT * D;
@@ -206,9 +213,15 @@ __global__ __launch_bounds__(64 * W) void decode_wg(DecodeArgs a, void* __restri
     const int qh0 = kvh * a.G + sub * 16;
     const int nrows = min(16, a.G - sub * 16);
     const int N = a.len_pos ? *a.len_pos + 1 : a.N;
-    const int KPW = a.len_pos ? wg_keys_per_wave(N, W) : a.KPW;
-    const int kbeg = min(N, wave * KPW);
-    const int kend = min(N, kbeg + KPW);
+    int s0 = 0, s1 = N;   // this workgroup's keys
+    if constexpr (kPart) {
+        const int KPS = wg_keys_per_split(N, a.P);
+        s0 = min(N, (int)blockIdx.x * KPS);
+        s1 = min(N, s0 + KPS);
+    }
+    const int KPW = (a.len_pos || kPart) ? wg_keys_per_wave(s1 - s0, W) : a.KPW;
+    const int kbeg = min(s1, s0 + wave * KPW);
+    const int kend = min(s1, kbeg + KPW);
     const size_t head_off = ((size_t)b * a.nKVH + kvh) * (size_t)a.stride * D;
 
     u32x4 qb[1][ND];
@@ -218,8 +231,12 @@ __global__ __launch_bounds__(64 * W) void decode_wg(DecodeArgs a, void* __restri
     stream_keys<D, kBf16, kDecStages, kNT>((const uint16_t*)a.K + head_off, (const uint16_t*)a.V + head_off, D, N, kbeg,
                                       kend, 0, 0, a.sc, qb, o, lacc, m, k_lds + wave * kRing, v_lds + wave * kRing,
                                       lane);
-    merge_waves<D, kBf16, W>(o, lacc, m, (float*)k_lds, (float*)v_lds, nrows,
-                             (uint16_t*)out + ((size_t)b * a.nQH + qh0) * D, wave, lane);
+    if constexpr (kPart)
+        merge_waves_part<D, W>(o, lacc, m, (float*)k_lds, (float*)v_lds, nrows, a.part_ml, a.part_o,
+                               (size_t)b * a.nQH + qh0, a.P, (int)blockIdx.x, wave, lane);
+    else
+        merge_waves<D, kBf16, W>(o, lacc, m, (float*)k_lds, (float*)v_lds, nrows,
+                                 (uint16_t*)out + ((size_t)b * a.nQH + qh0) * D, wave, lane);
 }
 
 // One wave per (batch, query head): o = sum_i 2^(m_i - M) O_i / sum_i 2^(m_i - M) l_i.
@@ -480,6 +497,46 @@ int attn_decode_replayable(const void* q, const void* K, const void* V, void* o,
                               : launch_decode<128, false>(c, p, q, K, V, o, ws, s, len_pos);
     return bf ? launch_decode<64, true>(c, p, q, K, V, o, ws, s, len_pos)
               : launch_decode<64, false>(c, p, q, K, V, o, ws, s, len_pos);
+}
+
+// Batch-1 decode attention left as P split-K partials for a consumer that merges them (the
+// runtime's O-projection GEMV, llm_gemv_residual_merge): P workgroups per (kv head, head group),
+// each over one of P key ranges of the cache (*len_pos + 1 keys when len_pos is set, else c.N),
+// writing part_ml [nQH][P][2] and part_o [nQH][P][D] at the start of ws. A short cache then runs
+// on P times the workgroups of the one-launch plan, with no merge launch of its own. Bytes of ws:
+// attn_decode_partials_bytes.
+size_t attn_decode_partials_bytes(const cdna3_decode_cfg& c, int P) {
+    const size_t nml = (size_t)c.nQHeads * P * 2;
+    return ((nml * sizeof(float) + 255) & ~(size_t)255) + (size_t)c.nQHeads * P * c.D * sizeof(float);
+}
+
+int attn_decode_partials(const void* q, const void* K, const void* V, const cdna3_decode_cfg& c, int dtype, int P,
+                         void* ws, size_t ws_bytes, const int* len_pos, hipStream_t s) {
+    Plan p;
+    if (!plan_decode(c, false, p) || c.batch != 1 || P < 1 || P > 65535 || !ws) return CDNA4_ERR_INVALID_VALUE;
+    if (ws_bytes < attn_decode_partials_bytes(c, P)) return CDNA4_ERR_INVALID_VALUE;
+    DecodeArgs a;
+    a.len_pos = len_pos;
+    a.q = q; a.K = K; a.V = V;
+    a.part_ml = (float*)ws;
+    a.part_o = (float*)((char*)ws + (((size_t)c.nQHeads * P * 2 * sizeof(float) + 255) & ~(size_t)255));
+    a.N = c.N; a.nQH = c.nQHeads; a.nKVH = c.nKVHeads; a.stride = c.stride_kv == 0 ? c.N : c.stride_kv;
+    a.G = p.G; a.HB = p.HB; a.KPW = 0; a.P = P;
+    a.sc = kLog2e / sqrtf((float)c.D);
+    const long long gy = (long long)c.nKVHeads * p.HB;
+    if (gy > 65535) return CDNA4_ERR_INVALID_VALUE;
+    const dim3 grid((unsigned)P, (unsigned)gy, 1u);
+    const bool bf = dtype == CDNA4_BF16;
+    if (c.D == 128) {
+        constexpr int W = wg_waves<128>();
+        if (bf) decode_wg<128, true, W, false, true><<<grid, 64 * W, 0, s>>>(a, nullptr);
+        else decode_wg<128, false, W, false, true><<<grid, 64 * W, 0, s>>>(a, nullptr);
+    } else {
+        constexpr int W = wg_waves<64>();
+        if (bf) decode_wg<64, true, W, false, true><<<grid, 64 * W, 0, s>>>(a, nullptr);
+        else decode_wg<64, false, W, false, true><<<grid, 64 * W, 0, s>>>(a, nullptr);
+    }
+    return launch_status();
 }
 
 }  // namespace cdna4

@@ -390,6 +390,85 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemv_residual_split(const ui
     }
 }
 
+// The attention output x (fp16, [heads][D] flat, K = heads * D) merged from the split-K partials
+// of the decode attention: chunk c of x (8 elements of head h = 8c / D) is
+// fp16(sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p), M = max_p m_p, over the P (<= kMaxParts)
+// partials part_ml[(h P + p) * 2] = (m_p, l_p), part_o[(h P + p) D + d] (the layout the decode
+// kernels write, batch 1). Rounded once, as the decode kernels round o.
+constexpr int kMaxParts = 4;
+
+__device__ __forceinline__ u32x4 merged_chunk(const float* __restrict__ part_ml, const float* __restrict__ part_o,
+                                              int P, int D, int c) {
+    const int h = (8 * c) / D, d0 = (8 * c) % D;
+    float2 ml[kMaxParts];
+    float4 lo[kMaxParts], hi[kMaxParts];
+#pragma unroll
+    for (int p = 0; p < kMaxParts; ++p) {   // every load issued before any arithmetic
+        const int pp = min(p, P - 1);
+        ml[p] = *(const float2*)(part_ml + ((size_t)h * P + pp) * 2);
+        lo[p] = *(const float4*)(part_o + ((size_t)h * P + pp) * D + d0);
+        hi[p] = *(const float4*)(part_o + ((size_t)h * P + pp) * D + d0 + 4);
+    }
+    float M = ml[0].x;
+#pragma unroll
+    for (int p = 1; p < kMaxParts; ++p)
+        if (p < P) M = fmaxf(M, ml[p].x);
+    float L = 0.f, v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < kMaxParts; ++p) {
+        if (p >= P) break;
+        const float wt = exp2f(ml[p].x - M);
+        L = fmaf(wt, ml[p].y, L);
+        v[0] = fmaf(wt, lo[p].x, v[0]); v[1] = fmaf(wt, lo[p].y, v[1]);
+        v[2] = fmaf(wt, lo[p].z, v[2]); v[3] = fmaf(wt, lo[p].w, v[3]);
+        v[4] = fmaf(wt, hi[p].x, v[4]); v[5] = fmaf(wt, hi[p].y, v[5]);
+        v[6] = fmaf(wt, hi[p].z, v[6]); v[7] = fmaf(wt, hi[p].w, v[7]);
+    }
+    const float inv = L > 0.f ? 1.f / L : 1.f;
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        r[i] = f32_to_f16_bits(v[2 * i] * inv) | (f32_to_f16_bits(v[2 * i + 1] * inv) << 16);
+    return r;
+}
+
+// gemv_residual_split with its input vector merged from decode partials (merged_chunk).
+template <int J>
+__global__ __launch_bounds__(64 * kSplitWaves) void gemv_residual_merge(const float* __restrict__ part_ml,
+                                                                        const float* __restrict__ part_o, int P, int D,
+                                                                        const uint16_t* __restrict__ W,
+                                                                        float* __restrict__ out, int K) {
+    __shared__ float part[kSplitWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int C = K / 8, Q = (C + kSplitWaves - 1) / kSplitWaves;
+    const int q0 = wave * Q, qn = min(C, q0 + Q) - q0;
+    const int row = blockIdx.x;
+    u32x4 w[J], xv[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int c = min(q0 + min(lane + 64 * j, max(qn - 1, 0)), C - 1);
+        w[j] = __builtin_nontemporal_load((const u32x4*)(W + (size_t)row * K) + c);
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int c = min(q0 + min(lane + 64 * j, max(qn - 1, 0)), C - 1);
+        xv[j] = merged_chunk(part_ml, part_o, P, D, c);
+    }
+    float y = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+        if (lane + 64 * j < qn) y = dot8(w[j], xv[j], y);
+    y = allreduce(y, Sum{});
+    if (lane == 0) part[wave] = y;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float acc = part[0];
+#pragma unroll
+        for (int i = 1; i < kSplitWaves; ++i) acc += part[i];
+        out[row] += acc;
+    }
+}
+
 // Final argmax over the per-wave keys of the logits GEMV: one workgroup of 1024 lanes, each
 // folding a strided share (loads issued 8 at a time), then the DPP butterfly per wave and wave 0
 // over the 16 wave results. Writes the token to ids[0] and tokens[step] and, when embed is
@@ -546,6 +625,22 @@ int llm_norm_cast(bool layer, const float* X, const void* W, const void* B, void
         case 4: norm_cast_launch<4>(layer, X, W, B, Y, M, H, eps, s); break;
         case 6: norm_cast_launch<6>(layer, X, W, B, Y, M, H, eps, s); break;
         default: norm_cast_launch<8>(layer, X, W, B, Y, M, H, eps, s); break;
+    }
+    return launch_status();
+}
+
+// out[n] += W[n] . x with x merged from P decode partials of K / D heads (batch 1; see merged_chunk).
+int llm_gemv_residual_merge(const float* part_ml, const float* part_o, int P, int D, const void* W, float* out, int N,
+                            int K, hipStream_t s) {
+    if (!gemv_shape_ok(K, true) || N < 1 || P < 1 || P > kMaxParts || D % 8 || K % D) return CDNA4_ERR_INVALID_VALUE;
+    const int q = (K / 8 + kSplitWaves - 1) / kSplitWaves;
+    const uint16_t* WW = (const uint16_t*)W;
+    const unsigned grid = (unsigned)N, block = 64 * kSplitWaves;
+    switch ((q + 63) / 64) {
+        case 1: gemv_residual_merge<1><<<grid, block, 0, s>>>(part_ml, part_o, P, D, WW, out, K); break;
+        case 2: gemv_residual_merge<2><<<grid, block, 0, s>>>(part_ml, part_o, P, D, WW, out, K); break;
+        case 3: gemv_residual_merge<3><<<grid, block, 0, s>>>(part_ml, part_o, P, D, WW, out, K); break;
+        default: gemv_residual_merge<4><<<grid, block, 0, s>>>(part_ml, part_o, P, D, WW, out, K); break;
     }
     return launch_status();
 }

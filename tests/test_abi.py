@@ -206,8 +206,9 @@ def test_header_runtime_kernels_use_no_lds(tmp_path):
 
 def test_library_kernels_avoid_lds_where_designed_to(tmp_path):
     # Reductions, scans, norms, KV-cache and runtime kernels and the decode merge are LDS-free by design; prefill and the
-    # decode kernels (split partials and the short-cache workgroup variant) stage K/V in LDS, and the residual GEMV
-    # of the runtime meets its four waves' partial sums of a row in LDS (one write per wave, one read of four).
+    # decode kernels (split partials and the short-cache workgroup variant) stage K/V in LDS, and the residual GEMVs
+    # of the runtime (plain and merging decode partials) meet their four waves' partial sums of a row in LDS (one
+    # write per wave, one read of four).
     for src in ("reduce_scan.hip", "norms.hip", "decode.hip", "kv_cache.hip", "llm.hip"):
         asm = _device_asm(os.path.join(ROOT, "amd-incstinct-labs_amd", "csrc", src), tmp_path)
         for name, body in _functions(asm).items():
@@ -215,7 +216,7 @@ def test_library_kernels_avoid_lds_where_designed_to(tmp_path):
             if "decode_mfma" in name or "decode_wg" in name:
                 continue
             ds = re.findall(r"^\s+(ds_\w+)", body, re.M)
-            if "gemv_residual_split" in name:
+            if "gemv_residual_split" in name or "gemv_residual_merge" in name:
                 assert len(ds) <= 4, (src, name, ds)
                 continue
             assert not ds, (src, name)

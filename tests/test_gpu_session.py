@@ -110,6 +110,21 @@ def test_generate_matches_oracle(model, n, new):
     _check_generation(meta, t, ids, out, 96)
 
 
+@pytest.mark.parametrize("parts", ["0", "1", "2", "4"])
+@pytest.mark.parametrize("n,new", [(21, 16), (200, 12)])
+def test_decode_attention_partials_match_oracle(model, monkeypatch, n, new, parts):
+    # Short-cache decode steps run the attention as P split-K partials per head that the O
+    # projection's GEMV merges (CDNA4_SESSION_ATTN_PARTS, default 3; "0" is the one-launch
+    # attention and a plain GEMV). Every P, including key ranges left empty (P x 32-key chunks per
+    # wave beyond the cache), against the oracle.
+    d, meta, t = model
+    monkeypatch.setenv("CDNA4_SESSION_ATTN_PARTS", parts)
+    ids = _prompt(meta, n, 500 + n)
+    with cdna4.Session(d, max_seq=256) as s:
+        out = s.generate_ex(ids, cdna4.GenerateCfg(new), with_logits=True)
+    _check_generation(meta, t, ids, out, 256, what=f"decode attention in {parts} partials")
+
+
 def test_session_reuse_and_plain_generate(model):
     # a second, shorter prompt on the same session sees none of the first one's cache rows
     d, meta, t = model
