@@ -9,6 +9,10 @@
 //   mfma_bf16_exp    the same with one v_exp_f32 beside every two MFMAs (the prefill's ratio of
 //                    exponentials to matrix instructions);
 //   mfma_f16(_exp)   both with v_mfma_f32_16x16x32_f16 on the same bit patterns;
+//   lds_dma_cu       the asynchronous global -> LDS copy rate of one CU: eight workgroups of four
+//                    waves (one per XCD), each streaming its own 16 MiB through a ring of four
+//                    16 KiB LDS stages (three in flight) with global_load_lds_dwordx4, reported per
+//                    CU; the 128 MiB are re-read every launch, so they come from the Infinity Cache;
 // each the median of five timed runs (HIP events), printed as one JSON line. `ceilings mfma S [exp]
 // [f16]` instead runs only one MFMA stream for about S seconds, one line per 50 launches.
 // The buffer reads are 1 GiB, four times the 256 MB Infinity Cache, so no read is served from it.
@@ -55,6 +59,35 @@ __global__ __launch_bounds__(256) void read_stream(const u32x4* __restrict__ p, 
         acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
     }
     if (acc == 0x9e3779b9u) sink[0] = acc;   // keeps the loads; the value never matches here
+}
+
+// One workgroup's copy loop of lds_dma_cu: per stage each wave copies 4 KiB (four 1 KiB copies),
+// keeps three stages in flight, and waits for the oldest before issuing the next.
+__global__ __launch_bounds__(256) void lds_dma(const char* __restrict__ src, size_t per_wg, uint32_t* sink) {
+    constexpr int S = 4;
+    __shared__ __attribute__((aligned(16))) char lds[S * 16384];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const char* base = src + blockIdx.x * per_wg;
+    const int nch = (int)(per_wg / 16384);
+    auto issue = [&](int c) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const char* g = base + (size_t)c * 16384 + (wave * 4 + j) * 1024 + lane * 16;
+            const uint32_t l = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(
+                lds + (c % S) * 16384 + (wave * 4 + j) * 1024);
+            asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(l) : "memory");
+        }
+    };
+    for (int c = 0; c < S - 1 && c < nch; ++c) issue(c);
+    for (int c = 0; c < nch; ++c) {
+        if (c + S - 1 < nch) {
+            issue(c + S - 1);
+            asm volatile("s_waitcnt vmcnt(12)" : : : "memory");   // 4 copies x (S - 1) younger stages
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+        }
+    }
+    if (threadIdx.x == 0 && lds[lane] == 123) sink[0] = 1;   // keeps the copies; never true here
 }
 
 template <int U>
@@ -228,14 +261,16 @@ int main(int argc, char** argv) {
     const float m1 = time_ms([&] { launch_mfma<bf16x8>(true, cus, sink, iters, fout); }, 5);
     const float h0 = time_ms([&] { launch_mfma<f16x8>(false, cus, sink, iters, fout); }, 5);
     const float h1 = time_ms([&] { launch_mfma<f16x8>(true, cus, sink, iters, fout); }, 5);
+    const size_t per_wg = (size_t)16 << 20;
+    const float dm = time_ms([&] { lds_dma<<<8, 256>>>((const char*)a, per_wg, sink + 2048); }, 5);
     CK(hipGetLastError());
     printf("{\"cus\": %d, \"read_nt_GBs\": %.1f, \"read_GBs\": %.1f, \"copy_nt_GBs\": %.1f, "
            "\"mfma_bf16_TFLOPs\": %.1f, \"mfma_bf16_exp_TFLOPs\": %.1f, \"mfma_f16_TFLOPs\": %.1f, "
-           "\"mfma_f16_exp_TFLOPs\": %.1f, "
+           "\"mfma_f16_exp_TFLOPs\": %.1f, \"lds_dma_cu_GBs\": %.1f, "
            "\"shapes\": {\"read_nt\": [%d, %d], \"read\": [%d, %d], \"copy_nt\": [%d, %d]}}\n",
            cus, bytes / (r_nt.ms * 1e-3) / 1e9, bytes / (r_df.ms * 1e-3) / 1e9, 2.0 * bytes / (c_nt.ms * 1e-3) / 1e9,
            flop / (m0 * 1e-3) / 1e12, flop / (m1 * 1e-3) / 1e12, flop / (h0 * 1e-3) / 1e12,
-           flop / (h1 * 1e-3) / 1e12, r_nt.grid, r_nt.u, r_df.grid, r_df.u, c_nt.grid,
+           flop / (h1 * 1e-3) / 1e12, per_wg / (dm * 1e-3) / 1e9, r_nt.grid, r_nt.u, r_df.grid, r_df.u, c_nt.grid,
            c_nt.u);
     CK(hipFree(a));
     CK(hipFree(b));
