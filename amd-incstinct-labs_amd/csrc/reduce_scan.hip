@@ -390,17 +390,19 @@ __device__ Acc look_back(const ScanState& st, size_t tile, Op op) {
     return acc;
 }
 
-// Wave w of workgroup g scans tile g * 4 + w (scan_layout::group_tile); the group runs one
-// look-back for its four tiles. With one tile per single-wave workgroup the look-back was the
-// bound: per-tile stamps showed a tile's loads arriving after 13 us and its look-back taking
-// another 17 us (median, ~2 us per round trip of the device-scope slot words behind the stream),
-// as prefixes trailed ~190 tiles behind the aggregates; four times fewer, larger look-back units
-// took the f32 scan at 2^26 from 125 to 102 us (16-bit inputs 112 -> 83 us, 64-bit 253 -> 202 us;
-// two or eight waves per group: 112 / 115 us).
+// Wave w of workgroup g scans tile g W + w (scan_layout::group_tile, W = scan_waves: 4, or 8 for
+// 8-byte inputs); the group runs one look-back for its W tiles. With one tile per single-wave
+// workgroup the look-back was the bound: per-tile stamps showed a tile's loads arriving after
+// 13 us and its look-back taking another 17 us (median, ~2 us per round trip of the device-scope
+// slot words behind the stream), as prefixes trailed ~190 tiles behind the aggregates; four times
+// fewer, larger look-back units took the f32 scan at 2^26 from 125 to 102 us (16-bit inputs 112 ->
+// 83 us, 64-bit 253 -> 202 us, and 200 -> 187 us with eight-wave groups).
+template <int DT> constexpr int scan_group_waves() { return scan_layout::scan_waves((int)sizeof(typename ScanElem<DT>::In)); }
+
 template <int DT, class Op, bool kVec>
-__global__ __launch_bounds__(64 * scan_layout::kScanWaves) void scan_tiles(const void* __restrict__ in_, size_t n,
-                                                                           void* __restrict__ out_, ScanState st) {
-    constexpr int kWaves = scan_layout::kScanWaves;
+__global__ __launch_bounds__(64 * scan_group_waves<DT>()) void scan_tiles(const void* __restrict__ in_, size_t n,
+                                                                          void* __restrict__ out_, ScanState st) {
+    constexpr int kWaves = scan_group_waves<DT>();
     using E = ScanElem<DT>;
     using Acc = typename E::Acc;
     using Out = typename E::Out;
@@ -414,7 +416,7 @@ __global__ __launch_bounds__(64 * scan_layout::kScanWaves) void scan_tiles(const
     const unsigned lane = threadIdx.x & 63u;
     const unsigned wave = threadIdx.x >> 6;
     const size_t group = blockIdx.x;
-    const size_t tile = scan_layout::group_tile(group, wave);
+    const size_t tile = scan_layout::group_tile(group, wave, kWaves);
     const bool live = tile < (n + TILE - 1) / TILE;   // the last group's waves past the last tile: no memory access
     const size_t base = live ? scan_layout::tile_base(tile, TILE) : 0;
     // The group's exchange line in the workspace (global memory, no LDS): the waves' tile totals,
@@ -644,7 +646,8 @@ int scan_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
     const bool vec = ((uintptr_t)in % 16) == 0 && ((uintptr_t)out % 16) == 0;
     const size_t n_main = scan_layout::main_elems(n, vec, (int)VEC);
     const size_t ntiles = vec ? scan_tiles_for<DT, true>(n_main) : scan_tiles_for<DT, false>(n_main);
-    const size_t ngroups = scan_layout::groups_for(ntiles);   // look-back slots: one per group
+    constexpr int kWaves = scan_group_waves<DT>();
+    const size_t ngroups = scan_layout::groups_for(ntiles, kWaves);   // look-back slots: one per group
     char* w = (char*)ws;
     ScanState st;
     st.error = (uint32_t*)w;
@@ -656,7 +659,7 @@ int scan_launch(const void* in, size_t n, void* out, void* ws, hipStream_t s) {
     st.agg = (uint64_t*)(w + scan_layout::agg_offset());
     st.pre = (uint64_t*)(w + scan_layout::pre_offset(ngroups));
     st.xchg = (unsigned char*)w + scan_layout::xchg_offset(ngroups);
-    constexpr unsigned kThreads = 64 * scan_layout::kScanWaves;
+    constexpr unsigned kThreads = 64 * kWaves;
     if (ngroups > 0) {
         if (vec)
             scan_tiles<DT, Op, true><<<(unsigned)ngroups, kThreads, 0, s>>>(in, n_main, out, st);

@@ -24,8 +24,8 @@ constexpr size_t tiles_for(size_t n, int vec, int u) { return (n + tile_elems(ve
 // [agg slots: align256(nslots * 16)][pre slots: align256(nslots * 16)][exchange lines:
 // nslots * kXchgStride], two 64-bit words per slot and array (one used by 32-bit values), and per
 // group one 128-byte line in which its waves leave their tile totals and wave 0 the group's prefix
-// (kScanWaves + 1 values of at most 8 bytes). The library sizes it by the misaligned path's tile
-// count, which bounds the group count of either path.
+// (W + 1 values of at most 8 bytes, W the group's waves). The library sizes it by the misaligned
+// path's tile count, which bounds the group count of either path.
 constexpr size_t kXchgStride = 128;
 constexpr size_t ws_bytes(size_t ntiles) { return 256 + 2 * align256(ntiles * 16) + align256(ntiles * kXchgStride); }
 constexpr size_t agg_offset() { return 256; }
@@ -51,14 +51,18 @@ constexpr bool vec_live(bool full, int j, unsigned lane, uint32_t rem, int VEC) 
 // Element e of vector j of a lane on the element-wise (misaligned) path, and its guard.
 constexpr uint32_t elem_in_tile(int j, unsigned lane, int e, int VEC) { return vec_in_tile(j, lane) * (uint32_t)VEC + e; }
 
-// Tiles run in workgroups of kScanWaves waves, one tile per wave: wave w of workgroup g scans tile
-// g * kScanWaves + w (waves past the last tile load and store nothing). The waves' totals meet in
-// the workgroup, and the look-back state (a slot per published value) is per workgroup: a group
-// publishes the total of its tiles and then its inclusive prefix.
-constexpr int kScanWaves = 4;
-static_assert((kScanWaves + 1) * 8 <= (int)kXchgStride, "a group's exchange values fit its line");
-constexpr size_t groups_for(size_t ntiles) { return (ntiles + kScanWaves - 1) / kScanWaves; }
-constexpr size_t group_tile(size_t group, unsigned wave) { return group * kScanWaves + wave; }
+// Tiles run in workgroups of W waves, one tile per wave: wave w of workgroup g scans tile g W + w
+// (waves past the last tile load and store nothing). The waves' totals meet in the workgroup, and
+// the look-back state (a slot per published value) is per workgroup: a group publishes the total
+// of its tiles and then its inclusive prefix. W = 4, and 8 for 8-byte inputs, whose tiles hold
+// half the elements of 4-byte ones, so that twice as many look-backs would trail the stream (i64
+// 2^26: 199.8 us with four waves, 187.3 with eight; f32 100.8 with four, 112.6 with eight, 109.7
+// with two; f16 77.5 / 83.1 / 87.2).
+constexpr int kScanWavesMax = 8;
+constexpr int scan_waves(int in_bytes) { return in_bytes == 8 ? 8 : 4; }
+static_assert((kScanWavesMax + 1) * 8 <= (int)kXchgStride, "a group's exchange values fit its line");
+constexpr size_t groups_for(size_t ntiles, int waves) { return (ntiles + waves - 1) / waves; }
+constexpr size_t group_tile(size_t group, unsigned wave, int waves) { return group * waves + wave; }
 
 // 64-bit word w of group (slot) t's slot (NW words per slot).
 constexpr size_t slot_word(size_t tile, int nw, unsigned w) { return tile * (size_t)nw + w; }

@@ -3,7 +3,7 @@
 // Uses the same constexpr functions the kernels and their launcher use
 // (amd-incstinct-labs_amd/csrc/scan_layout.hpp) and walks, for each element type, tile size and
 // input size given, every vector / element load and store of every lane of every tile (tiles in
-// groups of kScanWaves waves, the last group's extra waves touching nothing), every slot word a
+// groups of scan_waves(input bytes) waves, the last group's extra waves touching nothing), every slot word a
 // tile group publishes or reads during its look-back, the header words and the tail's reads, checking each against the sizes of the input, output and workspace buffers (the
 // workspace sized as cdna3_scan_workspace_size sizes it). Both the aligned (16-byte vector) and the
 // misaligned (element-wise, half-size tiles) paths are replayed.
@@ -58,7 +58,8 @@ static void replay(const Type& T, int U, size_t n, size_t in_off) {
     const size_t TILE = sl::tile_elems(VEC, u);
     const size_t in_end = in_off + n * (size_t)T.in_bytes;   // bytes of the input buffer from its 16-byte base
     const size_t out_end = n * (size_t)T.out_bytes;
-    const size_t ngroups = sl::groups_for(ntiles);
+    const int waves = sl::scan_waves(T.in_bytes);
+    const size_t ngroups = sl::groups_for(ntiles, waves);
     const size_t slot_bytes = ngroups * (size_t)T.NW * 8;
     CHECK(ngroups <= ws_tiles, "%s U%d n%zu: %zu groups, workspace sized for %zu", T.name, U, n, ngroups, ws_tiles);
     CHECK(sl::agg_offset() >= 4 && sl::agg_offset() + slot_bytes <= sl::pre_offset(ngroups), "%s n%zu agg", T.name, n);
@@ -68,8 +69,8 @@ static void replay(const Type& T, int U, size_t n, size_t in_off) {
     // every wave of every group maps to one tile; exactly the tiles below ntiles are live
     size_t live_tiles = 0;
     for (size_t g = 0; g < ngroups; ++g)
-        for (unsigned wv = 0; wv < (unsigned)sl::kScanWaves; ++wv)
-            if (sl::group_tile(g, wv) < ntiles) ++live_tiles;
+        for (unsigned wv = 0; wv < (unsigned)waves; ++wv)
+            if (sl::group_tile(g, wv, waves) < ntiles) ++live_tiles;
     CHECK(live_tiles == ntiles, "%s n%zu: groups cover %zu of %zu tiles", T.name, n, live_tiles, ntiles);
     for (size_t t = 0; t < ntiles; ++t) {
         const size_t base = sl::tile_base(t, TILE);
@@ -103,10 +104,11 @@ static void replay(const Type& T, int U, size_t n, size_t in_off) {
         }
     }
     for (size_t t = 0; t < ngroups; ++t) {
-        // the group's exchange line: kScanWaves tile totals and the group prefix, 8 bytes each at most
+        // the group's exchange line: its waves' tile totals and the group prefix, 8 bytes each at most
         const size_t x0 = sl::xchg_offset(ngroups) + t * sl::kXchgStride;
         CHECK(x0 >= sl::pre_offset(ngroups) + slot_bytes && x0 % 128 == 0, "%s n%zu exchange line %zu", T.name, n, t);
-        CHECK(x0 + (size_t)(sl::kScanWaves + 1) * 8 <= ws, "%s n%zu exchange line %zu past the workspace", T.name, n, t);
+        CHECK(x0 + (size_t)(waves + 1) * 8 <= ws && (waves + 1) * 8 <= (int)sl::kXchgStride,
+              "%s n%zu exchange line %zu past the workspace or its line", T.name, n, t);
         // publish: lanes 0 .. NW-1 of wave 0 write the words of group t's slot in both arrays
         for (unsigned w = 0; w < (unsigned)T.NW; ++w)
             CHECK((sl::slot_word(t, T.NW, w) + 1) * 8 <= slot_bytes, "%s n%zu publish group %zu", T.name, n, t);
