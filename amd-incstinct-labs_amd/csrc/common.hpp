@@ -27,6 +27,25 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// Rotate-half RoPE of one (d, d + D/2) pair of fp16 values with the pair's cos/sin entries
+// (shared by the fused RoPE + append kernel and the prompt GEMM's Q|K|V epilogue, so both round
+// alike).
+__device__ __forceinline__ void rope_pair(uint32_t a_bits, uint32_t b_bits, float c_lo, float s_lo, float c_hi,
+                                          float s_hi, uint32_t& lo, uint32_t& hi) {
+    const float a = f16_bits_to_f32(a_bits), b = f16_bits_to_f32(b_bits);
+    lo = f32_to_f16_bits(a * c_lo + (-b) * s_lo);
+    hi = f32_to_f16_bits(b * c_hi + a * s_hi);
+}
+
+// Destinations of the prompt GEMM's Q|K|V epilogue (gemm.hip, llm_gemm_qkv_rope): queries
+// head-major [QD / D][T][D], keys and values into the caches [heads][max_seq][D] at rows
+// pos0 .. pos0 + T - 1, cos/sin tables [position][D].
+struct QkvOut {
+    uint16_t *q_out, *Kc, *Vc;
+    const float *cosv, *sinv;
+    int QD, KVD, D, T, pos0, max_seq;
+};
+
 // ---- host side ------------------------------------------------------------------
 // 0 when the current device is gfx950, else CDNA4_ERR_INVALID_DEVICE_FUNCTION or the
 // runtime error. The answer is cached per device ordinal.

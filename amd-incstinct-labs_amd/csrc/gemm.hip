@@ -79,11 +79,19 @@ __device__ __forceinline__ void tile_of(int b, int tm, int tn, int& mt, int& nt)
 // fp16 = fp16(silu(X Wg^T) * (X Wu^T)) in fp32, the rounding the separate silu_mul kernel applies
 // to the fp32 product. A kSilu tile of BN rows takes BN / 2 gate rows and the BN / 2 up rows of the
 // same output columns, so a lane holds both values of its columns.
-enum { kOutF16 = 0, kOutF32 = 1, kOutSilu = 2 };
+enum { kOutF16 = 0, kOutF32 = 1, kOutSilu = 2, kOutQKV = 3 };
+
+// kOutQKV: the prompt's Q|K|V projection (columns [0, QD) query heads, [QD, QD + KVD) key heads,
+// the rest value heads, D columns each) with the runtime's RoPE + append in the epilogue: each
+// value is rounded to fp16 as the projection's output, the (d, d + D/2) pairs of query and key
+// heads rotated with the cos/sin rows of positions pos0 + m (rope_pair, as the separate append
+// kernel does), queries written head-major to q_out [QD / D][T][D] and keys and values into the
+// caches [heads][max_seq][D] at row pos0 + m. Tiles are whole heads (BN % D == 0), so a lane holds
+// both columns of its pairs: block i and block i + D / 64 (32 columns per block).
 
 template <int BM, int BN, int kOut, bool kAccum>
 __global__ __launch_bounds__(256) void gemm_ring(const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
-                                                 void* __restrict__ Y, int M, int N, int K, int ldy) {
+                                                 void* __restrict__ Y, int M, int N, int K, int ldy, QkvOut qe) {
     static_assert(BM % 32 == 0 && BN % 32 == 0, "tiles are whole 32-row groups");
     static_assert(kOut != kOutSilu || (BN % 64 == 0 && !kAccum), "a SiLU tile pairs whole gate and up groups");
     constexpr bool kSilu = kOut == kOutSilu;
@@ -175,6 +183,44 @@ __global__ __launch_bounds__(256) void gemm_ring(const uint16_t* __restrict__ X,
 
     // acc[i][j] lane (li, g): Y[m][n .. n + 3], m = m0 + 32 j + r0 + 4 wm, n = n0 + 32 i + 8 g + 4 wn
     // (kSilu: gate group i < FN / 2 and up group i + FN / 2 hold the same columns n).
+    if constexpr (kOut == kOutQKV) {
+        const int hb = qe.D / 64;   // blocks per half head
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+            const int m = m0 + 32 * j + r0 + 4 * wm;
+            if (m >= M) continue;
+            const float* cr = qe.cosv + (size_t)(qe.pos0 + m) * qe.D;
+            const float* sr = qe.sinv + (size_t)(qe.pos0 + m) * qe.D;
+#pragma unroll
+            for (int i = 0; i < FN; ++i) {
+                if ((i / hb) % 2) continue;   // block i in the second half of its head: done with its partner
+                const int n = n0 + 32 * i + 8 * g + 4 * wn;   // a first-half column; n + D / 2 its partner
+                if (n >= ncols) continue;
+                const int d = n % qe.D, half = qe.D / 2;
+                const gf32x4 va = acc[i][j], vb = acc[(i + hb) % FN][j];
+                uint32_t lo[4], hi[4];
+                uint16_t* dst;
+                if (n < qe.QD + qe.KVD) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        rope_pair(f32_to_f16_bits(va[e]), f32_to_f16_bits(vb[e]), cr[d + e], sr[d + e],
+                                  cr[d + e + half], sr[d + e + half], lo[e], hi[e]);
+                    dst = n < qe.QD ? qe.q_out + ((size_t)(n / qe.D) * qe.T + m) * qe.D
+                                    : qe.Kc + ((size_t)((n - qe.QD) / qe.D) * qe.max_seq + qe.pos0 + m) * qe.D;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        lo[e] = f32_to_f16_bits(va[e]);
+                        hi[e] = f32_to_f16_bits(vb[e]);
+                    }
+                    dst = qe.Vc + ((size_t)((n - qe.QD - qe.KVD) / qe.D) * qe.max_seq + qe.pos0 + m) * qe.D;
+                }
+                *(u32x2*)(dst + d) = u32x2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+                *(u32x2*)(dst + d + half) = u32x2{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
         const int m = m0 + 32 * j + r0 + 4 * wm;
@@ -211,11 +257,11 @@ int gemm_launch(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, bool 
                 hipStream_t s) {
     const unsigned grid = ceil_div((size_t)M, BM) * ceil_div((size_t)N, BN);
     if (y_f32) {
-        if (accum) gemm_ring<BM, BN, kOutF32, true><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
-        else gemm_ring<BM, BN, kOutF32, false><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
+        if (accum) gemm_ring<BM, BN, kOutF32, true><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy, QkvOut{});
+        else gemm_ring<BM, BN, kOutF32, false><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy, QkvOut{});
     } else {
-        if (accum) gemm_ring<BM, BN, kOutF16, true><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
-        else gemm_ring<BM, BN, kOutF16, false><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy);
+        if (accum) gemm_ring<BM, BN, kOutF16, true><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy, QkvOut{});
+        else gemm_ring<BM, BN, kOutF16, false><<<grid, 256, 0, s>>>(X, W, Y, M, N, K, ldy, QkvOut{});
     }
     return launch_status();
 }
@@ -223,7 +269,7 @@ int gemm_launch(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, bool 
 template <int BM, int BN>
 int gemm_silu_launch(const uint16_t* X, const uint16_t* W, void* Y, int M, int F, int K, int ldy, hipStream_t s) {
     const unsigned grid = ceil_div((size_t)M, BM) * ceil_div((size_t)F, BN / 2);
-    gemm_ring<BM, BN, kOutSilu, false><<<grid, 256, 0, s>>>(X, W, Y, M, 2 * F, K, ldy);
+    gemm_ring<BM, BN, kOutSilu, false><<<grid, 256, 0, s>>>(X, W, Y, M, 2 * F, K, ldy, QkvOut{});
     return launch_status();
 }
 
@@ -276,6 +322,43 @@ int llm_gemm_f16(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, bool
     CDNA4_GEMM_TILE(32, 32) CDNA4_GEMM_TILE(64, 64) CDNA4_GEMM_TILE(64, 96) CDNA4_GEMM_TILE(64, 128)
     CDNA4_GEMM_TILE(128, 64) CDNA4_GEMM_TILE(128, 96) CDNA4_GEMM_TILE(128, 128)
 #undef CDNA4_GEMM_TILE
+    return -1;
+}
+
+// The prompt's Q|K|V projection X [M][K] x W [QD + 2 KVD][K]^T with the RoPE + append epilogue
+// (kOutQKV; q_out, K and V caches as QkvOut describes, cos/sin tables [max_seq][D]). Tiles of
+// whole heads only (BN % D == 0, D % 64 == 0): the tile of the single-pass menu with the least
+// estimate among those. Returns -1, launching nothing, for shapes it does not take (the runtime
+// then projects with llm_gemm_f16 and appends separately).
+int llm_gemm_qkv_rope(const uint16_t* X, const uint16_t* W, int M, int K, const QkvOut& qe, hipStream_t s) {
+    const int N = qe.QD + 2 * qe.KVD;
+    if (M <= 0 || K <= 0 || K % kKMul || qe.D % 64 || qe.QD % qe.D || qe.KVD % qe.D) return -1;
+    if (((uintptr_t)X | (uintptr_t)W) % 16 || ((uintptr_t)qe.q_out | (uintptr_t)qe.Kc | (uintptr_t)qe.Vc) % 8) return -1;
+    if ((uint64_t)M * K * 2 >= (1ull << 32) || (uint64_t)N * K * 2 >= (1ull << 32)) return -1;
+    const int cus = device_cus() > 0 ? device_cus() : 256;
+    Tile best = {0, 0};
+    double best_t = 1e300;
+    for (const Tile& t : kTiles) {
+        if (t.bn % qe.D || t.bn % 64) continue;
+        const int lds = ring_stages(t.bm, t.bn) * (t.bm + t.bn) * kRowBytes;
+        const int per_cu = (160 * 1024) / lds >= 2 ? 2 : 1;
+        const double tiles = (double)ceil_div((size_t)M, t.bm) * ceil_div((size_t)N, t.bn);
+        const double wg = (double)(K / kBK) * kStageUs + (double)(t.bm + t.bn) * K * 2 / kCuBytesPerUs +
+                          2.0 * t.bm * t.bn * K / kCuFlopsPerUs;
+        const double est = ceil(tiles / ((double)cus * per_cu)) * wg;
+        if (est < best_t) {
+            best_t = est;
+            best = t;
+        }
+    }
+    const unsigned grid = ceil_div((size_t)M, best.bm) * ceil_div((size_t)N, best.bn);
+#define CDNA4_QKV_TILE(a, b)                                                                              \
+    if (best.bm == a && best.bn == b) {                                                                     \
+        gemm_ring<a, b, kOutQKV, false><<<grid, 256, 0, s>>>(X, W, nullptr, M, N, K, N, qe);                \
+        return launch_status();                                                                             \
+    }
+    CDNA4_QKV_TILE(64, 64) CDNA4_QKV_TILE(64, 128) CDNA4_QKV_TILE(128, 64) CDNA4_QKV_TILE(128, 128)
+#undef CDNA4_QKV_TILE
     return -1;
 }
 

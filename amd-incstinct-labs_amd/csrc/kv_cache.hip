@@ -16,14 +16,6 @@
 namespace cdna4 {
 namespace {
 
-// Rotate-half of one (d, d + D/2) pair of fp16 values with the pair's cos/sin entries.
-__device__ __forceinline__ void rope_pair(uint32_t a_bits, uint32_t b_bits, float c_lo, float s_lo, float c_hi,
-                                          float s_hi, uint32_t& lo, uint32_t& hi) {
-    const float a = f16_bits_to_f32(a_bits), b = f16_bits_to_f32(b_bits);
-    lo = f32_to_f16_bits(a * c_lo + (-b) * s_lo);
-    hi = f32_to_f16_bits(b * c_hi + a * s_hi);
-}
-
 // cache[h][pos0 + s][:] = src[s][h][:], 16 bytes per lane (D % 8 == 0).
 __global__ __launch_bounds__(256) void scatter_vec(const u32x4* __restrict__ src, u32x4* __restrict__ cache, int T,
                                                    int heads, int D, int pos0, int max_seq) {

@@ -70,6 +70,7 @@ int attn_decode_partials(const void* q, const void* K, const void* V, const cdna
                          void* ws, size_t ws_bytes, const int* len_pos, hipStream_t s);
 int llm_gemm_f16(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, bool accum, int M, int N, int K, int ldy,
                  hipStream_t s);
+int llm_gemm_qkv_rope(const uint16_t* X, const uint16_t* W, int M, int K, const QkvOut& qe, hipStream_t s);
 int llm_gemm_f16_silu(const uint16_t* X, const uint16_t* W, void* Y, int M, int F, int K, int ldy, hipStream_t s);
 int llm_bias_add_f16(void* Y, const void* b, int T, int N, hipStream_t s);
 int kv_rope_append(const void* q, const void* k, const void* v, long long ldq, long long ldk, long long ldv,
@@ -164,6 +165,7 @@ struct Session {
     int* dstate = nullptr;
     bool use_graph = true;
     bool rocblas_only = false;   // CDNA4_SESSION_ROCBLAS=1: prompt GEMMs through rocBLAS only
+    bool qkv_fused = true;       // CDNA4_SESSION_QKV_FUSED=0: prompt Q|K|V GEMM, then the separate append
     // Decode steps over a short cache (the one-launch attention plan): the attention runs as
     // attn_parts split-K partials per head, merged by the O-projection GEMV (0: the one-launch
     // attention and a plain GEMV). CDNA4_SESSION_ATTN_PARTS overrides it (0 .. 4). At config 5
@@ -388,12 +390,23 @@ int Session::run_layers(int T, int pos0, const int* pos_dev) {
             continue;
         }
         CK(llm_norm_cast(lnorm, hidden, l.n_attn, l.n_attn_b, xn, T, H, eps, stream));
-        // one GEMM for Q|K|V: row t of q is [q_t | k_t | v_t], QKVD = QD + 2 KVD wide
+        // one GEMM for Q|K|V: row t of q is [q_t | k_t | v_t], QKVD = QD + 2 KVD wide. Without a
+        // bias, the GEMM's epilogue rotates Q and K and writes Q head-major and K/V into the cache
+        // (the separate append below rounds and rotates alike).
         const int QKVD = QD + 2 * KVD;
-        CK(gemm(xn, l.wqkv, q, false, 0.f, T, QKVD, H, QKVD));
-        if (l.bqkv) CK(llm_bias_add_f16(q, l.bqkv, T, QKVD, stream));
-        CK(kv_rope_append(q, q + QD, q + QD + KVD, QKVD, QKVD, QKVD, qh, Kl, Vl, cos_tab + (size_t)pos0 * D,
-                          sin_tab + (size_t)pos0 * D, T, nH, nKV, D, pos0, max_seq, stream));
+        int qkv = -1;
+        if (!l.bqkv && !rocblas_only && qkv_fused) {
+            const QkvOut qe{qh, Kl, Vl, cos_tab, sin_tab, QD, KVD, D, T, pos0, max_seq};
+            qkv = llm_gemm_qkv_rope(xn, l.wqkv, T, H, qe, stream);
+        }
+        if (qkv == -1) {
+            CK(gemm(xn, l.wqkv, q, false, 0.f, T, QKVD, H, QKVD));
+            if (l.bqkv) CK(llm_bias_add_f16(q, l.bqkv, T, QKVD, stream));
+            CK(kv_rope_append(q, q + QD, q + QD + KVD, QKVD, QKVD, QKVD, qh, Kl, Vl, cos_tab + (size_t)pos0 * D,
+                              sin_tab + (size_t)pos0 * D, T, nH, nKV, D, pos0, max_seq, stream));
+        } else {
+            CK(qkv);
+        }
         // Prompt from an empty cache (pos0 == 0): causal over the T cached keys, read in place;
         // O written token-major for the O projection.
         cdna3_prefill_cfg pc{D, T, T, nH, nKV, 1, 1};
@@ -502,6 +515,8 @@ extern "C" int cdna3_session_create(const char* model_dir, int max_seq, cdna3_se
         s->impl.use_graph = !(g && g[0] == '0' && g[1] == 0);
         const char* rb = getenv("CDNA4_SESSION_ROCBLAS");
         s->impl.rocblas_only = rb && rb[0] == '1' && rb[1] == 0;
+        const char* qf = getenv("CDNA4_SESSION_QKV_FUSED");
+        s->impl.qkv_fused = !(qf && qf[0] == '0' && qf[1] == 0);
         const char* ap = getenv("CDNA4_SESSION_ATTN_PARTS");
         if (ap && ap[0] >= '0' && ap[0] <= '4' && ap[1] == 0) s->impl.attn_parts = ap[0] - '0';
         e = s->impl.read_config(model_dir);

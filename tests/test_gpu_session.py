@@ -125,6 +125,21 @@ def test_decode_attention_partials_match_oracle(model, monkeypatch, n, new, part
     _check_generation(meta, t, ids, out, 256, what=f"decode attention in {parts} partials")
 
 
+def test_prompt_qkv_epilogue_equals_separate_append(model, monkeypatch):
+    # Models without a Q|K|V bias project the prompt with RoPE and the cache append in the GEMM's
+    # epilogue; CDNA4_SESSION_QKV_FUSED=0 runs the same GEMM with its plain output and the separate
+    # append kernel. Both round each value to fp16 and rotate it alike: identical tokens and logits.
+    d, meta, t = model
+    ids = _prompt(meta, 77, 9)
+    outs = []
+    for fused in ("1", "0"):
+        monkeypatch.setenv("CDNA4_SESSION_QKV_FUSED", fused)
+        with cdna4.Session(d, max_seq=128) as s:
+            outs.append(s.generate_ex(ids, cdna4.GenerateCfg(6), with_logits=True))
+    assert outs[0]["tokens"] == outs[1]["tokens"]
+    assert np.array_equal(outs[0]["logits"], outs[1]["logits"])
+
+
 def test_session_reuse_and_plain_generate(model):
     # a second, shorter prompt on the same session sees none of the first one's cache rows
     d, meta, t = model
