@@ -38,9 +38,9 @@ constexpr int kKMul = kBK;     // K must be a multiple of this
 constexpr int kRowBytes = kBK * 2;
 constexpr int kLdsBudget = 128 * 1024;
 
-// Ring depth for a BM x BN tile: as many stages as kLdsBudget holds, at most 8.
-constexpr int ring_stages(int bm, int bn) {
-    const int s = kLdsBudget / ((bm + bn) * kRowBytes);
+// Ring depth for a BM x BN tile: as many stages as the LDS budget holds, at most 8.
+constexpr int ring_stages(int bm, int bn, int budget = kLdsBudget) {
+    const int s = budget / ((bm + bn) * kRowBytes);
     return s > 8 ? 8 : s;
 }
 
@@ -81,6 +81,12 @@ __device__ __forceinline__ void tile_of(int b, int tm, int tn, int& mt, int& nt)
 // same output columns, so a lane holds both values of its columns.
 enum { kOutF16 = 0, kOutF32 = 1, kOutSilu = 2, kOutQKV = 3 };
 
+// LDS budget of a tile's ring. The Q|K|V epilogue's 64 x 64 tiles take 64 KiB (four stages), so
+// two workgroups share a CU: at config 5 (512 x 2304 x 768) that ran the projection + append in a
+// time to first token of 0.770 ms against 0.804 with eight stages and one workgroup per CU, and
+// 0.788 with the 64 x 128 tile.
+constexpr int ring_budget(int kOut, int bm, int bn) { return kOut == kOutQKV && bm + bn <= 128 ? 64 * 1024 : kLdsBudget; }
+
 // kOutQKV: the prompt's Q|K|V projection (columns [0, QD) query heads, [QD, QD + KVD) key heads,
 // the rest value heads, D columns each) with the runtime's RoPE + append in the epilogue: each
 // value is rounded to fp16 as the projection's output, the (d, d + D/2) pairs of query and key
@@ -97,7 +103,7 @@ __global__ __launch_bounds__(256) void gemm_ring(const uint16_t* __restrict__ X,
     constexpr bool kSilu = kOut == kOutSilu;
     constexpr int kTileCols = kSilu ? BN / 2 : BN;   // output columns per tile
     const int ncols = kSilu ? N / 2 : N;              // output columns (F for kSilu)
-    constexpr int S = ring_stages(BM, BN);
+    constexpr int S = ring_stages(BM, BN, ring_budget(kOut, BM, BN));
     constexpr int FM = BM / 32, FN = BN / 32;        // 16-row blocks per wave: X (m), W (n)
     constexpr int kStage = (BN + BM) * kRowBytes;    // bytes per ring stage
     constexpr int kCopies = (BN + BM) / 8;           // 1 KB copy instructions per stage
@@ -340,7 +346,7 @@ int llm_gemm_qkv_rope(const uint16_t* X, const uint16_t* W, int M, int K, const 
     double best_t = 1e300;
     for (const Tile& t : kTiles) {
         if (t.bn % qe.D || t.bn % 64) continue;
-        const int lds = ring_stages(t.bm, t.bn) * (t.bm + t.bn) * kRowBytes;
+        const int lds = ring_stages(t.bm, t.bn, ring_budget(kOutQKV, t.bm, t.bn)) * (t.bm + t.bn) * kRowBytes;
         const int per_cu = (160 * 1024) / lds >= 2 ? 2 : 1;
         const double tiles = (double)ceil_div((size_t)M, t.bm) * ceil_div((size_t)N, t.bn);
         const double wg = (double)(K / kBK) * kStageUs + (double)(t.bm + t.bn) * K * 2 / kCuBytesPerUs +
