@@ -85,7 +85,11 @@ enum { kOutF16 = 0, kOutF32 = 1, kOutSilu = 2, kOutQKV = 3 };
 // two workgroups share a CU: at config 5 (512 x 2304 x 768) that ran the projection + append in a
 // time to first token of 0.770 ms against 0.804 with eight stages and one workgroup per CU, and
 // 0.788 with the 64 x 128 tile.
-constexpr int ring_budget(int kOut, int bm, int bn) { return kOut == kOutQKV && bm + bn <= 128 ? 64 * 1024 : kLdsBudget; }
+// 64 x 32 tiles (the runtime's residual projections, llm_gemm_f16 with cold operands) likewise
+// take 64 KiB (five stages), two workgroups per CU.
+constexpr int ring_budget(int kOut, int bm, int bn) {
+    return (kOut == kOutQKV && bm + bn <= 128) || (bm == 64 && bn == 32) ? 64 * 1024 : kLdsBudget;
+}
 
 // kOutQKV: the prompt's Q|K|V projection (columns [0, QD) query heads, [QD, QD + KVD) key heads,
 // the rest value heads, D columns each) with the runtime's RoPE + append in the epilogue: each
@@ -316,17 +320,26 @@ Tile pick_tile(int M, int N, int K, int cus, bool silu = false) {
 // Returns -1, launching nothing, for a shape this kernel does not take (K not a multiple of 64,
 // N or ldy not a multiple of 4, X / W not 16-byte or Y not 16- (fp32) / 8-byte (fp16) aligned,
 // operands past 4 GiB); the caller then uses rocBLAS. Otherwise 0 or the launch's error.
+// cold: the operands arrive from HBM or the Infinity Cache, not L2 (the runtime's prompt, where
+// each GEMM reads the previous kernel's output and a layer's weights once). There a 32 x 32 pick
+// becomes 64 x 32 (half the W re-reads, five-stage ring, two workgroups per CU): at config 5 the
+// O and down projections took the time to first token from 0.767 to 0.733 ms, though launched
+// back to back on the same operands (all in L2) 64 x 32 ran no faster (O 5.9 against 6.0 us,
+// down 14.1 against 13.7).
 int llm_gemm_f16(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, bool accum, int M, int N, int K, int ldy,
-                 hipStream_t s) {
+                 hipStream_t s, bool cold) {
     if (M <= 0 || N <= 0 || K <= 0 || K % kKMul || N % 4 || ldy % 4 || ldy < N) return -1;
     if (((uintptr_t)X | (uintptr_t)W) % 16 || (uintptr_t)Y % (y_f32 ? 16 : 8)) return -1;
     if ((uint64_t)M * K * 2 >= (1ull << 32) || (uint64_t)N * K * 2 >= (1ull << 32)) return -1;   // 32-bit copy offsets
     const int cus = device_cus() > 0 ? device_cus() : 256;
-    const Tile t = pick_tile(M, N, K, cus);
+    Tile t = pick_tile(M, N, K, cus);
+    if (cold && t.bm == 32 && t.bn == 32 && M >= 64 &&
+        (double)ceil_div((size_t)M, 64) * ceil_div((size_t)N, 32) <= 2.0 * cus)
+        t = Tile{64, 32};
 #define CDNA4_GEMM_TILE(a, b) \
     if (t.bm == a && t.bn == b) return gemm_launch<a, b>(X, W, Y, y_f32, accum, M, N, K, ldy, s);
-    CDNA4_GEMM_TILE(32, 32) CDNA4_GEMM_TILE(64, 64) CDNA4_GEMM_TILE(64, 96) CDNA4_GEMM_TILE(64, 128)
-    CDNA4_GEMM_TILE(128, 64) CDNA4_GEMM_TILE(128, 96) CDNA4_GEMM_TILE(128, 128)
+    CDNA4_GEMM_TILE(32, 32) CDNA4_GEMM_TILE(64, 32) CDNA4_GEMM_TILE(64, 64) CDNA4_GEMM_TILE(64, 96)
+    CDNA4_GEMM_TILE(64, 128) CDNA4_GEMM_TILE(128, 64) CDNA4_GEMM_TILE(128, 96) CDNA4_GEMM_TILE(128, 128)
 #undef CDNA4_GEMM_TILE
     return -1;
 }
@@ -419,6 +432,6 @@ extern "C" int cdna4_gemm_f16_nt(const void* X, const void* W, void* Y, int y_f3
     if (!X || !W || !Y) return CDNA4_ERR_INVALID_VALUE;
     if (int e = cdna4::check_device()) return e;
     const int e = cdna4::llm_gemm_f16((const uint16_t*)X, (const uint16_t*)W, Y, y_f32 == 1, accum == 1, M, N, K, ldy,
-                                      (hipStream_t)stream);
+                                      (hipStream_t)stream, false);
     return e == -1 ? CDNA4_ERR_INVALID_VALUE : e;
 }

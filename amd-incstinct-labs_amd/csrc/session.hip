@@ -69,7 +69,7 @@ size_t attn_decode_partials_bytes(const cdna3_decode_cfg& c, int P);
 int attn_decode_partials(const void* q, const void* K, const void* V, const cdna3_decode_cfg& c, int dtype, int P,
                          void* ws, size_t ws_bytes, const int* len_pos, hipStream_t s);
 int llm_gemm_f16(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, bool accum, int M, int N, int K, int ldy,
-                 hipStream_t s);
+                 hipStream_t s, bool cold);
 int llm_gemm_qkv_rope(const uint16_t* X, const uint16_t* W, int M, int K, const QkvOut& qe, hipStream_t s);
 int llm_gemm_f16_silu(const uint16_t* X, const uint16_t* W, void* Y, int M, int F, int K, int ldy, hipStream_t s);
 int llm_bias_add_f16(void* Y, const void* b, int T, int N, hipStream_t s);
@@ -335,13 +335,15 @@ int Session::reserve(int T) {
 // and Y^T = W X^T, where the row-major W [N][K] read column-major is W^T (so op(A) = transpose,
 // lda = K) and the row-major X [M][K] read column-major is X^T (op(B) = none, ldb = K). The
 // reference derives the same call (rocblas_gemm.hpp:8-20). The library's MFMA GEMM (gemm.hip)
-// takes every product whose shape it allows; at the cfg5 prompt (T 512, under the kernel trace)
-// it measured Q|K|V 8.3 us, O ~5, gate|up 12.4, down 13.7 against rocBLAS's 16.8, 10.5, 14.8 and
-// 16.5. rocBLAS serves the rest (and everything with CDNA4_SESSION_ROCBLAS=1).
+// takes every product whose shape it allows, told that its operands arrive cold (from HBM or the
+// Infinity Cache: the residual projections then take 64 x 32 tiles); at the cfg5 prompt (T 512,
+// under the kernel trace) it measured Q|K|V 8.3 us, O ~5, gate|up 12.4, down 13.7 against
+// rocBLAS's 16.8, 10.5, 14.8 and 16.5. rocBLAS serves the rest (and everything with
+// CDNA4_SESSION_ROCBLAS=1).
 int Session::gemm(const uint16_t* X, const uint16_t* W, void* Y, bool y_f32, float beta, int M, int N, int K,
                   int ldy) {
     if (!rocblas_only && (beta == 0.f || beta == 1.f)) {
-        const int e = llm_gemm_f16(X, W, Y, y_f32, beta == 1.f, M, N, K, ldy, stream);
+        const int e = llm_gemm_f16(X, W, Y, y_f32, beta == 1.f, M, N, K, ldy, stream, true);   // cold operands
         if (e != -1) return e;   // -1: a shape the kernel does not take
     }
     const float alpha = 1.f;
