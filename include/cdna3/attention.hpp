@@ -15,7 +15,7 @@
 //     workgroup per (batch, kv head, group of 16 query heads), so a few long sequences run on
 //     that many CUs. Measured on one MI355X at the reference's decode benchmark shape (batch 1,
 //     32 q / 8 kv heads, D 128, fp16): 74 us at N 8192, 41 us at N 4096. The overloads taking
-//     (workspace, bytes) split long caches over a split-K grid instead: 14.2 / 14.7 us at the
+//     (workspace, bytes) split long caches over a split-K grid instead: 11-14 / 9-15 us at the
 //     same shapes (decode_workspace_size gives the bytes, 1.06 MB there). Use them whenever
 //     batch x nKVHeads is well below the device's CU count.
 // New overloads: bf16 tensors, a batch dimension (DecodeCfg::batch), fp32 prefill, split-K

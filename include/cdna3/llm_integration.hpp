@@ -15,7 +15,7 @@
 // allocation, nothing shared between calls), as the reference's launcher did. That plan runs one
 // workgroup per (kv head, group of 16 query heads): 8 CUs for 32 q / 8 kv heads, 74 us at N 8192
 // (D 128, fp16) on one MI355X. Callers decoding a few long sequences should call
-// cdna3::attn::decode with a workspace (<cdna3/attention.hpp>), 14.2 us at that shape.
+// cdna3::attn::decode with a workspace (<cdna3/attention.hpp>), 11-14 us at that shape.
 #include <hip/hip_runtime_api.h>
 #include <hip/hip_fp16.h>
 #include "../cdna4_attn.h"
