@@ -13,6 +13,9 @@
 //                    waves (one per XCD), each streaming its own 16 MiB through a ring of four
 //                    16 KiB LDS stages (three in flight) with global_load_lds_dwordx4, reported per
 //                    CU; the 128 MiB are re-read every launch, so they come from the Infinity Cache;
+//   lds_dma_nt       the same copy loop on every CU at once, non-temporal (as the decode kernels
+//                    copy K/V), over the 1 GiB buffer: the chip's HBM -> LDS rate, best of one or
+//                    two workgroups per CU;
 // each the median of five timed runs (HIP events), printed as one JSON line. `ceilings mfma S [exp]
 // [f16]` instead runs only one MFMA stream for about S seconds, one line per 50 launches.
 // The buffer reads are 1 GiB, four times the 256 MB Infinity Cache, so no read is served from it.
@@ -63,6 +66,7 @@ __global__ __launch_bounds__(256) void read_stream(const u32x4* __restrict__ p, 
 
 // One workgroup's copy loop of lds_dma_cu: per stage each wave copies 4 KiB (four 1 KiB copies),
 // keeps three stages in flight, and waits for the oldest before issuing the next.
+template <bool kNT>
 __global__ __launch_bounds__(256) void lds_dma(const char* __restrict__ src, size_t per_wg, uint32_t* sink) {
     constexpr int S = 4;
     __shared__ __attribute__((aligned(16))) char lds[S * 16384];
@@ -75,7 +79,10 @@ __global__ __launch_bounds__(256) void lds_dma(const char* __restrict__ src, siz
             const char* g = base + (size_t)c * 16384 + (wave * 4 + j) * 1024 + lane * 16;
             const uint32_t l = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(
                 lds + (c % S) * 16384 + (wave * 4 + j) * 1024);
-            asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(l) : "memory");
+            if constexpr (kNT)
+                asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" : : "v"(g), "{m0}"(l) : "memory");
+            else
+                asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(l) : "memory");
         }
     };
     for (int c = 0; c < S - 1 && c < nch; ++c) issue(c);
@@ -262,16 +269,30 @@ int main(int argc, char** argv) {
     const float h0 = time_ms([&] { launch_mfma<f16x8>(false, cus, sink, iters, fout); }, 5);
     const float h1 = time_ms([&] { launch_mfma<f16x8>(true, cus, sink, iters, fout); }, 5);
     const size_t per_wg = (size_t)16 << 20;
-    const float dm = time_ms([&] { lds_dma<<<8, 256>>>((const char*)a, per_wg, sink + 2048); }, 5);
+    const float dm = time_ms([&] { lds_dma<false><<<8, 256>>>((const char*)a, per_wg, sink + 2048); }, 5);
+    // every CU: each workgroup copies its contiguous share of the 1 GiB buffer (whole 16 KiB stages)
+    float dn = 1e30f;
+    int dn_grid = 0;
+    size_t dn_bytes = 0;
+    for (int per_cu : {1, 2}) {
+        const int grid = cus * per_cu;
+        const size_t share = bytes / grid / 16384 * 16384;
+        const float ms = time_ms([&] { lds_dma<true><<<grid, 256>>>((const char*)a, share, sink + 2048); }, 5);
+        if (share * grid / (ms * 1e-3) > dn_bytes / (dn * 1e-3)) {
+            dn = ms;
+            dn_grid = grid;
+            dn_bytes = share * grid;
+        }
+    }
     CK(hipGetLastError());
     printf("{\"cus\": %d, \"read_nt_GBs\": %.1f, \"read_GBs\": %.1f, \"copy_nt_GBs\": %.1f, "
            "\"mfma_bf16_TFLOPs\": %.1f, \"mfma_bf16_exp_TFLOPs\": %.1f, \"mfma_f16_TFLOPs\": %.1f, "
-           "\"mfma_f16_exp_TFLOPs\": %.1f, \"lds_dma_cu_GBs\": %.1f, "
-           "\"shapes\": {\"read_nt\": [%d, %d], \"read\": [%d, %d], \"copy_nt\": [%d, %d]}}\n",
+           "\"mfma_f16_exp_TFLOPs\": %.1f, \"lds_dma_cu_GBs\": %.1f, \"lds_dma_nt_GBs\": %.1f, "
+           "\"shapes\": {\"read_nt\": [%d, %d], \"read\": [%d, %d], \"copy_nt\": [%d, %d], \"lds_dma_nt\": [%d]}}\n",
            cus, bytes / (r_nt.ms * 1e-3) / 1e9, bytes / (r_df.ms * 1e-3) / 1e9, 2.0 * bytes / (c_nt.ms * 1e-3) / 1e9,
            flop / (m0 * 1e-3) / 1e12, flop / (m1 * 1e-3) / 1e12, flop / (h0 * 1e-3) / 1e12,
-           flop / (h1 * 1e-3) / 1e12, per_wg / (dm * 1e-3) / 1e9, r_nt.grid, r_nt.u, r_df.grid, r_df.u, c_nt.grid,
-           c_nt.u);
+           flop / (h1 * 1e-3) / 1e12, per_wg / (dm * 1e-3) / 1e9, dn_bytes / (dn * 1e-3) / 1e9, r_nt.grid, r_nt.u,
+           r_df.grid, r_df.u, c_nt.grid, c_nt.u, dn_grid);
     CK(hipFree(a));
     CK(hipFree(b));
     CK(hipFree(sink));

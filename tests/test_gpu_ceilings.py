@@ -26,3 +26,4 @@ def test_measured_ceilings():
     assert 2000 < c["copy_nt_GBs"] < 8000
     assert 300 < c["mfma_bf16_TFLOPs"] < 2600 and 300 < c["mfma_bf16_exp_TFLOPs"] < 2600
     assert 10 < c["lds_dma_cu_GBs"] < 1000
+    assert 2000 < c["lds_dma_nt_GBs"] < 8000
