@@ -241,17 +241,19 @@ def test_prefill_strided_rows_4gib_apart():
 
 # ---- BASELINE config 3 at full size: every head of batches 0 and 3 -------------------------------
 
-def test_prefill_config3_subsample_every_head_of_batches_0_and_3():
-    # B4 H32 S8192 D128 causal bf16 N(0,1); rows 0..127, 4095, 8191 and 256 seeded random rows.
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_config3_subsample_every_head_of_batches_0_and_3(dtype):
+    # B4 H32 S8192 D128 causal N(0,1), bf16 (the config) and fp16 (the bench's prefill_fp16 leg);
+    # rows 0..127, 4095, 8191 and 256 seeded random rows.
     B, H, S, D = 4, 32, 8192, 128
     cfg = cdna4.PrefillCfg(D, S, S, H, H, B, 1)
-    plan = cdna4.prefill_plan(cfg, torch.bfloat16)
-    print(f"config 3 -> {plan.name} (grid {plan.grid})", flush=True)
+    plan = cdna4.prefill_plan(cfg, dtype)
+    print(f"config 3 ({dtype}) -> {plan.name} (grid {plan.grid})", flush=True)
     assert plan.name == "fa_mfma_8w"
     g = torch.Generator(device=DEV).manual_seed(2024)
-    Q = _randn((B, H, S, D), torch.bfloat16, g)
-    K = _randn((B, H, S, D), torch.bfloat16, g)
-    V = _randn((B, H, S, D), torch.bfloat16, g)
+    Q = _randn((B, H, S, D), dtype, g)
+    K = _randn((B, H, S, D), dtype, g)
+    V = _randn((B, H, S, D), dtype, g)
     O = torch.full_like(Q, float("nan"))
     cdna4.prefill(Q, K, V, O, cfg)
     torch.cuda.synchronize()
@@ -265,8 +267,9 @@ def test_prefill_config3_subsample_every_head_of_batches_0_and_3():
         gots += [o[h, rows] for h in range(H)]
         wants += [want[(0, h)] for h in range(H)]
         print(f"  batch {b} done", flush=True)
-    check_parity(gots, wants, torch.bfloat16,
-                 what=f"cfg3 (B4 H32 S8192 D128 causal bf16), every head of batches 0 and 3 x {len(rows)} rows")
+    name = "bf16" if dtype == torch.bfloat16 else "fp16"
+    check_parity(gots, wants, dtype,
+                 what=f"cfg3 (B4 H32 S8192 D128 causal {name}), every head of batches 0 and 3 x {len(rows)} rows")
 
 
 # ---- decode: split-K grid (decode_mfma + decode_merge) and the one-launch plan --------------------
