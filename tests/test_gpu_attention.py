@@ -179,34 +179,37 @@ def test_decode_full_size_config_and_split_invariance():
     assert torch.isfinite(o.float()).all()
 
 
-def test_decode_full_size_config_on_the_split_k_plan(monkeypatch):
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_full_size_config_on_the_split_k_plan(monkeypatch, dtype):
     # BASELINE config 4 names split-K across workgroups with a DPP final reduce: the same shape on
-    # that plan (forced; the one-launch plan is the default on a 256-CU part), against the oracle.
+    # that plan (forced; the one-launch plan is the default on a 256-CU part), against the oracle;
+    # fp16 as the config, and bf16 at the same size.
     B, HQ, HK, D, N = 32, 32, 8, 128, 8192
     monkeypatch.setenv("CDNA4_DECODE_SPLIT_K", "1")
     torch.manual_seed(2)
-    q = torch.randn(B, HQ, D, device=DEV, dtype=torch.float16)
-    K = torch.randn(B, HK, N, D, device=DEV, dtype=torch.float16)
-    V = torch.randn(B, HK, N, D, device=DEV, dtype=torch.float16)
+    q = torch.randn(B, HQ, D, device=DEV, dtype=dtype)
+    K = torch.randn(B, HK, N, D, device=DEV, dtype=dtype)
+    V = torch.randn(B, HK, N, D, device=DEV, dtype=dtype)
     checked = [1, 30]
     hostv = {}
     for i, b in enumerate(checked):
         vals = []
         for j, (T, shape) in enumerate(((q, (HQ, D)), (K, (HK, N, D)), (V, (HK, N, D)))):
-            x, t = rounded(oracle.normal(700 + 3 * i + j, int(np.prod(shape))), torch.float16)
+            x, t = rounded(oracle.normal(700 + 3 * i + j, int(np.prod(shape))), dtype)
             T[b] = t.reshape(shape)
             vals.append(x)
         hostv[b] = vals
     cfg = cdna4.DecodeCfg(D, N, HQ, HK, B)
-    plan = cdna4.decode_plan(cfg, torch.float16, with_workspace=True)
-    print(f"config-4 forced plan: {plan.name}", flush=True)
+    plan = cdna4.decode_plan(cfg, dtype, with_workspace=True)
+    print(f"config-4 forced plan ({dtype}): {plan.name}", flush=True)
     assert plan.name == "decode_split"
     ws = torch.empty(cdna4.decode_workspace_size(cfg), dtype=torch.uint8, device=DEV)
     o = torch.empty_like(q)
     cdna4.decode(q, K, V, o, cfg, workspace=ws)
     gots = [host(o[b]) for b in checked]
     refs = [oracle.decode(*hostv[b], D, N, HQ, HK, 1)[0] for b in checked]
-    check_parity(gots, refs, torch.float16, what="cfg4 on the split-K plan, batches 1, 30")
+    name = "fp16" if dtype == torch.float16 else "bf16"
+    check_parity(gots, refs, dtype, what=f"cfg4 shape on the split-K plan, {name}, batches 1, 30")
 
 
 def test_torch_op_mirrors():
